@@ -1,0 +1,255 @@
+"""Benchmark of the key-scan hot path on one MI355X.
+
+Workload (BASELINE.json metric "scanned tokens/s/GPU (scan+top-k) at 1M ctx"):
+config 3's layer shape -- 8 KV heads, G = 4 query heads per KV head, n = 2^20
+tokens, D = 128, "56-bit" plan (budget B = 48 code bits), k = 512 with 4 sink +
+32 local -- on seeded synthetic bf16 keys.  One step = make_plan -> scan ->
+sink_local_topk -> union row gather over all 8 KV heads.
+
+`value` counts scanned token*heads per second of scan + top-k with the index
+resident in HBM (n * BH / (t_scan + t_topk)).  The same step with the plane
+index and the K/V rows in mapped pinned host memory (the scan reads over PCIe)
+is reported under "host_resident".
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-host] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
+PCIE_PEAK_GBPS = 64.0         # PCIe 5.0 x16, per direction
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--n", type=int, default=None, help="override the token count (testing only)")
+    ap.add_argument("--no-host", action="store_true", help="skip the host-resident measurement")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--stages-only", action="store_true", help="scan + top-k only (for profiling runs)")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class StageTimer:
+    """HIP events on the current stream around each stage of each step."""
+
+    def __init__(self, torch, names):
+        self.torch = torch
+        self.names = names
+        self.ms = {n: [] for n in names}
+        self.evs = []
+
+    def step(self, fns):
+        t = self.torch
+        evs = [t.cuda.Event(enable_timing=True)]
+        evs[0].record()
+        out = {}
+        for name in self.names:
+            fns[name](out)
+            e = t.cuda.Event(enable_timing=True)
+            e.record()
+            evs.append(e)
+        self.evs.append(evs)
+        return out
+
+    def collect(self):
+        for evs in self.evs:
+            for name, (a, b) in zip(self.names, zip(evs[:-1], evs[1:])):
+                self.ms[name].append(a.elapsed_time(b))
+        self.evs = []
+        return {n: statistics.mean(v) for n, v in self.ms.items()}
+
+
+def run_regime(torch, bp, off, x, store, Ksrc, Vsrc, steps, warmup, stages_only=False):
+    dev = x["q"].device
+    q, g = x["q"], x["g"]
+    n, BH, k = x["n"], x["BH"], x["k"]
+
+    def s_plan(o):
+        o["plan"] = bp.make_plan(g, x["budget"])
+
+    def s_scan(o):
+        o["scores"] = store.scan(q, o["plan"])
+
+    def s_topk(o):
+        o["idx"] = bp.sink_local_topk(o["scores"], k, x["sink"], x["local"])
+
+    def s_gather(o):
+        o["rows"] = off.gather_union(o["idx"], n, Ksrc, Vsrc, n)
+
+    names = ["plan", "scan", "topk"] + ([] if stages_only else ["gather"])
+    fns = {"plan": s_plan, "scan": s_scan, "topk": s_topk, "gather": s_gather}
+    timer = StageTimer(torch, names)
+    for _ in range(warmup):
+        timer.step(fns)
+    torch.cuda.synchronize()
+    timer.evs = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = timer.step(fns)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    stage = timer.collect()
+    plan = out["plan"]
+    scan_bytes = bp.bytes_planes(plan["t"], n)
+    uniq = int(out["rows"][2].sum().item()) if "rows" in out else 0
+    row_bytes = 2 * uniq * 128 * 2
+    return {"stage_ms": stage, "wall_ms_per_step": wall, "scan_bytes": scan_bytes, "row_bytes": row_bytes,
+            "unique_rows": uniq, "bits_per_token": scan_bytes * 8 / (n * BH),
+            "nact_mean": float(plan["nact"].float().mean().item()), "idx": out["idx"]}
+
+
+def cpu_baseline(x_cpu, reps=3):
+    """The oracle's port of the reference CPU scorer (scripts/sketch.py:110-131 planes
+    branch + exact top-k) on one KV head of the same distribution, 1 thread."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import fathom_oracle as O
+
+    K = x_cpu["K"][0].float().numpy()
+    q = x_cpu["q"][0].numpy()
+    var = x_cpu["var"][0].numpy()
+    n = K.shape[0]
+    times = []
+    with threadpool_limits(limits=1):
+        for _ in range(reps + 1):
+            t0 = time.perf_counter()
+            s, _ = O.sketch_planes_scores(q, K, var, x_cpu["budget"])
+            O.sink_local_topk(s[None], x_cpu["k"], x_cpu["sink"], x_cpu["local"])
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times[1:])
+    return {"value": n / med, "unit": "scanned tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 KV head x {n} tokens x G={q.shape[0]} of the same synthetic distribution, "
+                      f"oracle sketch-planes scorer (B={x_cpu['budget']:g}) + exact sink/local top-k, "
+                      f"median of {reps} after 1 warm-up, {med:.2f} s each"}
+
+
+def read_traffic():
+    """HBM bytes per scan launch measured by rocprofv3 --pmc (committed summary), or None."""
+    p = os.path.join(ROOT, "profiles", "scan_c3_hbm_traffic.md")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":")[1])
+    return None
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {a.gpus} is not supported in this build "
+              "(the path shards by (batch, KV head) with no exchange; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from fathom_amd import bitplane as bp
+    from fathom_amd import offload as off
+    from fathom_amd import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.perf_counter()
+    x = W.config_inputs(a.config, device=dev, n=a.n)
+    V = W.synth_values(x["BH"], x["n"], device=dev)
+    store = bp.PlaneStore(x["K"], keep_code=False)
+    torch.cuda.synchronize()
+    log(f"[bench] inputs + store built in {time.perf_counter() - t0:.1f} s: {W.CONFIGS[a.config]['name']}"
+        f" n={x['n']}")
+
+    hbm = run_regime(torch, bp, off, x, store, x["K"], V, a.steps, a.warmup, a.stages_only)
+    st = hbm["stage_ms"]
+    n, BH = x["n"], x["BH"]
+    scan_topk_ms = st["scan"] + st["topk"]
+    value = n * BH / (scan_topk_ms * 1e-3)
+    achieved = hbm["scan_bytes"] / (st["scan"] * 1e-3) / 1e9
+    log(f"[bench] HBM: stages {json.dumps({k: round(v, 4) for k, v in st.items()})} ms, "
+        f"{hbm['bits_per_token']:.2f} bits/token, scan {achieved:.1f} GB/s")
+
+    host = None
+    if not a.no_host and not a.stages_only:
+        hps = []
+        try:
+            _, pl_dev, h = off.host_mapped(store.planes_k)
+            hps.append(h)
+            _, sc_dev, h = off.host_mapped(store.scales_k)
+            hps.append(h)
+            _, K_dev, h = off.host_mapped(x["K"])
+            hps.append(h)
+            _, V_dev, h = off.host_mapped(V)
+            hps.append(h)
+            hstore = bp.PlaneStore.__new__(bp.PlaneStore)
+            hstore.BH, hstore.n, hstore.nsb, hstore.sub = store.BH, store.n, store.nsb, store.sub
+            hstore.planes32, hstore.scales_k = pl_dev, sc_dev
+            hr = run_regime(torch, bp, off, x, hstore, K_dev, V_dev, max(3, a.steps // 2), 2)
+            same = bool(torch.equal(hr["idx"], hbm["idx"]))
+            hs = hr["stage_ms"]
+            tot = sum(hs.values())
+            pcie_bytes = hr["scan_bytes"] + hr["row_bytes"]
+            # measured pinned H2D copy rate, the reference's memcpy comparison
+            src = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+            dst = torch.empty_like(src, device=dev)
+            dst.copy_(src, non_blocking=True)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(4):
+                dst.copy_(src, non_blocking=True)
+            e1.record()
+            torch.cuda.synchronize()
+            h2d = 4 * src.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9
+            host = {"stage_ms": {k: round(v, 4) for k, v in hs.items()},
+                    "scanned_tokens_per_s": n * BH / ((hs["scan"] + hs["topk"]) * 1e-3),
+                    "step_ms": tot, "pcie_bytes_per_step": pcie_bytes,
+                    "pcie_GBps_step": pcie_bytes / (tot * 1e-3) / 1e9,
+                    "scan_pcie_GBps": hr["scan_bytes"] / (hs["scan"] * 1e-3) / 1e9,
+                    "roofline_pcie": {"peak": PCIE_PEAK_GBPS, "frac_step": pcie_bytes / (tot * 1e-3) / 1e9 / PCIE_PEAK_GBPS,
+                                      "frac_scan": hr["scan_bytes"] / (hs["scan"] * 1e-3) / 1e9 / PCIE_PEAK_GBPS},
+                    "measured_h2d_memcpy_GBps": h2d, "unique_rows": hr["unique_rows"],
+                    "index_sets_equal_hbm": same}
+            log(f"[bench] host-resident: {json.dumps(host)}")
+        finally:
+            for h in hps:
+                off.free_host(h)
+
+    cpu = None
+    if not a.no_cpu:
+        xs = W.config_inputs(a.config, device="cpu", n=min(x["n"], 262144), BH=1)
+        cpu = cpu_baseline(xs)
+        log(f"[bench] cpu baseline: {json.dumps(cpu)}")
+
+    rec = {
+        "metric": "scanned tokens/s/GPU (scan+top-k) at 1M ctx",
+        "value": value, "unit": "token*heads/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": sum(st.values()), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded lognormal-scaled keys, planted keys; no model weights)",
+        "config": {"workload": W.CONFIGS[a.config]["name"] + ", index + rows in HBM", "BH": BH, "G": x["G"],
+                   "n": n, "budget_bits": x["budget"], "k": x["k"], "sink": x["sink"], "local": x["local"],
+                   "bits_per_token": round(hbm["bits_per_token"], 3), "parallelism": "single GPU"},
+        "stage_ms": {k: round(v, 4) for k, v in st.items()},
+        "scan_topk_ms": scan_topk_ms,
+        "roofline": {"bound": "hbm", "kernel": "scan_planes_kernel", "achieved": achieved, "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
+                     "algorithmic_bytes_per_launch": hbm["scan_bytes"]},
+        "host_resident": host,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,144 @@
+// Per-query reverse water-filling plan: one wave64 per (batch, KV head).
+//
+// Each lane owns CPL consecutive channels.  The 30-step bisection of the water
+// line runs in float32 exactly as kernels/bitplane.py:88-95 states it (wave sum
+// of the integer depths is exact in any order); the compacted lists are built
+// with wave prefix sums so every output array is written in full (zero padded)
+// and no separate clear is needed.
+#include "common.hpp"
+
+namespace fathom {
+namespace {
+
+// float32 log2 shared bit-for-bit with the CPU oracle: x = m 2^e with m folded
+// into (1/sqrt2, sqrt2], ln m = 2 atanh(s), s = (m-1)/(m+1), odd series to
+// z^11 (z = s^2) in Horner form, log2 x = e + ln m * log2(e), every step a
+// separate IEEE float64 operation (no contraction), rounded once to float32.
+__device__ float flog2(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  if (isinf(x)) return x;
+  const uint32_t bits = __float_as_uint(x);
+  int e = (int)((bits >> 23) & 0xFFu) - 127;
+  double m = (double)(int)((bits & 0x7FFFFFu) | 0x800000u) / 8388608.0;
+  if (m > 1.4142135623730951) {
+    m = m * 0.5;
+    e += 1;
+  }
+  const double s = (m - 1.0) / (m + 1.0);
+  const double z = s * s;
+  double p = 1.0 / 23.0;
+  p = p * z; p = p + 1.0 / 21.0;
+  p = p * z; p = p + 1.0 / 19.0;
+  p = p * z; p = p + 1.0 / 17.0;
+  p = p * z; p = p + 1.0 / 15.0;
+  p = p * z; p = p + 1.0 / 13.0;
+  p = p * z; p = p + 1.0 / 11.0;
+  p = p * z; p = p + 1.0 / 9.0;
+  p = p * z; p = p + 1.0 / 7.0;
+  p = p * z; p = p + 1.0 / 5.0;
+  p = p * z; p = p + 1.0 / 3.0;
+  p = p * z; p = p + 1.0;
+  const double ln_m = (2.0 * s) * p;
+  const double r = (double)e + ln_m * 1.4426950408889634;
+  return (float)r;
+}
+
+template <int CPL>
+__global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, const float *__restrict__ budget, int D,
+                                                  int bmax, int iters, int8_t *__restrict__ t_out,
+                                                  int32_t *__restrict__ pairs, int32_t *__restrict__ npairs,
+                                                  int32_t *__restrict__ act, int32_t *__restrict__ nact,
+                                                  int32_t *__restrict__ cls, int32_t *__restrict__ clsn) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x;
+  const int64_t bh = blockIdx.x;
+  const float bm = (float)bmax;
+  float lg[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int j = lane * CPL + k;
+    // kernels/bitplane.py:89: lg = log2(max(g, 1e-30)); NaN g takes the 1e-30 floor.
+    lg[k] = (j < D) ? flog2(fmaxf(g[bh * D + j], 1e-30f)) : -INFINITY;
+  }
+  const float Br = budget[bh];
+  float lo = -60.0f, hi = 60.0f;
+  for (int it = 0; it < iters; ++it) {
+    const float mid = (lo + hi) * 0.5f;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) s += fminf(fmaxf(rintf((lg[k] - mid) * 0.5f), 0.0f), bm);
+    const float tot = wave_sum_f(s);
+    if (tot > Br) lo = mid; else hi = mid;
+  }
+  int t[CPL];
+  int cnt_act = 0, cnt_pairs = 0;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int j = lane * CPL + k;
+    t[k] = (j < D) ? (int)fminf(fmaxf(rintf((lg[k] - hi) * 0.5f), 0.0f), bm) : 0;
+    if (j < D) t_out[bh * D + j] = (int8_t)t[k];
+    cnt_act += t[k] > 0;
+    cnt_pairs += t[k];
+  }
+  // active channels, ascending
+  {
+    int pos = wave_excl_scan_i(cnt_act, lane);
+    const int total = wave_sum_i(cnt_act);
+#pragma unroll
+    for (int k = 0; k < CPL; ++k)
+      if (t[k] > 0) act[bh * D + pos++] = lane * CPL + k;
+    for (int i = total + lane; i < D; i += kWave) act[bh * D + i] = 0;
+    if (lane == 0) nact[bh] = total;
+  }
+  // (channel, plane) pairs: channel-major, plane ascending
+  {
+    int pos = wave_excl_scan_i(cnt_pairs, lane);
+    const int total = wave_sum_i(cnt_pairs);
+    const int64_t base = bh * (int64_t)D * bmax;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k)
+      for (int p = 0; p < t[k]; ++p) pairs[base + pos++] = (lane * CPL + k) * bmax + p;
+    for (int i = total + lane; i < D * bmax; i += kWave) pairs[base + i] = 0;
+    if (lane == 0) npairs[bh] = total;
+  }
+  // per-depth channel lists
+  for (int c = 1; c <= bmax; ++c) {
+    int cnt = 0;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) cnt += t[k] == c;
+    int pos = wave_excl_scan_i(cnt, lane);
+    const int total = wave_sum_i(cnt);
+    const int64_t base = (bh * bmax + (c - 1)) * (int64_t)D;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k)
+      if (t[k] == c) cls[base + pos++] = lane * CPL + k;
+    for (int i = total + lane; i < D; i += kWave) cls[base + i] = 0;
+    if (lane == 0) clsn[bh * bmax + (c - 1)] = total;
+  }
+}
+
+}  // namespace
+}  // namespace fathom
+
+using namespace fathom;
+
+extern "C" int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D, int bmax, int iters,
+                                int8_t *t, int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls,
+                                int32_t *clsn, void *stream) {
+  if (!g || !budget || !t || !pairs || !npairs || !act || !nact || !cls || !clsn)
+    return fail(FATHOM_ERR_INVALID, "make_plan: null pointer");
+  if (BH < 1 || BH > 0x7FFFFFFF) return fail(FATHOM_ERR_INVALID, "make_plan: BH=%lld unsupported", (long long)BH);
+  if (D < 1 || D > 256) return fail(FATHOM_ERR_INVALID, "make_plan: D=%lld outside [1, 256]", (long long)D);
+  if (bmax < 1 || bmax > 8) return fail(FATHOM_ERR_INVALID, "make_plan: bmax=%d outside [1, 8]", bmax);
+  if (iters < 0 || iters > 200) return fail(FATHOM_ERR_INVALID, "make_plan: iters=%d outside [0, 200]", iters);
+  hipStream_t st = (hipStream_t)stream;
+  const int d = (int)D;
+  if (D <= 64)
+    plan_kernel<1><<<(unsigned)BH, 64, 0, st>>>(g, budget, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
+  else if (D <= 128)
+    plan_kernel<2><<<(unsigned)BH, 64, 0, st>>>(g, budget, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
+  else
+    plan_kernel<4><<<(unsigned)BH, 64, 0, st>>>(g, budget, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
+  return launch_status("plan_kernel");
+}

@@ -1,0 +1,167 @@
+/*
+ * fathom_hip.h -- C ABI of the MI355X (gfx950) bit-plane key-scan library.
+ *
+ * The reference exposes this path as the Python module kernels/bitplane.py
+ * (imported as `from bitplane import *`, scripts/B_e2e_offload_v2.py:12-17,
+ * scripts/B_kernel_bench.py:8-12) plus the gather kernels and ctypes host
+ * mapping of scripts/B_e2e_offload_v2.py.  Each entry point below replaces one
+ * of those; the replaced reference interface is cited above it.
+ *
+ * Conventions (all entry points):
+ *   - every pointer is device-visible: HBM, or pinned host memory mapped into
+ *     the GPU address space (fathom_host_alloc_mapped); the caller owns every
+ *     buffer, including workspaces;
+ *   - tensors are dense, row-major (C order), with the shapes documented;
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t, NULL = the
+ *     default stream); no entry point synchronises the host;
+ *   - the return value is a status: FATHOM_OK (0) or an error code; the text
+ *     of the last error on the calling thread is fathom_last_error();
+ *   - no state is kept between calls: entry points are thread-safe as long as
+ *     concurrent calls do not share output or workspace buffers.
+ */
+#ifndef FATHOM_HIP_H
+#define FATHOM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define FATHOM_OK 0
+#define FATHOM_ERR_INVALID 1   /* shape or argument rejected before any launch */
+#define FATHOM_ERR_HIP 2       /* HIP runtime error (launch, copy, query) */
+#define FATHOM_ERR_ALLOC 3     /* host allocation failed */
+#define FATHOM_ERR_WORKSPACE 4 /* workspace missing or too small */
+
+/* element types of key and scale tensors */
+#define FATHOM_DT_F32 0
+#define FATHOM_DT_F16 1
+#define FATHOM_DT_BF16 2
+
+/* Library version string and last error text (per calling thread). */
+const char *fathom_version(void);
+const char *fathom_last_error(void);
+
+/*
+ * Quantise keys to 4-bit codes and pack them as bit planes, in one pass.
+ * Replaces quantise_u4 + pack_planes + to_superblocks as PlaneStore.__init__
+ * chains them (kernels/bitplane.py:23-32, 44-50, 60-65, 312-316).
+ *   K           [lead, n, D] of k_dtype (FATHOM_DT_*)
+ *   scale_dtype FATHOM_DT_* the block absmax is rounded to (reference default f16)
+ *   outputs (each may be NULL to skip it):
+ *   code        [lead, n, D] uint8 in [0, 16)
+ *   scales_blk  [lead, nblk, D] of scale_dtype (nblk = ceil(n / 64))
+ *   planes_log  [lead, nblk, D, 4] uint64 (bit i = token 64b+i, plane 0 = MSB)
+ *   planes_sb   [lead, nsb, D, 4, sub] uint64, nsb = ceil(nblk / sub), zero padded
+ *   scales_sb   [lead, nsb, D, sub] fp16 bits; required iff planes_sb != NULL
+ */
+int fathom_quantise_pack(const void *K, int k_dtype, int64_t lead, int64_t n, int64_t D, int scale_dtype,
+                         int64_t sub, uint8_t *code, void *scales_blk, uint64_t *planes_log, uint64_t *planes_sb,
+                         uint16_t *scales_sb, void *stream);
+
+/* pack_planes (kernels/bitplane.py:44-50): code [lead, n, D] uint8 -> planes [lead, nblk, D, 4]. */
+int fathom_pack_planes(const uint8_t *code, int64_t lead, int64_t n, int64_t D, uint64_t *planes, void *stream);
+
+/* unpack_planes (kernels/bitplane.py:52-58): planes [lead, nblk, D, 4] -> code [lead, n, D] uint8. */
+int fathom_unpack_planes(const uint64_t *planes, int64_t lead, int64_t nblk, int64_t D, int64_t n, uint8_t *code,
+                         void *stream);
+
+/*
+ * to_superblocks (kernels/bitplane.py:60-65): logical planes [lead, nblk, D, 4] and
+ * scales [lead, nblk, D] (elements of scale_bytes = 2 or 4 bytes) -> planes_sb
+ * [lead, nsb, D, 4, sub] and scales_sb [lead, nsb, D, sub], zero padded.
+ */
+int fathom_to_superblocks(const uint64_t *planes, const void *scales, int scale_bytes, int64_t lead, int64_t nblk,
+                          int64_t D, int64_t sub, uint64_t *planes_sb, void *scales_sb, void *stream);
+
+/*
+ * dequant_planes (kernels/bitplane.py:34-42): value of the top t[j] planes,
+ * out [lead, n, D] float32 from code [lead, n, D], scales [lead, nblk, D] of
+ * scale_dtype and t [D] int32 (device).
+ */
+int fathom_dequant_planes(const uint8_t *code, const void *scales, int scale_dtype, const int32_t *t, int64_t lead,
+                          int64_t n, int64_t D, float *out, void *stream);
+
+/*
+ * make_plan (kernels/bitplane.py:83-116, plan_kernel + make_plan): per
+ * (batch, KV head) reverse water-filling.  g [BH, D] float32 gains, budget [BH]
+ * float32 (code bits).  Outputs, all fully written (zero padded):
+ *   t [BH, D] int8; pairs [BH, D*bmax] int32 (channel*bmax + plane);
+ *   npairs [BH]; act [BH, D]; nact [BH]; cls [BH, bmax, D]; clsn [BH, bmax].
+ * 1 <= bmax <= 8, D <= 256.
+ */
+int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D, int bmax, int iters, int8_t *t,
+                     int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls, int32_t *clsn,
+                     void *stream);
+
+/*
+ * PlaneStore.scan (kernels/bitplane.py:319-338, scan_planes_cls_kernel :275-307):
+ * out[bh, g, tok] = sum_j q[bh, g, j] * value_{t_j}(tok, j) for the 64-token
+ * blocks [blk0, blk1) (tokens < n); other tokens of `out` are not written.
+ *   q         [BH, G, D] float32, 1 <= G <= 8, D <= 256
+ *   t, act, nact  from fathom_make_plan (bmax <= 4)
+ *   planes_sb [BH, nsb, D, 4, sub] uint64, scales_sb [BH, nsb, D, sub] fp16
+ *             (HBM, or mapped pinned host memory: the scan then reads over PCIe)
+ *   out       [BH, G, n] float32
+ */
+int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t, const int32_t *act,
+                       const int32_t *nact, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb,
+                       int64_t sub, int64_t blk0, int64_t blk1, float *out, void *stream);
+
+/*
+ * sink_local_topk (kernels/bitplane.py:372-378; inline form with the current
+ * length m at scripts/B_e2e_offload_v2.py:224-227).  For each of `rows` rows of
+ * scores [rows, n] float32: mask [0, sink) and [max(m - local, 0), n) to -inf,
+ * select the top kk = k - sink - local by (score descending, index ascending;
+ * NaN above +inf, -0.0 == +0.0), then append 0..sink-1 and m-local..m-1.
+ *   idx [rows, k] int64.  Requires 0 <= kk <= n, sink <= n, local <= m, n <= m.
+ * workspace: fathom_topk_workspace_bytes(rows, n, k) bytes of device memory,
+ * contents arbitrary on entry.
+ */
+size_t fathom_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
+int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink,
+                           int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * gather_rows (scripts/B_e2e_offload_v2.py:73-83, gather_rows_kernel):
+ * dst[bh, r, :] = src[bh, idx[bh, r], :] for idx >= 0, zero row for idx < 0.
+ *   src [BH, cap, row_bytes] (HBM or mapped host), idx [BH, R] int32,
+ *   dst [BH, R, row_bytes]; row_bytes % 4 == 0.
+ */
+int fathom_gather_rows(const void *src, int64_t cap, const int32_t *idx, int64_t BH, int64_t R, int64_t row_bytes,
+                       void *dst, void *stream);
+
+/*
+ * Group-union row gather (scripts/B_e2e_offload_v2.py:228-241): for idx
+ * [BH, GK] int64 (GK = G*k <= 16384), fetch every distinct token < n of a row
+ * once from Ksrc/Vsrc [BH, cap, row_bytes] (usually mapped host memory), tokens
+ * >= n from the device buffers Krec/Vrec [BH, nrec, row_bytes] at row
+ * clamp(idx - n, 0, nrec - 1), negative tokens as zero rows, and write
+ * Kout/Vout [BH, GK, row_bytes] in the order of idx.  n_unique [BH] int32
+ * (may be NULL) receives the number of distinct host rows fetched.
+ * workspace: fathom_gather_union_workspace_bytes(BH, GK) bytes.
+ */
+size_t fathom_gather_union_workspace_bytes(int64_t BH, int64_t GK);
+int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t n, const void *Ksrc, const void *Vsrc,
+                        int64_t cap, const void *Krec, const void *Vrec, int64_t nrec, int64_t row_bytes, void *Kout,
+                        void *Vout, int32_t *n_unique, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Pinned, GPU-mapped host memory (scripts/B_e2e_offload_v2.py:33-39,
+ * host_mapped / free_host through cudaHostAlloc(flags=3) and
+ * cudaHostGetDevicePointer).  coherent != 0 asks for fine-grained (coherent)
+ * memory, 0 for non-coherent.  *dev_ptr is the address kernels use.
+ */
+int fathom_host_alloc_mapped(size_t bytes, int coherent, void **host_ptr, void **dev_ptr);
+int fathom_host_free(void *host_ptr);
+
+/* Asynchronous copy between any two device-visible or host buffers (hipMemcpyAsync, kind default). */
+int fathom_memcpy(void *dst, const void *src, size_t bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FATHOM_HIP_H */

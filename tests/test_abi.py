@@ -1,0 +1,53 @@
+"""CPU checks of the C ABI boundary: the built library loads, exports every
+entry point include/fathom_hip.h declares, and the Python binding declares a
+prototype for each; the Python API refuses host tensors (no CPU fallback)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from fathom_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fathom_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fathom_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "fathom_scan_planes" in names and "fathom_sink_local_topk" in names
+    assert len(names) == len(_lib.PROTOTYPES)
+    assert set(names) == set(_lib.PROTOTYPES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert _lib.lib().fathom_version().decode().startswith("fathom-hip")
+
+
+def test_workspace_queries_and_argument_errors_without_gpu():
+    L = _lib.lib()
+    assert L.fathom_topk_workspace_bytes(32, 1 << 20, 512) >= 32 * (1 << 20) * 8
+    assert L.fathom_gather_union_workspace_bytes(8, 2048) == 8 * 2048 * 8
+    # argument validation happens before any HIP call
+    rc = L.fathom_make_plan(None, None, 1, 128, 4, 30, None, None, None, None, None, None, None, None)
+    assert rc == _lib.ERR_INVALID and b"null" in L.fathom_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(rc, "fathom_make_plan")
+
+
+def test_python_api_rejects_host_tensors():
+    from fathom_amd import bitplane as bp
+    with pytest.raises(ValueError, match="GPU"):
+        bp.quantise_u4(torch.zeros(2, 64, 128))
+    with pytest.raises(ValueError, match="GPU"):
+        bp.make_plan(torch.ones(2, 128), 48)

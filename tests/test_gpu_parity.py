@@ -1,0 +1,330 @@
+"""GPU parity tests: the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Bit-exact: codes, scales, plane words (logical and superblock order), plans,
+top-k index sets given the same scores, gathered rows.  Scores: within 1e-3
+relative of the float64 oracle, with an absolute floor of 1e-4 x the row's
+largest |score| (summation-order noise near zero crossings).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from fathom_amd import bitplane as bp
+from fathom_amd import offload as off
+from fathom_amd import workloads as W
+from oracle import fathom_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+SDT = {"f16": torch.float16, "f32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _u64(t):
+    return t.cpu().numpy().view(np.uint64)
+
+
+def _scores_close(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    floor = 1e-4 * np.abs(ref).max(-1, keepdims=True)
+    err = np.abs(got - ref)
+    bad = err > 1e-3 * np.abs(ref) + floor
+    assert not bad.any(), f"{int(bad.sum())} scores off; max err {err.max():.3e}"
+
+
+def _keys(BH, n, d=128, seed=0, dtype=torch.float32, edge=True):
+    g = torch.Generator().manual_seed(seed)
+    sigma = torch.exp(torch.randn(BH, d, generator=g))
+    K = torch.randn(BH, n, d, generator=g) * sigma[:, None, :]
+    if edge:
+        K[0, :64, 0] = 0.0                       # all-zero block: 0/0 codes
+        K[0, :, 1] = 1e-9                        # fp16 absmax underflow
+        K[0, 70, 2] = float("nan")               # NaN poisons a block
+        if BH > 1:
+            K[1, :, 3] = 7.0e4                   # fp16 absmax overflow
+        K[0, 100:164, 5] = torch.linspace(-2, 2, 64)
+    return K.to(dtype)
+
+
+# ----------------------------------------------------------------------------- store build
+@pytest.mark.parametrize("kdtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("sdt", ["f16", "f32", "bf16"])
+@pytest.mark.parametrize("n", [64, 1000, 4097])
+def test_quantise_and_pack_bitexact(kdtype, sdt, n):
+    print(f"[quantise] kdtype={kdtype} sdt={sdt} n={n}", flush=True)
+    K = _keys(2, n, dtype=kdtype, edge=kdtype != torch.float16)
+    code_r, sc_r = O.quantise_u4(K.float().numpy(), sdt)
+    code, sc = bp.quantise_u4(K.to(DEV), SDT[sdt])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(code.cpu().numpy(), code_r)
+    np.testing.assert_array_equal(sc.float().cpu().numpy(), sc_r)
+    planes = bp.pack_planes(code)
+    np.testing.assert_array_equal(_u64(planes), O.pack_planes(code_r))
+    np.testing.assert_array_equal(bp.unpack_planes(planes, n).cpu().numpy(), code_r)
+
+
+@pytest.mark.parametrize("sub", [16, 1, 3, "whole"])
+@pytest.mark.parametrize("n", [1000, 70001])
+def test_planestore_superblocks_bitexact(sub, n, monkeypatch):
+    print(f"[planestore] sub={sub} n={n}", flush=True)
+    nb = math.ceil(n / 64)
+    s = nb if sub == "whole" else sub
+    monkeypatch.setattr(bp, "SUB", s)
+    K = _keys(3, n, seed=1, dtype=torch.bfloat16)
+    st = bp.PlaneStore(K.to(DEV))
+    code_r, sc_r = O.quantise_u4(K.float().numpy())
+    pl_r, scs_r = O.to_superblocks(O.pack_planes(code_r), sc_r.astype(np.float16), s)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(st.code.cpu().numpy(), code_r)
+    np.testing.assert_array_equal(_u64(st.planes_k), pl_r)
+    np.testing.assert_array_equal(st.scales_k.cpu().numpy(), scs_r)
+    # the standalone permutation gives the same store
+    pl2, sc2 = bp.to_superblocks(bp.pack_planes(st.code), st.scales_blk)
+    np.testing.assert_array_equal(_u64(pl2), pl_r)
+    np.testing.assert_array_equal(sc2.cpu().numpy(), scs_r)
+
+
+def test_dequant_bitexact():
+    K = _keys(2, 777, seed=2, edge=False)
+    code_r, sc_r = O.quantise_u4(K.numpy())
+    code, sc = bp.quantise_u4(K.to(DEV))
+    for tv in [0, 1, 3, 4, np.arange(128) % 5]:
+        t = torch.as_tensor(tv)
+        got = bp.dequant_planes(code[1], sc[1], t).cpu().numpy()
+        np.testing.assert_array_equal(got, O.dequant_planes(code_r[1], sc_r[1], np.asarray(tv)))
+
+
+# ----------------------------------------------------------------------------- plan
+@pytest.mark.parametrize("d", [128, 64, 100, 256])
+@pytest.mark.parametrize("bmax", [4, 1, 2, 8])
+def test_make_plan_bitexact(d, bmax):
+    print(f"[plan] d={d} bmax={bmax}", flush=True)
+    rng = np.random.default_rng(d * 10 + bmax)
+    BH = 37
+    g = (np.exp(rng.standard_normal((BH, d)) * 3) * rng.random((BH, d))).astype(np.float32)
+    g[0, :5] = 0
+    g[1, :] = 0
+    g[2, 3] = np.nan
+    g[3, :] = 1.0                                    # all tied
+    budget = rng.integers(0, d * bmax + 20, BH).astype(np.float32)
+    ref = O.make_plan(g, budget, bmax=bmax)
+    got = bp.make_plan(torch.from_numpy(g).to(DEV), torch.from_numpy(budget).to(DEV), bmax=bmax)
+    for key in ("t", "pairs", "npairs", "act", "nact", "cls", "clsn"):
+        np.testing.assert_array_equal(got[key].cpu().numpy(), ref[key], err_msg=key)
+
+
+def test_make_plan_scalar_budget_and_iters():
+    rng = np.random.default_rng(9)
+    g = np.exp(rng.standard_normal((8, 128)) * 2).astype(np.float32)
+    for it in (30, 10, 0):
+        ref = O.make_plan(g, 48.0, iters=it)
+        got = bp.make_plan(torch.from_numpy(g).to(DEV), 48.0, iters=it)
+        np.testing.assert_array_equal(got["t"].cpu().numpy(), ref["t"])
+
+
+def test_make_plan_worked_example():
+    K = np.array([[1.8, 0.4, -0.2, 0.05], [-1.1, 0.9, 0.3, -0.02], [0.3, -1.2, 0.1, 0.04],
+                  [1.2, 0.7, 0.4, 0.01], [-0.6, -0.3, -0.5, 0.03], [0.9, 1.1, -0.3, -0.05]], np.float32)
+    g = (np.float32([3, 1, 2, 0.1]) ** 2 + np.float32([1, 2, -1, 0.2]) ** 2) * K.var(0, ddof=1)
+    for B, t in ((8, [4, 3, 1, 0]), (6, [3, 2, 1, 0])):
+        got = bp.make_plan(torch.from_numpy(g[None]).to(DEV), float(B))
+        assert got["t"][0].tolist() == t
+
+
+# ----------------------------------------------------------------------------- scan
+def _scan_case(cfg, n, BH, sub=None, seed=0, budget=None):
+    x = W.config_inputs(cfg, seed=seed, n=n, BH=BH)
+    if sub is not None:
+        bp.SUB = sub
+    try:
+        st = bp.PlaneStore(x["K"].to(DEV))
+    finally:
+        bp.SUB = 16
+    plan = bp.make_plan(x["g"].to(DEV), budget if budget is not None else x["budget"])
+    return x, st, plan
+
+
+@pytest.mark.parametrize("cfg,n,BH,sub", [(1, 16384, None, None), (2, 16421, 2, None), (2, 8192, 2, 128),
+                                          (4, 8192, 2, None), (3, 20000, 1, 7)])
+def test_scan_matches_oracle(cfg, n, BH, sub):
+    print(f"[scan] cfg={cfg} n={n} BH={BH} sub={sub}", flush=True)
+    x, st, plan = _scan_case(cfg, n, BH, sub)
+    scores = st.scan(x["q"].to(DEV), plan).cpu().numpy()
+    t = plan["t"].cpu().numpy()
+    code_r, sc_r = O.quantise_u4(x["K"].float().numpy())
+    ref = O.scan_planes(x["q"].numpy(), code_r, sc_r.astype(np.float16).astype(np.float32), t)
+    _scores_close(scores, ref)
+
+
+@pytest.mark.parametrize("budget", [40.0, 48.0, 80.0, 0.0, 512.0])
+def test_scan_budgets_c4_shape(budget):
+    x, st, plan = _scan_case(4, 4096, 2, budget=budget)
+    scores = st.scan(x["q"].to(DEV), plan).cpu().numpy()
+    code_r, sc_r = O.quantise_u4(x["K"].float().numpy())
+    ref = O.scan_planes(x["q"].numpy(), code_r, sc_r, plan["t"].cpu().numpy())
+    _scores_close(scores, ref)
+
+
+def test_scan_block_range_writes_only_its_tokens():
+    x, st, plan = _scan_case(2, 9000, 2)
+    q = x["q"].to(DEV)
+    full = st.scan(q, plan)
+    out = torch.full_like(full, 12345.0)
+    st.scan(q, plan, out=out, blocks=(3, 40))
+    lo, hi = 3 * 64, min(40 * 64, 9000)
+    torch.testing.assert_close(out[..., lo:hi], full[..., lo:hi], rtol=0, atol=0)
+    assert (out[..., :lo] == 12345.0).all() and (out[..., hi:] == 12345.0).all()
+
+
+def test_scan_host_resident_equals_hbm():
+    """Same kernel reading the store zero-copy from mapped pinned host memory."""
+    x, st, plan = _scan_case(2, 33000, 2)
+    q = x["q"].to(DEV)
+    ref = st.scan(q, plan).clone()
+    _, pl_dev, hp1 = off.host_mapped(st.planes_k)
+    _, sc_dev, hp2 = off.host_mapped(st.scales_k)
+    try:
+        st.planes32, st.scales_k = pl_dev, sc_dev
+        got = st.scan(q, plan)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    finally:
+        off.free_host(hp1)
+        off.free_host(hp2)
+
+
+# ----------------------------------------------------------------------------- top-k
+def _topk_case(rows, k, sink, local, m=None):
+    got = bp.sink_local_topk(torch.from_numpy(rows).to(DEV), k, sink, local, m=m).cpu().numpy()
+    ref = O.sink_local_topk(rows, k, sink, local, m=m)
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("n,k,sink,local", [(1000, 128, 4, 64), (16384, 128, 4, 64), (131072, 512, 4, 32),
+                                            (100000, 2048, 4, 32), (3000, 2048, 4, 32), (600, 40, 0, 0)])
+def test_topk_random_bitexact(n, k, sink, local):
+    print(f"[topk] n={n} k={k}", flush=True)
+    rng = np.random.default_rng(n + k)
+    rows = rng.standard_normal((2, 3, n)).astype(np.float32)
+    _topk_case(rows, k, sink, local)
+
+
+def test_topk_ties_nan_inf_negzero():
+    rng = np.random.default_rng(1)
+    n = 5000
+    rows = rng.integers(-3, 4, size=(4, n)).astype(np.float32)     # huge tie groups
+    rows[0, rng.integers(0, n, 20)] = np.nan
+    rows[1, rng.integers(0, n, 20)] = -np.inf
+    rows[1, rng.integers(0, n, 20)] = np.inf
+    rows[2, rng.integers(0, n, 300)] = -0.0
+    rows[3] = 0.0
+    _topk_case(rows, 512, 4, 32)
+    _topk_case(rows, 100, 3, 5, m=n + 2)
+
+
+def test_topk_huge_tie_bucket_slow_path():
+    """All scores inside one first-level bucket (> 8192 candidates)."""
+    rng = np.random.default_rng(2)
+    n = 200000
+    rows = (1.0 + rng.integers(0, 50, size=(2, n)) * 1e-7).astype(np.float32)
+    _topk_case(rows, 512, 4, 32)
+    _topk_case(np.ones((1, 70000), np.float32), 300, 4, 32)
+
+
+def test_topk_config3_rows():
+    print("[topk] 32 x 1M", flush=True)
+    rng = np.random.default_rng(3)
+    rows = rng.standard_normal((8, 4, 1 << 20)).astype(np.float32)
+    _topk_case(rows, 512, 4, 32)
+
+
+# ----------------------------------------------------------------------------- gathers
+def test_gather_rows_matches_oracle():
+    rng = np.random.default_rng(4)
+    BH, cap, R = 3, 5000, 700
+    src = torch.randn(BH, cap, 128).to(torch.bfloat16)
+    idx = rng.integers(-2, cap + 3, size=(BH, R)).astype(np.int32)
+    got = off.gather_rows(src.to(DEV), cap, torch.from_numpy(idx).to(DEV), BH)
+    ref = O.gather_rows(src.view(torch.int16).numpy(), idx)
+    np.testing.assert_array_equal(got.cpu().view(torch.int16).numpy(), ref)
+
+
+@pytest.mark.parametrize("host", [False, True])
+def test_gather_union_matches_oracle(host):
+    rng = np.random.default_rng(5)
+    BH, n, G, k, nrec = 4, 20000, 7, 2048, 6
+    K = torch.randn(BH, n, 128).to(torch.bfloat16)
+    V = torch.randn(BH, n, 128).to(torch.bfloat16)
+    Kr = torch.randn(BH, nrec, 128).to(torch.bfloat16)
+    Vr = torch.randn(BH, nrec, 128).to(torch.bfloat16)
+    idx = rng.integers(0, 3000, size=(BH, G, k))                   # heavy overlap across heads
+    idx[:, :, -3:] = n + rng.integers(0, nrec + 2, size=(BH, G, 3))
+    idx[0, 0, 0] = -4
+    hps = []
+    try:
+        if host:
+            _, Ksrc, h1 = off.host_mapped(K)
+            _, Vsrc, h2 = off.host_mapped(V)
+            hps = [h1, h2]
+        else:
+            Ksrc, Vsrc = K.to(DEV), V.to(DEV)
+        Ks, Vs, nu = off.gather_union(torch.from_numpy(idx).to(DEV), n, Ksrc, Vsrc, n, Kr.to(DEV), Vr.to(DEV))
+        torch.cuda.synchronize()
+        rK, rV, rnu = O.gather_union(idx, n, K.view(torch.int16).numpy(), V.view(torch.int16).numpy(),
+                                     Kr.view(torch.int16).numpy(), Vr.view(torch.int16).numpy())
+        np.testing.assert_array_equal(Ks.cpu().view(torch.int16).numpy(), rK)
+        np.testing.assert_array_equal(Vs.cpu().view(torch.int16).numpy(), rV)
+        np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
+    finally:
+        for h in hps:
+            off.free_host(h)
+
+
+# ----------------------------------------------------------------------------- end to end
+def test_config1_pipeline_matches_oracle():
+    """Config 1 end to end: store, plan, scan, sink/local top-k on the GPU vs the oracle."""
+    x = W.config_inputs(1)
+    st = bp.PlaneStore(x["K"].to(DEV))
+    plan = bp.make_plan(x["g"].to(DEV), x["budget"])
+    scores = st.scan(x["q"].to(DEV), plan)
+    idx = bp.sink_local_topk(scores, x["k"], x["sink"], x["local"]).cpu().numpy()
+    code_r, sc_r = O.quantise_u4(x["K"].numpy())
+    pr = O.make_plan(x["g"].numpy(), x["budget"])
+    np.testing.assert_array_equal(plan["t"].cpu().numpy(), pr["t"])
+    ref_s = O.scan_planes(x["q"].numpy(), code_r, sc_r, pr["t"])
+    _scores_close(scores.cpu().numpy(), ref_s)
+    # same scores -> same index set, bit for bit
+    np.testing.assert_array_equal(idx, O.sink_local_topk(scores.cpu().numpy(), x["k"], x["sink"], x["local"]))
+    # against the float64 oracle scores, any difference must sit at the selection boundary
+    ref_idx = O.sink_local_topk(ref_s.astype(np.float32), x["k"], x["sink"], x["local"])
+    diff = set(idx[0, 0].tolist()) ^ set(ref_idx[0, 0].tolist())
+    if diff:
+        s = ref_s[0, 0]
+        kth = np.sort(s[x["sink"]:x["n"] - x["local"]])[::-1][x["k"] - x["sink"] - x["local"] - 1]
+        assert all(abs(s[i] - kth) <= 1e-4 * np.abs(s).max() for i in diff)
+    planted = set(x["planted"][0].tolist())
+    assert len(planted & set(idx[0, 0].tolist())) >= 4
+
+
+def test_config2_full_size_invariants():
+    """Config 2 at its full size: store round trip, plan parity, scores vs a float32
+    torch reference from the dequantised keys, top-k parity given the scores."""
+    print("[c2] full size", flush=True)
+    x = W.config_inputs(2, device=DEV)
+    st = bp.PlaneStore(x["K"])
+    n = x["n"]
+    nb = math.ceil(n / 64)
+    logical = st.planes_k.permute(0, 1, 4, 2, 3).reshape(x["BH"], -1, 128, 4)[:, :nb]
+    assert torch.equal(bp.unpack_planes(logical, n), st.code)
+    plan = bp.make_plan(x["g"], x["budget"])
+    pr = O.make_plan(x["g"].cpu().numpy(), x["budget"])
+    np.testing.assert_array_equal(plan["t"].cpu().numpy(), pr["t"])
+    scores = st.scan(x["q"], plan)
+    ref = bp.scan_planes_reference(x["q"], st.code, st.scales_blk, plan["t"])
+    err = (scores - ref).abs()
+    tol = 1e-3 * ref.abs() + 1e-4 * ref.abs().amax(-1, keepdim=True)
+    assert bool((err <= tol).all()), float(err.max())
+    idx = bp.sink_local_topk(scores, x["k"])
+    np.testing.assert_array_equal(idx.cpu().numpy(), O.sink_local_topk(scores.cpu().numpy(), x["k"]))

@@ -1,0 +1,321 @@
+"""CPU checks that pin the numpy oracle (no GPU).
+
+Each check compares the oracle with something independent of its own
+formulas: the paper's worked example, a different quantiser formula (the
+sketch quantiser), pure-Python bit loops, the greedy water-filling algorithm,
+float64 log2, a per-bit scan formulation, or a brute-force sort.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import fathom_oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _worked():
+    with open(os.path.join(GOLD, "worked_example.json")) as f:
+        return json.load(f)
+
+
+# ----------------------------------------------------------------------------- worked example (paper App. A)
+def test_worked_example_variance_and_gain():
+    w = _worked()
+    K = np.array(w["keys"], np.float32)
+    var = K.var(0, ddof=1)
+    np.testing.assert_allclose(var, w["var_3dp"], atol=6e-4)
+    qa, qb = np.array(w["q_head_A"], np.float32), np.array(w["q_head_B"], np.float32)
+    g = (qa ** 2 + qb ** 2) * var
+    np.testing.assert_allclose(g, w["g_2dp"], atol=6e-3)
+
+
+@pytest.mark.parametrize("budget", [8, 6])
+def test_worked_example_plan(budget):
+    w = _worked()
+    K = np.array(w["keys"], np.float32)
+    var = K.var(0, ddof=1)
+    g = (np.array(w["q_head_A"], np.float32) ** 2 + np.array(w["q_head_B"], np.float32) ** 2) * var
+    p = O.make_plan(g[None], budget)
+    exp = w["plan"][str(budget)]
+    assert p["t"][0].tolist() == exp["t"]
+    theta = 2.0 ** float(p["hi"][0])          # t = round(log4(g / theta)) with log2(theta) = hi
+    assert exp["theta_lo"] < theta <= exp["theta_hi"]
+    assert round(theta, 3) == exp["theta_printed"]
+
+
+def test_worked_example_codes_and_one_plane():
+    w = _worked()
+    K = np.array(w["keys"], np.float32)
+    code, sc = O.quantise_u4(K)
+    assert sc[0, 2] == np.float32(w["channel2_amax"])
+    assert code[:, 2].tolist() == w["channel2_codes"]
+    one = O.dequant_planes(code, sc, np.array([0, 0, 1, 0]))[:, 2]
+    np.testing.assert_array_equal(one, np.array(w["channel2_one_plane_values"], np.float32))
+
+
+def test_worked_example_scores():
+    w = _worked()
+    K = np.array(w["keys"], np.float32)
+    q = np.stack([np.array(w["q_head_A"], np.float32), np.array(w["q_head_B"], np.float32)])
+    code, sc = O.quantise_u4(K)
+    t = np.array(w["plan"]["8"]["t"])
+    s = O.scan_planes(q[None], code[None], sc[None], t[None])[0]
+    np.testing.assert_allclose(s[0], w["scores_B8_head_A_2dp"], atol=5.1e-3)
+    np.testing.assert_allclose(s[1], w["scores_B8_head_B_2dp"], atol=5.1e-3)
+    np.testing.assert_allclose(q @ K.T, [w["exact_head_A_2dp"], w["exact_head_B_2dp"]], atol=5.1e-3)
+    top2 = [list(np.argsort(-row, kind="stable")[:2]) for row in s]
+    assert top2 == [w["top2_head_A"], w["top2_head_B"]]
+
+
+# ----------------------------------------------------------------------------- quantiser: prefix theorem
+def _qblock_given_amax(x, amax, t):
+    """scripts/sketch.py:8-17 t-bit mid-rise quantiser, absmax supplied per (block, channel)."""
+    n, d = x.shape
+    nb = -(-n // 64)
+    xb = np.concatenate([x, np.zeros((nb * 64 - n, d), np.float32)]).reshape(nb, 64, d)
+    half = np.float32(2.0 ** (t - 1))
+    s = amax[:, None, :] / half
+    out = (np.clip(np.floor(xb / s), -half, half - 1) + np.float32(0.5)) * s
+    return out.reshape(-1, d)[:n]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_prefix_theorem(seed):
+    """Depth-t dequantisation of the 4-bit store == the t-bit sketch quantiser with
+    the same fp16 absmax, bit for bit, for every t (paper Sec. 3 claim)."""
+    rng = np.random.default_rng(seed)
+    n, d = 200, 16
+    x = (rng.standard_normal((n, d)) * np.exp(rng.standard_normal(d))).astype(np.float32)
+    # put some values exactly on cell edges of the fp16 absmax grid
+    code, sc = O.quantise_u4(x)
+    for blk in range(sc.shape[0]):
+        for j in range(0, d, 3):
+            x[blk * 64 + 5, j] = sc[blk, j] / 8 * 3 if blk * 64 + 5 < n else 0
+            x[min(blk * 64 + 7, n - 1), j] = -sc[blk, j] / 4
+    code, sc = O.quantise_u4(x)
+    for t in range(1, 5):
+        got = O.dequant_planes(code, sc, t)
+        ref = _qblock_given_amax(x, sc, t)
+        np.testing.assert_array_equal(got, ref)
+
+
+def test_quantise_edge_values():
+    x = np.zeros((130, 4), np.float32)
+    x[:, 0] = 1e-9                         # amax -> fp16(1e-8) = 0: x / 0 = +inf -> code 15
+    x[:64, 1] = 0.0                        # 0 / 0 -> NaN -> code 0
+    x[64:, 1] = np.linspace(-3, 3, 66)
+    x[5, 2] = np.nan                       # NaN poisons the block's absmax -> every code 0
+    x[:, 3] = 70000.0                      # fp16 overflow -> amax inf -> x / inf = 0 -> code 8
+    code, sc = O.quantise_u4(x)
+    assert (code[:, 0] == 15).all() and sc[0, 0] == 0
+    assert (code[:64, 1] == 0).all()
+    assert np.isnan(sc[0, 2]) and (code[:64, 2] == 0).all()
+    assert np.isinf(sc[0, 3]) and (code[:, 3] == 8).all()
+
+
+def test_sketch_scores_equal_store_scores_with_fp32_scales():
+    """The CPU baseline scorer (sketch re-quantisation per depth, fp32 absmax) equals the
+    store scan on codes quantised with fp32 scales: two formulas, one result."""
+    rng = np.random.default_rng(3)
+    n, d, G = 300, 32, 3
+    k = (rng.standard_normal((n, d)) * np.exp(rng.standard_normal(d))).astype(np.float32)
+    q = rng.standard_normal((G, d)).astype(np.float32)
+    var = k[16:].var(0, ddof=1)
+    s1, t = O.sketch_planes_scores(q, k, var, 20)
+    code, sc = O.quantise_u4(k, "f32")
+    s2 = O.scan_planes(q[None], code[None], sc[None], t[None])[0]
+    np.testing.assert_allclose(s1, s2, rtol=1e-5, atol=1e-4 * np.abs(s2).max())
+
+
+# ----------------------------------------------------------------------------- packing
+def test_pack_bruteforce_and_roundtrip():
+    rng = np.random.default_rng(0)
+    code = rng.integers(0, 16, size=(2, 130, 3), dtype=np.uint8)
+    planes = O.pack_planes(code)
+    assert planes.shape == (2, 3, 3, 4) and planes.dtype == np.uint64
+    for b in range(2):
+        for blk in range(3):
+            for j in range(3):
+                for p in range(4):
+                    word = 0
+                    for i in range(64):
+                        tok = blk * 64 + i
+                        c = int(code[b, tok, j]) if tok < 130 else 0
+                        word |= ((c >> (3 - p)) & 1) << i
+                    assert int(planes[b, blk, j, p]) == word
+    np.testing.assert_array_equal(O.unpack_planes(planes, 130), code)
+
+
+@pytest.mark.parametrize("sub", [1, 3, 16])
+def test_to_superblocks_bruteforce(sub):
+    rng = np.random.default_rng(sub)
+    nb, d = 5, 3
+    planes = rng.integers(0, 2 ** 63, size=(2, nb, d, 4), dtype=np.uint64)
+    scales = rng.random((2, nb, d)).astype(np.float32)
+    pl, sc = O.to_superblocks(planes, scales, sub)
+    nsb = -(-nb // sub)
+    assert pl.shape == (2, nsb, d, 4, sub) and sc.shape == (2, nsb, d, sub)
+    for b in range(2):
+        for s in range(nsb):
+            for j in range(d):
+                for bs in range(sub):
+                    blk = s * sub + bs
+                    assert sc[b, s, j, bs] == (scales[b, blk, j] if blk < nb else 0)
+                    for p in range(4):
+                        assert pl[b, s, j, p, bs] == (planes[b, blk, j, p] if blk < nb else 0)
+
+
+def test_bytes_planes():
+    t = np.array([[4, 3, 1, 0], [0, 0, 0, 0]])
+    assert O.bytes_planes(t, 130) == ((8 * 8 + 2 * 3) * 3)
+
+
+# ----------------------------------------------------------------------------- log2
+def test_flog2_matches_float64_log2():
+    rng = np.random.default_rng(0)
+    e = rng.uniform(-99, 127, 400_000)
+    x = (2.0 ** e * rng.uniform(1, 2, e.shape)).astype(np.float32)
+    x = np.concatenate([x, np.float32(2.0) ** np.arange(-99, 127, dtype=np.float32),
+                        np.array([1e-30, 1.0, 3.0, 0.63333338, 12.216667, 65504.0], np.float32)])
+    ref = np.log2(x.astype(np.float64)).astype(np.float32)
+    got = O.flog2(x)
+    assert np.array_equal(got, ref), int((got != ref).sum())
+    assert O.flog2(np.float32(np.inf)) == np.inf and np.isnan(O.flog2(np.float32(np.nan)))
+
+
+# ----------------------------------------------------------------------------- plan
+def test_plan_invariants_and_compaction():
+    rng = np.random.default_rng(1)
+    BH, d = 12, 128
+    g = (np.exp(rng.standard_normal((BH, d)) * 3) * rng.random((BH, d))).astype(np.float32)
+    g[0, :10] = 0
+    budget = rng.integers(0, 300, BH).astype(np.float32)
+    p = O.make_plan(g, budget)
+    t = p["t"].astype(np.int64)
+    assert (t >= 0).all() and (t <= 4).all()
+    assert (t.sum(1) <= budget).all()
+    for b in range(BH):
+        order = np.argsort(g[b])
+        assert (np.diff(t[b][order]) >= 0).all()          # larger gain never gets fewer planes
+        a = [j for j in range(d) if t[b, j] > 0]
+        assert p["act"][b].tolist() == a + [0] * (d - len(a)) and p["nact"][b] == len(a)
+        pr = [j * 4 + q for j in range(d) for q in range(t[b, j])]
+        assert p["pairs"][b].tolist() == pr + [0] * (4 * d - len(pr)) and p["npairs"][b] == len(pr)
+        for c in range(1, 5):
+            cc = [j for j in range(d) if t[b, j] == c]
+            assert p["cls"][b, c - 1].tolist() == cc + [0] * (d - len(cc)) and p["clsn"][b, c - 1] == len(cc)
+
+
+def test_plan_equals_greedy_waterfill():
+    """Where the bisection spends the whole budget, t equals the greedy reverse
+    water-filling allocation (scripts/sketch.py:19-25) at the same budget."""
+    rng = np.random.default_rng(7)
+    checked = 0
+    for trial in range(60):
+        d = 128
+        g = np.exp(rng.standard_normal(d) * 3).astype(np.float32)
+        B = int(rng.integers(1, 400))
+        t = O.make_plan(g[None], B)["t"][0].astype(np.int64)
+        if t.sum() != B:
+            continue
+        assert t.tolist() == O.waterfill(g, B).tolist()
+        checked += 1
+    assert checked > 40
+
+
+# ----------------------------------------------------------------------------- scan
+@pytest.mark.parametrize("sub", [16, 2, 5])
+def test_scan_bits_formulation_equals_dequant_formulation(sub):
+    rng = np.random.default_rng(sub)
+    BH, G, n, d = 2, 3, 500, 16
+    K = (rng.standard_normal((BH, n, d)) * np.exp(rng.standard_normal(d))).astype(np.float32)
+    q = rng.standard_normal((BH, G, d)).astype(np.float32)
+    code, sc = O.quantise_u4(K)
+    t = rng.integers(0, 5, size=(BH, d))
+    pl, scb = O.to_superblocks(O.pack_planes(code), sc, sub)
+    a = O.scan_planes(q, code, sc, t)
+    b = O.scan_planes_bits(q, pl, scb, t, n, sub)
+    np.testing.assert_allclose(a, b, rtol=1e-9, atol=1e-9)
+
+
+def test_scan_depth4_error_bound():
+    """At depth 4 every value is within a/16 of the key, so |score - q.k| <= sum_j |q_j| a_bj / 16."""
+    rng = np.random.default_rng(4)
+    n, d = 640, 32
+    K = (rng.standard_normal((1, n, d)) * np.exp(rng.standard_normal(d))).astype(np.float32)
+    q = rng.standard_normal((1, 2, d)).astype(np.float32)
+    code, sc = O.quantise_u4(K)
+    s = O.scan_planes(q, code, sc, np.full((1, d), 4))[0]
+    exact = q[0].astype(np.float64) @ K[0].T.astype(np.float64)
+    bound = (np.abs(q[0]).astype(np.float64) @ np.repeat(sc[0], 64, 0)[:n].T.astype(np.float64)) / 16
+    assert (np.abs(s - exact) <= bound * (1 + 1e-6) + 1e-9).all()
+
+
+# ----------------------------------------------------------------------------- top-k
+def _brute_topk(row, k, sink, local, m):
+    n = len(row)
+    s = [float(v) for v in row]
+    for i in range(min(sink, n)):
+        s[i] = -math.inf
+    for i in range(max(m - local, 0), n):
+        s[i] = -math.inf
+
+    def key(i):
+        v = s[i]
+        return (0, 0.0, i) if math.isnan(v) else (1, -v, i)
+
+    kk = k - sink - local
+    return sorted(range(n), key=key)[:kk] + list(range(sink)) + list(range(m - local, m))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_bruteforce(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(40, 300))
+    rows = rng.integers(-5, 6, size=(3, n)).astype(np.float32)       # many ties
+    rows[0, rng.integers(0, n, 5)] = np.nan
+    rows[1, rng.integers(0, n, 5)] = -np.inf
+    rows[2, rng.integers(0, n, 8)] = -0.0
+    sink, local = int(rng.integers(0, 5)), int(rng.integers(0, 10))
+    m = n + int(rng.integers(0, 3))
+    k = sink + local + int(rng.integers(0, n - sink))
+    got = O.sink_local_topk(rows, k, sink, local, m=m)
+    for r in range(3):
+        assert got[r].tolist() == _brute_topk(rows[r], k, sink, local, m)
+
+
+# ----------------------------------------------------------------------------- gathers
+def test_gather_rows_and_union():
+    rng = np.random.default_rng(5)
+    BH, n, d, G, k, nrec = 2, 50, 8, 3, 7, 4
+    Ks = rng.standard_normal((BH, n, d)).astype(np.float32)
+    Vs = rng.standard_normal((BH, n, d)).astype(np.float32)
+    Kr = rng.standard_normal((BH, nrec, d)).astype(np.float32)
+    Vr = rng.standard_normal((BH, nrec, d)).astype(np.float32)
+    idx = rng.integers(0, n + nrec + 2, size=(BH, G, k))
+    idx[0, 0, 0] = -1
+    K, V, nu = O.gather_union(idx, n, Ks, Vs, Kr, Vr)
+    for b in range(BH):
+        host = set()
+        for g in range(G):
+            for i in range(k):
+                tok = int(idx[b, g, i])
+                if 0 <= tok < n:
+                    host.add(tok)
+                    exp_k, exp_v = Ks[b, tok], Vs[b, tok]
+                elif tok >= n:
+                    r = min(max(tok - n, 0), nrec - 1)
+                    exp_k, exp_v = Kr[b, r], Vr[b, r]
+                else:
+                    exp_k = exp_v = np.zeros(d, np.float32)
+                np.testing.assert_array_equal(K[b, g, i], exp_k)
+                np.testing.assert_array_equal(V[b, g, i], exp_v)
+        assert nu[b] == len(host)
+    r = O.gather_rows(Ks, np.array([[3, -1, 0], [49, 2, -5]]))
+    np.testing.assert_array_equal(r[0, 0], Ks[0, 3])
+    assert (r[0, 1] == 0).all() and (r[1, 2] == 0).all()
+    np.testing.assert_array_equal(r[1, 0], Ks[1, 49])
