@@ -124,14 +124,18 @@ __global__ __launch_bounds__(256) void topk_hist_kernel(const float *__restrict_
   }
 }
 
-__device__ __forceinline__ void wave_append(bool pred, uint64_t val, uint32_t *counter, uint64_t *buf, int lane) {
+// Wave-aggregated append of `val` where pred holds; slots past `cap` are
+// dropped (the counts of a consistent selection never reach cap).
+__device__ __forceinline__ void wave_append(bool pred, uint64_t val, uint32_t *counter, uint64_t *buf, uint64_t cap,
+                                            int lane) {
   const uint64_t m = __ballot(pred);
   if (m == 0) return;
   const int leader = __ffsll((unsigned long long)m) - 1;
   uint32_t base = 0;
   if (lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
   base = __shfl(base, leader, kWave);
-  if (pred) buf[base + __popcll(m & ((1ull << lane) - 1ull))] = val;
+  const uint64_t slot = (uint64_t)base + __popcll(m & ((1ull << lane) - 1ull));
+  if (pred && slot < cap) buf[slot] = val;
 }
 
 __global__ __launch_bounds__(256) void topk_collect_kernel(const float *__restrict__ scores, int64_t n, int64_t sink,
@@ -151,8 +155,8 @@ __global__ __launch_bounds__(256) void topk_collect_kernel(const float *__restri
     const uint32_t key = in ? masked_key(rs, i, sink, lstart) : 0u;
     const uint32_t d = key >> kDigitShift;
     const uint64_t k64 = ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
-    wave_append(in && d > d1, k64, &st->sel_cnt, sel, lane);
-    wave_append(in && d == d1, k64, &st->cand_cnt, cand, lane);
+    wave_append(in && d > d1, k64, &st->sel_cnt, sel, (uint64_t)k, lane);
+    wave_append(in && d == d1, k64, &st->cand_cnt, cand, (uint64_t)n, lane);
   }
 }
 
@@ -195,8 +199,8 @@ __global__ __launch_bounds__(kFinThreads) void topk_finalize_kernel(int64_t n, i
   const int64_t row = blockIdx.x;
   const int64_t kk = k - sink - local;
   const RowState st = ws.state[row];
-  const uint32_t sel_cnt = st.sel_cnt;
-  const uint32_t cand_cnt = st.cand_cnt;
+  const uint32_t sel_cnt = min(st.sel_cnt, (uint32_t)kk);
+  const uint32_t cand_cnt = min(st.cand_cnt, (uint32_t)n);
   const uint32_t need2 = (uint32_t)kk - sel_cnt;
   const uint64_t *cand = ws.cand + row * n;
   const uint64_t *sel = ws.sel + row * k;
