@@ -3,13 +3,16 @@
 Workload (BASELINE.json metric "scanned tokens/s/GPU (scan+top-k) at 1M ctx"):
 config 3's layer shape -- 8 KV heads, G = 4 query heads per KV head, n = 2^20
 tokens, D = 128, "56-bit" plan (budget B = 48 code bits), k = 512 with 4 sink +
-32 local -- on seeded synthetic bf16 keys.  One step = make_plan -> scan ->
-sink_local_topk -> union row gather over all 8 KV heads.
+32 local -- on seeded synthetic bf16 keys.  One step = make_plan -> fused
+scan + sink/local top-k -> union row gather over all 8 KV heads.  The unfused
+pair (scan writing scores, then sink_local_topk) is timed in the same steps and
+must select the same indices.
 
 `value` counts scanned token*heads per second of scan + top-k with the index
-resident in HBM (n * BH / (t_scan + t_topk)).  The same step with the plane
-index and the K/V rows in mapped pinned host memory (the scan reads over PCIe)
-is reported under "host_resident".
+resident in HBM (n * BH / t_scan_topk).  The roofline object is for the scan
+kernel (one launch, algorithmic bytes = bytes_planes).  The same step with the
+plane index and the K/V rows in mapped pinned host memory (the scan reads over
+PCIe) is reported under "host_resident".
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-host] [--no-cpu]
 """
@@ -75,7 +78,9 @@ class StageTimer:
 
 
 def run_regime(torch, bp, off, x, store, Ksrc, Vsrc, steps, warmup, stages_only=False):
-    dev = x["q"].device
+    """Times one decode-step selection per step.  Stages: plan, the unfused scan
+    (scores to HBM) and top-k over those scores (the reference's two calls), the
+    fused scan+top-k (what the step uses), and the union row gather."""
     q, g = x["q"], x["g"]
     n, BH, k = x["n"], x["BH"], x["k"]
 
@@ -86,13 +91,16 @@ def run_regime(torch, bp, off, x, store, Ksrc, Vsrc, steps, warmup, stages_only=
         o["scores"] = store.scan(q, o["plan"])
 
     def s_topk(o):
-        o["idx"] = bp.sink_local_topk(o["scores"], k, x["sink"], x["local"])
+        o["idx_unfused"] = bp.sink_local_topk(o["scores"], k, x["sink"], x["local"])
+
+    def s_fused(o):
+        o["idx"] = store.scan_topk(q, o["plan"], k, x["sink"], x["local"])
 
     def s_gather(o):
         o["rows"] = off.gather_union(o["idx"], n, Ksrc, Vsrc, n)
 
-    names = ["plan", "scan", "topk"] + ([] if stages_only else ["gather"])
-    fns = {"plan": s_plan, "scan": s_scan, "topk": s_topk, "gather": s_gather}
+    names = ["plan", "scan", "topk", "scan_topk"] + ([] if stages_only else ["gather"])
+    fns = {"plan": s_plan, "scan": s_scan, "topk": s_topk, "scan_topk": s_fused, "gather": s_gather}
     timer = StageTimer(torch, names)
     for _ in range(warmup):
         timer.step(fns)
@@ -105,6 +113,8 @@ def run_regime(torch, bp, off, x, store, Ksrc, Vsrc, steps, warmup, stages_only=
     wall = (time.perf_counter() - t0) * 1e3 / steps
     stage = timer.collect()
     plan = out["plan"]
+    if not bool(torch.equal(out["idx"], out["idx_unfused"])):
+        raise RuntimeError("fused scan+top-k disagrees with scan then sink_local_topk")
     scan_bytes = bp.bytes_planes(plan["t"], n)
     uniq = int(out["rows"][2].sum().item()) if "rows" in out else 0
     row_bytes = 2 * uniq * 128 * 2
@@ -174,7 +184,7 @@ def main():
     hbm = run_regime(torch, bp, off, x, store, x["K"], V, a.steps, a.warmup, a.stages_only)
     st = hbm["stage_ms"]
     n, BH = x["n"], x["BH"]
-    scan_topk_ms = st["scan"] + st["topk"]
+    scan_topk_ms = st["scan_topk"]
     value = n * BH / (scan_topk_ms * 1e-3)
     achieved = hbm["scan_bytes"] / (st["scan"] * 1e-3) / 1e9
     log(f"[bench] HBM: stages {json.dumps({k: round(v, 4) for k, v in st.items()})} ms, "
@@ -198,7 +208,7 @@ def main():
             hr = run_regime(torch, bp, off, x, hstore, K_dev, V_dev, max(3, a.steps // 2), 2)
             same = bool(torch.equal(hr["idx"], hbm["idx"]))
             hs = hr["stage_ms"]
-            tot = sum(hs.values())
+            tot = hs["plan"] + hs["scan_topk"] + hs["gather"]
             pcie_bytes = hr["scan_bytes"] + hr["row_bytes"]
             # measured pinned H2D copy rate, the reference's memcpy comparison
             src = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
@@ -213,7 +223,7 @@ def main():
             torch.cuda.synchronize()
             h2d = 4 * src.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9
             host = {"stage_ms": {k: round(v, 4) for k, v in hs.items()},
-                    "scanned_tokens_per_s": n * BH / ((hs["scan"] + hs["topk"]) * 1e-3),
+                    "scanned_tokens_per_s": n * BH / (hs["scan_topk"] * 1e-3),
                     "step_ms": tot, "pcie_bytes_per_step": pcie_bytes,
                     "pcie_GBps_step": pcie_bytes / (tot * 1e-3) / 1e9,
                     "scan_pcie_GBps": hr["scan_bytes"] / (hs["scan"] * 1e-3) / 1e9,
@@ -228,20 +238,21 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        xs = W.config_inputs(a.config, device="cpu", n=min(x["n"], 262144), BH=1)
-        cpu = cpu_baseline(xs)
+        xs = W.config_inputs(a.config, device="cpu", n=min(x["n"], 1 << 20), BH=1)
+        cpu = cpu_baseline(xs, reps=5)
         log(f"[bench] cpu baseline: {json.dumps(cpu)}")
 
     rec = {
         "metric": "scanned tokens/s/GPU (scan+top-k) at 1M ctx",
         "value": value, "unit": "token*heads/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": sum(st.values()), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": st["plan"] + st["scan_topk"] + st.get("gather", 0.0), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded lognormal-scaled keys, planted keys; no model weights)",
         "config": {"workload": W.CONFIGS[a.config]["name"] + ", index + rows in HBM", "BH": BH, "G": x["G"],
                    "n": n, "budget_bits": x["budget"], "k": x["k"], "sink": x["sink"], "local": x["local"],
                    "bits_per_token": round(hbm["bits_per_token"], 3), "parallelism": "single GPU"},
         "stage_ms": {k: round(v, 4) for k, v in st.items()},
         "scan_topk_ms": scan_topk_ms,
+        "unfused_scan_plus_topk_ms": st["scan"] + st["topk"],
         "roofline": {"bound": "hbm", "kernel": "scan_planes_kernel", "achieved": achieved, "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": hbm["scan_bytes"]},

@@ -243,6 +243,30 @@ class PlaneStore:
                   int(self.nsb), sub, b0, b1, _ptr(out), _stream(q.device))
         return out
 
+    def scan_topk(self, q, plan, k, sink=4, local=32, m=None):
+        """Fused scan + sink/local top-k: the same int64 indices [BH, G, k] as
+        sink_local_topk(self.scan(q, plan), k, sink, local, m), without writing the
+        score tensor (the scan keeps only candidates above a sampled threshold)."""
+        _need_gpu(q)
+        BH, G, d = q.shape
+        if BH != self.BH:
+            raise AssertionError(f"q has BH={BH}, store has {self.BH}")
+        if plan["cls"].shape[1] > 4:
+            raise ValueError("the store holds 4 planes: plan with bmax <= 4")
+        n = self.n
+        m = n if m is None else int(m)
+        sub = int(getattr(self, "sub", SUB))
+        qc = q.contiguous().float()
+        idx = torch.empty(BH, G, int(k), dtype=torch.int64, device=q.device)
+        L = _lib.lib()
+        nbytes = L.fathom_scan_topk_workspace_bytes(BH, G, n, int(k), int(sink), int(local))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        _lib.call("fathom_scan_topk", _ptr(qc), BH, G, d, _ptr(plan["t"]), _ptr(plan["act"]), _ptr(plan["nact"]),
+                  ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), n,
+                  int(self.nsb), sub, m, int(k), int(sink), int(local), _ptr(idx), _ptr(ws), nbytes,
+                  _stream(q.device))
+        return idx
+
     def nbytes(self):
         return self.BH * self.nsb * D * 4 * int(getattr(self, "sub", SUB)) * 8 + \
             self.BH * self.nsb * D * int(getattr(self, "sub", SUB)) * 2

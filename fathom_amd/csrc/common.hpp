@@ -64,6 +64,12 @@ __device__ __forceinline__ uint32_t score_key(float s) {
 }
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;  // score_key(-inf)
 
+// Inverse of score_key on non-NaN keys: the float whose key is `key` (keys
+// above +inf's key decode to NaN, which compares false).
+__device__ __forceinline__ float key_value(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
 // ------------------------------------------------------------------ wave primitives
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll

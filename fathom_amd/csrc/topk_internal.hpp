@@ -1,0 +1,119 @@
+// Selection machinery shared by the standalone top-k and the fused scan+top-k.
+//
+// Exact top-kk of a row in three steps:
+//   select    the exact kk-th largest key T of a sample of the row (tiles of
+//             1024 tokens, every S-th tile).  A sample is a subset of the row,
+//             so T never exceeds the row's kk-th largest key: every element of
+//             the top kk has key >= T;
+//   filter    elements with key >= T are appended to the row's candidate list
+//             (about S * kk of them for a representative sample);
+//   finalize  one workgroup per row selects the exact kk largest candidates by
+//             K64 = key << 32 | (0xFFFFFFFF - index) and writes them sorted.
+// Exactness never depends on the sample: a poor sample only yields more
+// candidates (the list holds a whole row, so it cannot overflow).
+#pragma once
+#include "common.hpp"
+
+namespace fathom {
+
+constexpr int64_t kTileTok = 2048;  // tokens per scan tile (32 blocks)
+constexpr int64_t kMaxSample = 65536; // sampled keys per row (held in registers by select)
+
+struct TopkSel {
+  uint32_t *thr;       // [rows] threshold key
+  uint32_t *cand_cnt;  // [rows] candidates appended
+  uint64_t *cand;      // [rows, cand_cap] K64 candidates
+  int64_t cand_cap;
+};
+
+// Sample stride in tiles: about 8192 / kk expected candidates per row while
+// keeping at least 4 kk sampled tokens and at most kMaxSample of them.
+inline int64_t topk_tile_stride(int64_t n, int64_t kk) {
+  const int64_t ntiles = cdiv(n, kTileTok);
+  int64_t S = kk > 0 ? 8192 / kk : 64;
+  const int64_t keep = kk > 0 ? (ntiles * kTileTok) / (4 * kk) : 64;
+  if (keep < S) S = keep;
+  const int64_t fit = cdiv(ntiles, kMaxSample / kTileTok);
+  if (S < fit) S = fit;
+  if (S < 1) S = 1;
+  return S;
+}
+
+inline int64_t topk_sample_tiles(int64_t n, int64_t S) { return cdiv(cdiv(n, kTileTok), S); }
+
+// 256-byte section alignment inside workspaces
+inline size_t ws_align(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Layout of the selection state inside a workspace; returns bytes used.
+size_t topk_sel_layout(int64_t rows, int64_t cand_cap, char *base, TopkSel *s);
+
+// Whole top-k workspace: sampled keys [rows, samp_cap] + selection state with a
+// candidate list of a full row.  S is sized for kk = k (an upper bound on
+// k - sink - local; a larger kk only means a denser sample).
+size_t topk_layout(int64_t rows, int64_t n, int64_t k, char *base, uint32_t **samp, int64_t *samp_cap, TopkSel *sel,
+                   int64_t *S_out);
+
+int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, TopkSel s, hipStream_t st);
+int launch_sample_scores(const float *scores, int64_t rows, int64_t n, int64_t S, int64_t sink, int64_t lstart,
+                         uint32_t *samp, int64_t samp_cap, hipStream_t st);
+int launch_filter_scores(const float *scores, int64_t rows, int64_t n, int64_t sink, int64_t lstart, TopkSel s,
+                         hipStream_t st);
+int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, TopkSel s, int64_t *idx,
+                    hipStream_t st);
+// kk == 0: only the sink and local positions are written.
+int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st);
+// Shape checks shared by the top-k entry points (FATHOM_OK or an error status).
+int check_topk_args(int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local, const char *who);
+
+// Wave-aggregated append of K64 values whose predicate holds to a row's list.
+__device__ __forceinline__ void wave_append(bool pred, uint64_t val, uint32_t *counter, uint64_t *buf, uint64_t cap,
+                                            int lane) {
+  const uint64_t m = __ballot(pred);
+  if (m == 0) return;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  uint32_t base = 0;
+  if (lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
+  base = __shfl(base, leader, kWave);
+  const uint64_t slot = (uint64_t)base + __popcll(m & ((1ull << lane) - 1ull));
+  if (pred && slot < cap) buf[slot] = val;
+}
+
+// Wave-aggregated append into a workgroup-local LDS list; entries past lcap go
+// straight to the global list (one atomic each: only hit by adversarial rows).
+__device__ __forceinline__ void wave_append_local(bool pred, uint64_t val, uint32_t *lcnt, uint64_t *lbuf,
+                                                  uint32_t lcap, uint32_t *gcnt, uint64_t *gbuf, uint64_t gcap,
+                                                  int lane) {
+  const uint64_t m = __ballot(pred);
+  if (m == 0) return;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  uint32_t base = 0;
+  if (lane == leader) base = atomicAdd(lcnt, (uint32_t)__popcll(m));
+  base = __shfl(base, leader, kWave);
+  const uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+  if (pred) {
+    if (slot < lcap) {
+      lbuf[slot] = val;
+    } else {
+      const uint32_t p = atomicAdd(gcnt, 1u);
+      if ((uint64_t)p < gcap) gbuf[p] = val;
+    }
+  }
+}
+
+// Copies a workgroup's LDS list to the global list with one reservation.
+// Call from all threads after a barrier that completes the appends.
+__device__ __forceinline__ void flush_local(const uint32_t *lcnt, const uint64_t *lbuf, uint32_t lcap,
+                                            uint32_t *gcnt, uint64_t *gbuf, uint64_t gcap, uint32_t *s_base) {
+  const uint32_t nloc = min(*lcnt, lcap);
+  if (threadIdx.x == 0) *s_base = nloc ? atomicAdd(gcnt, nloc) : 0u;
+  __syncthreads();
+  const uint32_t base = *s_base;
+  for (uint32_t i = threadIdx.x; i < nloc; i += blockDim.x)
+    if ((uint64_t)base + i < gcap) gbuf[base + i] = lbuf[i];
+}
+
+__device__ __forceinline__ uint64_t k64_of(uint32_t key, int64_t i) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+
+}  // namespace fathom

@@ -112,6 +112,22 @@ int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const i
                        int64_t sub, int64_t blk0, int64_t blk1, float *out, void *stream);
 
 /*
+ * Fused scan + sink/local top-k: the selection of fathom_scan_planes followed by
+ * fathom_sink_local_topk on its scores (kernels/bitplane.py:319-338 then
+ * :372-378, as chained by scripts/B_kernel_bench.py:74 and
+ * scripts/B_e2e_offload_v2.py:203, 224-227), without materialising the score
+ * tensor.  Same arguments as fathom_scan_planes over the whole sequence, plus
+ * the top-k arguments of fathom_sink_local_topk; idx [BH * G, k] int64 is
+ * identical to running the two entry points.  workspace:
+ * fathom_scan_topk_workspace_bytes(BH, G, n, k, sink, local) bytes.
+ */
+size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink, int64_t local);
+int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t, const int32_t *act,
+                     const int32_t *nact, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb,
+                     int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/*
  * sink_local_topk (kernels/bitplane.py:372-378; inline form with the current
  * length m at scripts/B_e2e_offload_v2.py:224-227).  For each of `rows` rows of
  * scores [rows, n] float32: mask [0, sink) and [max(m - local, 0), n) to -inf,

@@ -331,3 +331,56 @@ def test_config2_full_size_invariants():
     assert bool((err <= tol).all()), float(err.max())
     idx = bp.sink_local_topk(scores, x["k"])
     np.testing.assert_array_equal(idx.cpu().numpy(), O.sink_local_topk(scores.cpu().numpy(), x["k"]))
+
+
+# ----------------------------------------------------------------------------- fused scan + top-k
+@pytest.mark.parametrize("cfg,n,BH,k,sub", [(1, 16384, None, 128, None), (2, 40000, 2, 512, None),
+                                            (4, 30000, 2, 2048, None), (2, 5000, 3, 300, 7), (2, 700, 1, 60, None)])
+def test_scan_topk_fused_equals_unfused(cfg, n, BH, k, sub):
+    print(f"[fused] cfg={cfg} n={n} BH={BH} k={k} sub={sub}", flush=True)
+    x, st, plan = _scan_case(cfg, n, BH, sub)
+    q = x["q"].to(DEV)
+    sink, local = x["sink"], x["local"]
+    ref = bp.sink_local_topk(st.scan(q, plan), k, sink, local)
+    got = st.scan_topk(q, plan, k, sink, local)
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    m = n + 3
+    ref = bp.sink_local_topk(st.scan(q, plan), k, sink, local, m=m)
+    got = st.scan_topk(q, plan, k, sink, local, m=m)
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
+
+
+def test_scan_topk_fused_host_resident():
+    x, st, plan = _scan_case(2, 50000, 2)
+    q = x["q"].to(DEV)
+    ref = st.scan_topk(q, plan, 512)
+    _, pl_dev, hp1 = off.host_mapped(st.planes_k)
+    _, sc_dev, hp2 = off.host_mapped(st.scales_k)
+    try:
+        st.planes32, st.scales_k = pl_dev, sc_dev
+        got = st.scan_topk(q, plan, 512)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    finally:
+        off.free_host(hp1)
+        off.free_host(hp2)
+
+
+def test_scan_topk_adversarial_order():
+    """Scores rising along the sequence: the sampled threshold admits far more
+    candidates than usual; the result stays exact."""
+    BH, n, d = 1, 60000, 128
+    K = torch.zeros(BH, n, d)
+    K[0, :, 0] = torch.linspace(-1, 1, n) * 3.0
+    K[0, :, 1] = torch.randn(n) * 0.01
+    st = bp.PlaneStore(K.to(DEV))
+    q = torch.zeros(BH, 2, d)
+    q[0, :, 0] = 1.0
+    q[0, 1, 1] = 1.0
+    g = torch.ones(BH, d)
+    g[0, 0] = 1000.0
+    g[0, 1] = 10.0
+    plan = bp.make_plan(g.to(DEV), 6.0)
+    ref = bp.sink_local_topk(st.scan(q.to(DEV), plan), 512)
+    got = st.scan_topk(q.to(DEV), plan, 512)
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
