@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--no-host", action="store_true", help="skip the host-resident measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--stages-only", action="store_true", help="scan + top-k only (for profiling runs)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the run, launch a plain fp32 device copy kernel of this many MiB 3 times "
+                         "(the known-size kernel that scales rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -235,6 +238,15 @@ def main():
         finally:
             for h in hps:
                 off.free_host(h)
+
+    if a.calib_copy_mib > 0:
+        # torch's elementwise copy kernel: reads and writes calib_copy_mib MiB per launch
+        src = torch.ones(a.calib_copy_mib << 18, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: 3 x {a.calib_copy_mib} MiB read + written")
 
     cpu = None
     if not a.no_cpu:
