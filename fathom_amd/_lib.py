@@ -25,10 +25,10 @@ PROTOTYPES = {
     "fathom_to_superblocks": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "fathom_dequant_planes": (_i32, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "fathom_make_plan": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "fathom_scan_planes": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+    "fathom_scan_planes": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp, _vp]),
     "fathom_scan_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
-    "fathom_scan_topk": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+    "fathom_scan_topk": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _vp, _vp, _sz, _vp]),
     "fathom_topk_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "fathom_sink_local_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),

@@ -186,6 +186,16 @@ def make_plan_torch(g, budget, bmax=4, iters=30):
 
 
 # ----------------------------------------------------------------------------- store + scan
+def _plan_classes(plan, BH, d):
+    """The plan's depth-class lists as the scan kernels read them: cls int32
+    [BH, bmax, D] and clsn int32 [BH, bmax], contiguous, on the GPU."""
+    cls, clsn = plan["cls"], plan["clsn"]
+    _need_gpu(cls, clsn)
+    if cls.dim() != 3 or cls.shape[0] != BH or cls.shape[2] != d or tuple(clsn.shape) != tuple(cls.shape[:2]):
+        raise ValueError(f"plan cls/clsn of shapes {tuple(cls.shape)}/{tuple(clsn.shape)} do not match BH={BH}, D={d}")
+    return cls.to(torch.int32).contiguous(), clsn.to(torch.int32).contiguous()
+
+
 class PlaneStore:
     """K [BH, n, D] (any float dtype, on the GPU) -> superblock-ordered bit-plane
     store on the same device (kernels/bitplane.py:310-340).
@@ -238,7 +248,8 @@ class PlaneStore:
         b0, b1 = (0, nb) if blocks is None else (int(blocks[0]), int(blocks[1]))
         sub = int(getattr(self, "sub", SUB))
         qc = q.contiguous().float()
-        _lib.call("fathom_scan_planes", _ptr(qc), BH, G, d, _ptr(plan["t"]), _ptr(plan["act"]), _ptr(plan["nact"]),
+        cls, clsn = _plan_classes(plan, BH, d)
+        _lib.call("fathom_scan_planes", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1],
                   ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), self.n,
                   int(self.nsb), sub, b0, b1, _ptr(out), _stream(q.device))
         return out
@@ -261,7 +272,8 @@ class PlaneStore:
         L = _lib.lib()
         nbytes = L.fathom_scan_topk_workspace_bytes(BH, G, n, int(k), int(sink), int(local))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-        _lib.call("fathom_scan_topk", _ptr(qc), BH, G, d, _ptr(plan["t"]), _ptr(plan["act"]), _ptr(plan["nact"]),
+        cls, clsn = _plan_classes(plan, BH, d)
+        _lib.call("fathom_scan_topk", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1],
                   ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), n,
                   int(self.nsb), sub, m, int(k), int(sink), int(local), _ptr(idx), _ptr(ws), nbytes,
                   _stream(q.device))

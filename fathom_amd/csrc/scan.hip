@@ -1,24 +1,31 @@
 // Partial-depth bit-plane scan (PlaneStore.scan) and the fused scan + top-k.
 //
-// A workgroup (4 waves) owns one (batch*KV head, tile of 32 blocks = 2048
-// tokens); wave w owns blocks 8w..8w+7 of the tile and lane = token of a block.
-// Active channels are processed 32 at a time.  For each chunk the workgroup
-// writes to LDS the per (channel, block, head) weight q_gj * a_bj * 2^(1-t_j)
-// (the dequantiser's step) and accumulates the constant q_gj a_bj (2^-t_j - 1);
-// then every wave adds weight * code for its tokens.
+// Score of token i of row (bh, g), with depth t_j planes read for channel j:
+//   s = sum_j q_gj * a_bj * 2^(1 - t_j) * x_j(i),   x = c_t - (2^t - 1) / 2,
+// where c_t is the top-t-bit code and a_bj the block absmax.  This is the
+// reference's dequantised value (c_t + 0.5 - 2^(t-1)) * a / 2^(t-1)
+// (kernels/bitplane.py:34-42) with the constant term folded into x: x is the
+// sum over the t plane bits of +-2^(t-2-p), so it is built from the plane
+// words alone by t v_cndmask selections between +-(4, 2, 1, 0.5) -- all inline
+// constants -- and t-1 adds, exactly.
 //
-// Two ways of reaching the plane words (chosen per call from the store's memory
-// type):
-//  * direct (store in HBM): the words of a (channel, plane) for the wave's 8
-//    blocks are wave-uniform, so they arrive by scalar loads (two 32-byte loads
-//    when the 8 blocks are consecutive words) into SGPRs, and each word is used
-//    as the lane mask of v_cndmask (inverse ballot): the t-bit code of the
-//    lane's token is a sum of t masked power-of-two constants -- 2t-1 VALU ops,
-//    no per-lane bit extraction and no LDS traffic for the planes;
-//  * staged (store in mapped host memory): the chunk's words and scales are
-//    copied to LDS with coalesced 8-byte vector loads, so the PCIe reads are
-//    whole (channel, plane) runs, and lanes extract bits from LDS.
-// Both produce bit-identical scores (same products, same summation order).
+// Lane = token: a 64-bit plane word holds one bit per lane of a wave64.
+// A workgroup owns a tile of 32 blocks (2048 tokens) of one row bh; each of
+// its 4 waves owns 8 consecutive blocks ("group") and works alone after the
+// workgroup has put q_gj * 2^(1-t_j) for all listed channels in LDS.
+// Channels are visited by depth class (the plan's cls lists), so the depth is
+// a compile-time constant of the inner loop.  Two kernels reach the planes:
+//  * direct (store in HBM, sub % 8 == 0): the group's plane words are 8
+//    consecutive words of each (channel, plane) and its 8 fp16 scales 16
+//    consecutive bytes, read by scalar loads into SGPRs; each word is the lane
+//    mask of a v_cndmask (no per-lane bit extraction) and each scale feeds a
+//    v_fma_mix (fp16 operand, no conversion): per (channel, block) the VALU
+//    work is 2t + G instructions;
+//  * staged (store in mapped host memory, or any other sub): a chunk of
+//    channels' words and scales is copied to LDS with coalesced vector loads,
+//    so PCIe reads are whole (channel, plane) runs, and lanes extract bits.
+// Both build the same exact x, multiply by the same scale and accumulate in
+// the same channel order: their scores are bit-identical.
 //
 // Output modes: scores [BH, G, n] (PlaneStore.scan), sampled keys (every S-th
 // tile, for the top-k threshold), or candidate emission (key >= threshold ->
@@ -29,10 +36,11 @@
 namespace fathom {
 namespace {
 
-constexpr int kTB = 32;     // blocks per tile
-constexpr int kBPW = 8;     // blocks per wave
-constexpr int kCH = 32;     // active channels per chunk
+constexpr int kGB = 8;             // blocks per wave
+constexpr int kWaves = 4;          // waves per workgroup
+constexpr int kTB = kGB * kWaves;  // blocks per tile
 constexpr int kMaxD = 256;
+constexpr int kCH = 16;            // channels per staged chunk
 constexpr uint32_t kRowLocal = 128;  // LDS candidates per (workgroup, row)
 static_assert(kTB * kBlk == kTileTok, "scan tile and top-k sample tile must agree");
 
@@ -46,83 +54,120 @@ struct Emit {
   int64_t sink, lstart;
 };
 
-typedef unsigned int u32x8 __attribute__((ext_vector_type(8)));  // four 64-bit plane words
+struct ScanArgs {
+  const float *q;          // [BH, G, D]
+  const int32_t *cls;      // [BH, bmax, D]
+  const int32_t *clsn;     // [BH, bmax]
+  const uint64_t *planes;  // [BH, nsb, D, 4, sub]
+  const uint16_t *scales;  // [BH, nsb, D, sub] fp16 bits
+  int64_t n, nsb, sub;
+  int64_t blk0, blk_end;   // blocks [blk0, blk_end) are emitted
+  int64_t tile0;           // tile of blockIdx.x == 0 (tile T = blocks [32T, 32T + 32))
+  int64_t tile_stride;     // tiles between consecutive workgroups
+  int D, bmax, ncls;       // classes 1..ncls are scanned (ncls = min(bmax, 4))
+};
 
-// Wave-uniform loads through the constant address space: always scalar loads
-// into SGPRs (the store and plan are read-only for the kernel's lifetime).
+typedef unsigned int u32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Wave-uniform loads through the constant address space: scalar loads into
+// SGPRs (the store, plan and queries are read-only for the kernel's lifetime).
 template <typename T>
 __device__ __forceinline__ T ld_uniform(const T *p) {
   return *(const __attribute__((address_space(4))) T *)(p);
 }
 
-// Weight exponent: codes of depth 4 are formed as code/2 (the inline constants
-// 4, 2, 1, 0.5), so their weight carries one more factor of two.
-__device__ __forceinline__ int wexp(int c) { return c >= 4 ? -2 : 1 - c; }
-
-__device__ __forceinline__ int64_t word_base(int64_t bh, int64_t b, int64_t nsb, int64_t sub, int D) {
-  const int64_t sb = b / sub;
-  return (bh * nsb + sb) * D * 4 * sub + (b - sb * sub);
-}
-
-__device__ __forceinline__ int64_t scale_index(int64_t bh, int64_t b, int64_t nsb, int64_t sub, int D, int j) {
-  const int64_t sb = b / sub;
-  return ((bh * nsb + sb) * D + j) * sub + (b - sb * sub);
+__device__ __forceinline__ int64_t sgpr64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 template <int G>
-struct ScanShared {
-  float q[G * kMaxD];
-  int ch[kCH];
-  int dep[kCH];
-  float sc[kCH * kTB];
-  float wt[kCH * kTB * G];  // [channel][block][head]
-  float cst[kTB * G];
+struct QShared {
+  float qw[kMaxD * G];  // q_gj * 2^(1 - t_j) for listed channels, [channel][head]
+};
+
+// Workgroup prologue: the depth-scaled query weights of every listed channel.
+// With prefetch, it also touches (one dword each) every plane and scale line
+// the tile's four groups will read, so the waves' scalar loads find them in
+// L2 instead of waiting on HBM one channel at a time; the returned value is
+// only there to keep those loads alive.
+template <int G>
+__device__ __forceinline__ uint32_t load_qw(QShared<G> &sh, const ScanArgs &a, int64_t bh, int64_t tb0,
+                                            bool prefetch) {
+  uint32_t pf = 0u;
+  const int64_t nblk_store = a.nsb * a.sub;
+  for (int c = 1; c <= a.ncls; ++c) {
+    const int nc = min(max(a.clsn[bh * a.bmax + c - 1], 0), a.D);
+    const int32_t *lst = a.cls + (bh * a.bmax + c - 1) * a.D;
+    for (int i = threadIdx.x; i < nc * G; i += 256) {
+      const int ci = i / G, g = i - ci * G;
+      const int j = lst[ci];
+      if (j >= 0 && j < a.D) sh.qw[j * G + g] = ldexpf(a.q[(bh * G + g) * a.D + j], 1 - c);
+    }
+    if (!prefetch) continue;
+    // items: (channel, plane or scale, group) -- c planes + 1 scale line per group
+    for (int i = threadIdx.x; i < nc * (c + 1) * kWaves; i += 256) {
+      const int w = i % kWaves, p = (i / kWaves) % (c + 1), ci = i / (kWaves * (c + 1));
+      const int j = lst[ci];
+      const int64_t b = tb0 + w * kGB;
+      if (j < 0 || j >= a.D || b >= nblk_store) continue;
+      const int64_t sb = (int64_t)((uint64_t)b / (uint64_t)a.sub);
+      const int64_t off = b - sb * a.sub;
+      if (p < c)
+        pf ^= *reinterpret_cast<const uint32_t *>(a.planes + ((bh * a.nsb + sb) * a.D + j) * 4 * a.sub + p * a.sub + off);
+      else
+        pf ^= *reinterpret_cast<const uint32_t *>(a.scales + ((bh * a.nsb + sb) * a.D + j) * a.sub + (off & ~1));
+    }
+  }
+  return pf;
+}
+
+// Exact symmetric code x = c - (2^C - 1)/2 of a lane's token from its C plane
+// words (word p is the lane mask of a select between +-2^(C-2-p)).
+template <int C>
+__device__ __forceinline__ float sym_code(const uint64_t *w) {
+#define FATHOM_SEL(p, v) (__builtin_amdgcn_inverse_ballot_w64(w[p]) ? (v) : -(v))
+  if (C == 1) return FATHOM_SEL(0, 0.5f);
+  if (C == 2) return FATHOM_SEL(0, 1.0f) + FATHOM_SEL(C > 1 ? 1 : 0, 0.5f);
+  if (C == 3) return (FATHOM_SEL(0, 2.0f) + FATHOM_SEL(C > 1 ? 1 : 0, 1.0f)) + FATHOM_SEL(C > 2 ? 2 : 0, 0.5f);
+  return (FATHOM_SEL(0, 4.0f) + FATHOM_SEL(C > 1 ? 1 : 0, 2.0f)) +
+         (FATHOM_SEL(C > 2 ? 2 : 0, 1.0f) + FATHOM_SEL(C > 3 ? 3 : 0, 0.5f));
+#undef FATHOM_SEL
+}
+
+// Same value from the integer code (staged kernel): exact in fp32.
+template <int C>
+__device__ __forceinline__ float sym_from_int(uint32_t code) {
+  return (float)code - (float)((1 << C) - 1) * 0.5f;
+}
+
+// a * x with a given as fp16 bits (v_fma_mix_f32: the fp16 operand needs no
+// conversion; + 0 keeps it one rounding, as a product).
+__device__ __forceinline__ float scaled(uint16_t a_bits, float x) {
+  return fmaf(__half2float(__ushort_as_half(a_bits)), x, 0.0f);
+}
+
+// --------------------------------------------------------------------- emission
+template <int G>
+struct EmitShared {
   uint64_t lbuf[G][kRowLocal];
   uint32_t lcnt[G];
   uint32_t lbase[G];
 };
 
-// Chunk prologue: channel list, block scales, weights, constant term.
-template <int G>
-__device__ __forceinline__ void chunk_prepare(ScanShared<G> &sh, const int8_t *tpl, const int32_t *act,
-                                              const uint16_t *scales, int64_t bh, int64_t tb0, int64_t blk_end,
-                                              int64_t nsb, int64_t sub, int D, int a0, int na, float &cst_acc) {
-  const int tid = threadIdx.x;
-  if (tid < na) {
-    const int j = act[bh * D + a0 + tid];
-    const bool ok = j >= 0 && j < D;
-    sh.ch[tid] = ok ? j : 0;
-    sh.dep[tid] = ok ? min(max((int)tpl[bh * D + j], 0), 4) : 0;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < na * kTB; idx += 256) {
-    const int bi = idx % kTB, a = idx / kTB;
-    const int64_t b = tb0 + bi;
-    sh.sc[idx] = (b < blk_end && sh.dep[a] > 0) ? f16_bits_to_float(scales[scale_index(bh, b, nsb, sub, D, sh.ch[a])])
-                                                : 0.0f;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < na * kTB * G; idx += 256) {
-    const int g = idx % G, bi = (idx / G) % kTB, a = idx / (G * kTB);
-    sh.wt[idx] = sh.q[g * D + sh.ch[a]] * ldexpf(sh.sc[a * kTB + bi], wexp(sh.dep[a]));
-  }
-  if (tid < kTB * G) {
-    const int bi = tid / G, g = tid % G;
-    for (int a = 0; a < na; ++a) {
-      const float cadd = ldexpf(0.5f, 1 - sh.dep[a]) - 1.0f;  // 2^-t - 1
-      cst_acc += sh.q[g * D + sh.ch[a]] * (sh.sc[a * kTB + bi] * cadd);
-    }
-  }
-  __syncthreads();
-}
-
 template <int G, int MODE>
-__device__ __forceinline__ void emit_tile(const Emit &em, ScanShared<G> &sh, float (&acc)[kBPW][G],
-                                          float cst_acc, int64_t bh, int64_t tb0, int64_t blk_end, int64_t n,
-                                          int wave, int lane, int64_t tile_idx) {
+__device__ __forceinline__ void emit_group(const Emit &em, EmitShared<G> &es, const float (&acc)[kGB][G],
+                                           int64_t bh, int64_t gb0, int64_t blk0, int64_t blk_end, int64_t n,
+                                           int wave, int lane, int64_t samp_tile) {
   const int tid = threadIdx.x;
-  if (tid < kTB * G) sh.cst[tid] = cst_acc;
-  if (MODE == kEmitFilter && tid < G) sh.lcnt[tid] = 0u;
+  if (MODE == kEmitFilter) {
+    if (tid < G) es.lcnt[tid] = 0u;
+    __syncthreads();
+  }
   float thr_f[G];
   bool thr_all[G];
   if (MODE == kEmitFilter) {
@@ -133,16 +178,14 @@ __device__ __forceinline__ void emit_tile(const Emit &em, ScanShared<G> &sh, flo
       thr_f[g] = key_value(thr);
     }
   }
-  __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kBPW; ++r) {
-    const int bi = wave * kBPW + r;
-    const int64_t b = tb0 + bi;
+  for (int r = 0; r < kGB; ++r) {
+    const int64_t b = gb0 + r;
     const int64_t tok = b * kBlk + lane;
-    const bool valid = b < blk_end && tok < n;
+    const bool valid = b >= blk0 && b < blk_end && tok < n;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float v = acc[r][g] + sh.cst[bi * G + g];
+      const float v = acc[r][g];
       const int64_t row = bh * G + g;
       if (MODE == kEmitScores) {
         if (valid) em.out[row * n + tok] = v;
@@ -150,13 +193,13 @@ __device__ __forceinline__ void emit_tile(const Emit &em, ScanShared<G> &sh, flo
         const bool masked = tok < em.sink || tok >= em.lstart;
         if (MODE == kEmitSample) {
           const uint32_t key = valid ? (masked ? kKeyNegInf : score_key(v)) : 0u;
-          em.samp[row * em.samp_cap + tile_idx * kTileTok + bi * kBlk + lane] = key;
+          em.samp[row * em.samp_cap + samp_tile * kTileTok + (wave * kGB + r) * kBlk + lane] = key;
         } else {
           // key >= thr tested on floats: thr_f is the value whose key is thr
           const float vm = masked ? -INFINITY : v;
           const bool pass = valid && (thr_all[g] || vm >= thr_f[g] || vm != vm);
-          wave_append_local(pass, pass ? k64_of(masked ? kKeyNegInf : score_key(v), tok) : 0ull, &sh.lcnt[g],
-                            sh.lbuf[g], kRowLocal, &em.sel.cand_cnt[row], em.sel.cand + row * em.sel.cand_cap,
+          wave_append_local(pass, pass ? k64_of(masked ? kKeyNegInf : score_key(v), tok) : 0ull, &es.lcnt[g],
+                            es.lbuf[g], kRowLocal, &em.sel.cand_cnt[row], em.sel.cand + row * em.sel.cand_cap,
                             (uint64_t)em.sel.cand_cap, lane);
         }
       }
@@ -166,280 +209,249 @@ __device__ __forceinline__ void emit_tile(const Emit &em, ScanShared<G> &sh, flo
     // one reservation per row, all rows at once, then one copy pass
     __syncthreads();
     if (tid < G) {
-      const uint32_t nloc = min(sh.lcnt[tid], kRowLocal);
-      sh.lbase[tid] = nloc ? atomicAdd(&em.sel.cand_cnt[bh * G + tid], nloc) : 0u;
+      const uint32_t nloc = min(es.lcnt[tid], kRowLocal);
+      es.lbase[tid] = nloc ? atomicAdd(&em.sel.cand_cnt[bh * G + tid], nloc) : 0u;
     }
     __syncthreads();
     for (int e = tid; e < G * (int)kRowLocal; e += 256) {
       const int g = e / (int)kRowLocal, i = e % (int)kRowLocal;
-      const uint32_t nloc = min(sh.lcnt[g], kRowLocal);
-      const uint64_t slot = (uint64_t)sh.lbase[g] + i;
+      const uint32_t nloc = min(es.lcnt[g], kRowLocal);
+      const uint64_t slot = (uint64_t)es.lbase[g] + i;
       if ((uint32_t)i < nloc && slot < (uint64_t)em.sel.cand_cap)
-        em.sel.cand[(bh * G + g) * em.sel.cand_cap + slot] = sh.lbuf[g][i];
+        em.sel.cand[(bh * G + g) * em.sel.cand_cap + slot] = es.lbuf[g][i];
     }
   }
 }
 
 // --------------------------------------------------------------------- direct (HBM) kernel
-// Value of a depth-C code of block r from its C plane words held in SGPRs: each
-// word is the lane mask of a v_cndmask between 0 and a power of two (inline
-// constants; depth 4 yields code / 2).
+// HB blocks per load group: 8 for depth <= 2, 4 for deeper classes (at most
+// 32 SGPRs of plane words live per group).
 template <int C>
-__device__ __forceinline__ float code_value(const uint64_t (&w)[C][4], int r) {
-  if (C == 1) return __builtin_amdgcn_inverse_ballot_w64(w[0][r]) ? 1.0f : 0.0f;
-  if (C == 2)
-    return (__builtin_amdgcn_inverse_ballot_w64(w[0][r]) ? 2.0f : 0.0f) +
-           (__builtin_amdgcn_inverse_ballot_w64(w[C > 1 ? 1 : 0][r]) ? 1.0f : 0.0f);
-  if (C == 3)
-    return ((__builtin_amdgcn_inverse_ballot_w64(w[0][r]) ? 4.0f : 0.0f) +
-            (__builtin_amdgcn_inverse_ballot_w64(w[C > 1 ? 1 : 0][r]) ? 2.0f : 0.0f)) +
-           (__builtin_amdgcn_inverse_ballot_w64(w[C > 2 ? 2 : 0][r]) ? 1.0f : 0.0f);
-  return ((__builtin_amdgcn_inverse_ballot_w64(w[0][r]) ? 4.0f : 0.0f) +
-          (__builtin_amdgcn_inverse_ballot_w64(w[C > 1 ? 1 : 0][r]) ? 2.0f : 0.0f)) +
-         ((__builtin_amdgcn_inverse_ballot_w64(w[C > 2 ? 2 : 0][r]) ? 1.0f : 0.0f) +
-          (__builtin_amdgcn_inverse_ballot_w64(w[C > 3 ? 3 : 0][r]) ? 0.5f : 0.0f));
-}
+struct Depth {
+  static constexpr int HB = C <= 2 ? 8 : 4;
+};
 
-__device__ __forceinline__ uint64_t word_of(const u32x8 &v, int r) {
-  return ((uint64_t)v[2 * r + 1] << 32) | v[2 * r];
-}
+template <int HB>
+struct WordVec;
+template <>
+struct WordVec<8> {
+  typedef u32x16 W;
+  typedef u32x4 S;
+};
+template <>
+struct WordVec<4> {
+  typedef u32x8 W;
+  typedef u32x2 S;
+};
 
-__device__ __forceinline__ int64_t sgpr64(int64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
-// One active channel of depth C for the wave's 8 blocks, in two halves of 4
-// blocks (at most 32 SGPRs of plane words live): every plane word of a half is
-// requested before the first is used, then weight * code.  CONTIG: the 8 blocks
-// are 8 consecutive words of each (channel, plane) starting at wb0, one 32-byte
-// scalar load per plane and half; otherwise one scalar load per block from the
-// per-block word offsets in LDS (negative: block past the scanned range).
-template <int C, int G, bool CONTIG>
-__device__ __forceinline__ void accum_channel(const uint64_t *planes, int64_t wb0, const int64_t *wbs, int64_t coff,
-                                              int64_t sub, const float *wt, float (&acc)[kBPW][G]) {
+// One channel of depth C over the wave's 8 blocks: pj = its plane-0 word of the
+// group's first block (plane p at + p*sub), sj = its first fp16 scale.
+template <int C, int G>
+__device__ __forceinline__ void direct_channel(const uint64_t *pj, const uint16_t *sj, int64_t sub, const float *qv,
+                                               float (&acc)[kGB][G]) {
+  constexpr int HB = Depth<C>::HB;
+  typedef typename WordVec<HB>::W WV;
+  typedef typename WordVec<HB>::S SV;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    // keeps the second half's loads below the first half's use (merged into
-    // one 64-byte load per plane they would need up to 64 SGPRs and spill)
-    if (h == 1 && C >= 3) __builtin_amdgcn_sched_barrier(0);
-    uint64_t w[C][4];
+  for (int h = 0; h < kGB / HB; ++h) {
+    // keeps the next half's loads below this half's use (merged loads would
+    // need twice the SGPRs)
+    if (h > 0) __builtin_amdgcn_sched_barrier(0);
+    WV wv[C];
 #pragma unroll
-    for (int p = 0; p < C; ++p) {
-      if (CONTIG) {
-        const u32x8 v = ld_uniform(reinterpret_cast<const u32x8 *>(planes + wb0 + coff + p * sub + 4 * h));
+    for (int p = 0; p < C; ++p) wv[p] = ld_uniform(reinterpret_cast<const WV *>(pj + p * sub + h * HB));
+    const SV sv = ld_uniform(reinterpret_cast<const SV *>(sj + h * HB));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) w[p][r] = word_of(v, r);
-      } else {
+    for (int r = 0; r < HB; ++r) {
+      uint64_t w[C];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t b = sgpr64(wbs[4 * h + r]);
-          w[p][r] = b >= 0 ? ld_uniform(planes + b + coff + p * sub) : 0ull;
-        }
-      }
-    }
+      for (int p = 0; p < C; ++p) w[p] = ((uint64_t)wv[p][2 * r + 1] << 32) | wv[p][2 * r];
+      const float x = sym_code<C>(w);
+      const uint32_t sd = sv[r >> 1];
+      const float u = scaled((uint16_t)((r & 1) ? (sd >> 16) : (sd & 0xFFFFu)), x);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float cf = code_value<C>(w, r);
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[4 * h + r][g] = fmaf(wt[(4 * h + r) * G + g], cf, acc[4 * h + r][g]);
+      for (int g = 0; g < G; ++g) acc[h * HB + r][g] = fmaf(qv[g], u, acc[h * HB + r][g]);
     }
   }
 }
 
-template <int G, bool CONTIG>
-__device__ __forceinline__ void accum_switch(int c, const uint64_t *planes, int64_t wb0, const int64_t *wbs,
-                                             int64_t coff, int64_t sub, const float *wt, float (&acc)[kBPW][G]) {
-  switch (c) {
-    case 1: accum_channel<1, G, CONTIG>(planes, wb0, wbs, coff, sub, wt, acc); break;
-    case 2: accum_channel<2, G, CONTIG>(planes, wb0, wbs, coff, sub, wt, acc); break;
-    case 3: accum_channel<3, G, CONTIG>(planes, wb0, wbs, coff, sub, wt, acc); break;
-    case 4: accum_channel<4, G, CONTIG>(planes, wb0, wbs, coff, sub, wt, acc); break;
-    default: break;
+template <int C, int G>
+__device__ __forceinline__ void direct_class(const ScanArgs &a, const QShared<G> &qs, int64_t bh, const uint64_t *pw,
+                                             const uint16_t *ps, float (&acc)[kGB][G]) {
+  if (C > a.ncls) return;
+  const int nc = min(max(ld_uniform(a.clsn + bh * a.bmax + C - 1), 0), a.D);
+  const int32_t *lst = a.cls + (bh * a.bmax + C - 1) * a.D;
+  int jn = nc > 0 ? ld_uniform(lst) : 0;
+  for (int i = 0; i < nc; ++i) {
+    const int j = jn;
+    if (i + 1 < nc) jn = ld_uniform(lst + i + 1);
+    if ((unsigned)j >= (unsigned)a.D) continue;
+    float qv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) qv[g] = qs.qw[j * G + g];
+    direct_channel<C, G>(pw + (int64_t)j * 4 * a.sub, ps + (int64_t)j * a.sub, a.sub, qv, acc);
   }
 }
 
 template <int G, int MODE>
-__global__ __launch_bounds__(256) void scan_direct_kernel(
-    const float *__restrict__ q, int D, const int8_t *__restrict__ tpl, const int32_t *__restrict__ act,
-    const int32_t *__restrict__ nact_p, const uint64_t *__restrict__ planes, const uint16_t *__restrict__ scales,
-    int64_t n, int64_t nsb, int64_t sub, int64_t blk0, int64_t blk_end, int64_t tile_stride, Emit em) {
-  __shared__ ScanShared<G> sh;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+__global__ __launch_bounds__(256) void scan_direct_kernel(ScanArgs a, Emit em) {
+  __shared__ QShared<G> qs;
+  __shared__ EmitShared<G> es;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t bh = blockIdx.y;
-  const int64_t tb0 = blk0 + (int64_t)blockIdx.x * tile_stride * kTB;
-  // Plan entries come from device memory: a channel outside [0, D) or a depth
-  // <= 0 contributes nothing, depths above the store's 4 planes read 4.
-  const int nact = min(max(nact_p[bh], 0), D);
-
-  for (int i = tid; i < G * D; i += 256) sh.q[i] = q[bh * G * D + i];
-  // word offsets of the tile's blocks (-1 past the scanned range)
-  __shared__ int64_t wbs[kTB];
-  if (tid < kTB) {
-    const int64_t b = tb0 + tid;
-    wbs[tid] = b < blk_end ? word_base(bh, b, nsb, sub, D) : -1;
-  }
+  const int64_t tile = a.tile0 + (int64_t)blockIdx.x * a.tile_stride;
+  const int64_t gb0 = tile * kTB + wave * kGB;  // first block of this wave's group
+  const uint32_t pf = load_qw<G>(qs, a, bh, tile * kTB, true);
   __syncthreads();
-  const int64_t *wbw = &wbs[wave * kBPW];
-  const int64_t wb0 = sgpr64(wbw[0]);
-  const bool contig = wb0 >= 0 && sgpr64(wbw[kBPW - 1]) == wb0 + (kBPW - 1);
-  float acc[kBPW][G];
+  float acc[kGB][G];
 #pragma unroll
-  for (int r = 0; r < kBPW; ++r)
+  for (int r = 0; r < kGB; ++r)
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[r][g] = 0.0f;
-  float cst_acc = 0.0f;
-
-  for (int a0 = 0; a0 < nact; a0 += kCH) {
-    const int na = min(kCH, nact - a0);
-    __syncthreads();  // LDS of the previous chunk is consumed
-    // L2 prefetch: one dword per (channel, plane, half tile) pulls the chunk's
-    // 128-byte plane lines into L2 while the prologue runs, so the scalar
-    // loads below hit L2 instead of waiting on HBM one channel at a time.
-    uint32_t pf = 0u;
-    {
-      const int a = tid >> 3, p = (tid >> 1) & 3, hb = (tid & 1) * (kTB / 2);
-      if (a < na) {
-        const int j = act[bh * D + a0 + a];
-        if (j >= 0 && j < D && p < (int)tpl[bh * D + j]) {
-          const int64_t b = tb0 + hb;
-          if (b < blk_end)
-            pf = *reinterpret_cast<const uint32_t *>(planes + word_base(bh, b, nsb, sub, D) + ((int64_t)j * 4 + p) * sub);
-        }
-      }
-    }
-    chunk_prepare<G>(sh, tpl, act, scales, bh, tb0, blk_end, nsb, sub, D, a0, na, cst_acc);
-    for (int a = 0; a < na; ++a) {
-      // readfirstlane: the compiler cannot prove the loop index wave-uniform
-      // across the barriers above; channel and depth stay in SGPRs
-      const int ai = __builtin_amdgcn_readfirstlane(a0 + a);
-      const int j0 = __builtin_amdgcn_readfirstlane(ld_uniform(act + bh * D + ai));
-      const bool ok = j0 >= 0 && j0 < D;
-      const int j = ok ? j0 : 0;
-      const int c = __builtin_amdgcn_readfirstlane(ok ? min(max((int)ld_uniform(tpl + bh * D + j), 0), 4) : 0);
-      const int64_t coff = (int64_t)j * 4 * sub;
-      const float *wt = &sh.wt[(a * kTB + wave * kBPW) * G];
-      if (contig)
-        accum_switch<G, true>(c, planes, wb0, wbw, coff, sub, wt, acc);
-      else
-        accum_switch<G, false>(c, planes, wb0, wbw, coff, sub, wt, acc);
-    }
-    asm volatile("" ::"v"(pf));  // the prefetched dword is retired here, after the chunk's work
+  // groups outside the emitted range or past the store are not read
+  if (gb0 < a.blk_end && gb0 + kGB > a.blk0 && gb0 < a.nsb * a.sub) {
+    const int64_t sb = sgpr64(gb0 / a.sub);
+    const int64_t off = gb0 - sb * a.sub;
+    const uint64_t *pw = a.planes + (bh * a.nsb + sb) * a.D * 4 * a.sub + off;
+    const uint16_t *ps = a.scales + (bh * a.nsb + sb) * a.D * a.sub + off;
+    direct_class<1, G>(a, qs, bh, pw, ps, acc);
+    direct_class<2, G>(a, qs, bh, pw, ps, acc);
+    direct_class<3, G>(a, qs, bh, pw, ps, acc);
+    direct_class<4, G>(a, qs, bh, pw, ps, acc);
   }
-  __syncthreads();
-  emit_tile<G, MODE>(em, sh, acc, cst_acc, bh, tb0, blk_end, n, wave, lane, blockIdx.x);
+  asm volatile("" ::"v"(pf));  // the prefetch loads retire here
+  emit_group<G, MODE>(em, es, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
 }
 
-// --------------------------------------------------------------------- staged (host-resident) kernel
+// --------------------------------------------------------------------- staged kernel
 template <int G>
 struct StagedShared {
-  ScanShared<G> s;
-  uint64_t w[kCH * 4 * kTB];  // [channel][plane][block]
+  uint64_t w[kCH * 4 * kTB];   // [channel][plane][block]
+  uint16_t s[kCH * kTB];       // [channel][block]
+  int ch[kCH];
 };
 
-template <int G, int MODE>
-__global__ __launch_bounds__(256) void scan_staged_kernel(
-    const float *__restrict__ q, int D, const int8_t *__restrict__ tpl, const int32_t *__restrict__ act,
-    const int32_t *__restrict__ nact_p, const uint64_t *__restrict__ planes, const uint16_t *__restrict__ scales,
-    int64_t n, int64_t nsb, int64_t sub, int64_t blk0, int64_t blk_end, int64_t tile_stride, Emit em) {
-  __shared__ StagedShared<G> st;
-  ScanShared<G> &sh = st.s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t bh = blockIdx.y;
-  const int64_t tb0 = blk0 + (int64_t)blockIdx.x * tile_stride * kTB;
-  const int nact = min(max(nact_p[bh], 0), D);
-
-  for (int i = tid; i < G * D; i += 256) sh.q[i] = q[bh * G * D + i];
-  float acc[kBPW][G];
-#pragma unroll
-  for (int r = 0; r < kBPW; ++r)
-#pragma unroll
-    for (int g = 0; g < G; ++g) acc[r][g] = 0.0f;
-  float cst_acc = 0.0f;
-
-  for (int a0 = 0; a0 < nact; a0 += kCH) {
-    const int na = min(kCH, nact - a0);
-    __syncthreads();
-    chunk_prepare<G>(sh, tpl, act, scales, bh, tb0, blk_end, nsb, sub, D, a0, na, cst_acc);
-    // stage the tile's plane words of the chunk: consecutive threads read
-    // consecutive blocks of one (channel, plane), i.e. contiguous 8-byte words
-    for (int idx = tid; idx < na * 4 * kTB; idx += 256) {
-      const int bi = idx % kTB, p = (idx / kTB) % 4, a = idx / (4 * kTB);
-      if (p < sh.dep[a]) {
-        const int64_t b = tb0 + bi;
-        st.w[idx] = (b < blk_end) ? planes[word_base(bh, b, nsb, sub, D) + ((int64_t)sh.ch[a] * 4 + p) * sub] : 0ull;
-      }
+template <int C, int G>
+__device__ __forceinline__ void staged_class(const ScanArgs &a, const QShared<G> &qs, StagedShared<G> &st, int64_t bh,
+                                             int64_t tb0, int wave, int lane, float (&acc)[kGB][G]) {
+  if (C > a.ncls) return;
+  const int tid = threadIdx.x;
+  const int nc = min(max(a.clsn[bh * a.bmax + C - 1], 0), a.D);
+  const int32_t *lst = a.cls + (bh * a.bmax + C - 1) * a.D;
+  const int64_t nblk_store = a.nsb * a.sub;
+  for (int c0 = 0; c0 < nc; c0 += kCH) {
+    const int na = min(kCH, nc - c0);
+    __syncthreads();  // the previous chunk is consumed
+    if (tid < na) {
+      const int j = lst[c0 + tid];
+      st.ch[tid] = (j >= 0 && j < a.D) ? j : -1;
     }
     __syncthreads();
-    for (int a = 0; a < na; ++a) {
-      const int c = sh.dep[a];
-      const uint64_t *wa = &st.w[a * 4 * kTB];
+    // consecutive threads read consecutive blocks of one (channel, plane):
+    // contiguous words within each superblock
+    for (int idx = tid; idx < na * C * kTB; idx += 256) {
+      const int bi = idx % kTB, p = (idx / kTB) % C, ci = idx / (C * kTB);
+      const int j = st.ch[ci];
+      const int64_t b = tb0 + bi;
+      uint64_t v = 0ull;
+      if (j >= 0 && b < nblk_store) {
+        const int64_t sb = b / a.sub;
+        v = a.planes[((bh * a.nsb + sb) * a.D + j) * 4 * a.sub + p * a.sub + (b - sb * a.sub)];
+      }
+      st.w[(ci * 4 + p) * kTB + bi] = v;
+    }
+    for (int idx = tid; idx < na * kTB; idx += 256) {
+      const int bi = idx % kTB, ci = idx / kTB;
+      const int j = st.ch[ci];
+      const int64_t b = tb0 + bi;
+      uint16_t v = 0;
+      if (j >= 0 && b < nblk_store) {
+        const int64_t sb = b / a.sub;
+        v = a.scales[((bh * a.nsb + sb) * a.D + j) * a.sub + (b - sb * a.sub)];
+      }
+      st.s[ci * kTB + bi] = v;
+    }
+    __syncthreads();
+    for (int ci = 0; ci < na; ++ci) {
+      const int j = st.ch[ci];
+      if (j < 0) continue;
+      float qv[G];
 #pragma unroll
-      for (int r = 0; r < kBPW; ++r) {
-        const int bi = wave * kBPW + r;
+      for (int g = 0; g < G; ++g) qv[g] = qs.qw[j * G + g];
+#pragma unroll
+      for (int r = 0; r < kGB; ++r) {
+        const int bi = wave * kGB + r;
         uint32_t code = 0;
-        for (int p = 0; p < c; ++p) code = (code << 1) | (uint32_t)((wa[p * kTB + bi] >> lane) & 1ull);
-        // same encoding as the direct kernel: depth-4 codes enter as code/2
-        const float cf = (c >= 4) ? 0.5f * (float)code : (float)code;
-        const float *wt = &sh.wt[(a * kTB + bi) * G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) acc[r][g] = fmaf(wt[g], cf, acc[r][g]);
+        for (int p = 0; p < C; ++p) code = (code << 1) | (uint32_t)((st.w[(ci * 4 + p) * kTB + bi] >> lane) & 1ull);
+        const float u = scaled(st.s[ci * kTB + bi], sym_from_int<C>(code));
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[r][g] = fmaf(qv[g], u, acc[r][g]);
       }
     }
   }
-  __syncthreads();
-  emit_tile<G, MODE>(em, sh, acc, cst_acc, bh, tb0, blk_end, n, wave, lane, blockIdx.x);
 }
 
-struct ScanCall {
-  const float *q;
-  int64_t BH, G;
-  int D;
-  const int8_t *t;
-  const int32_t *act, *nact;
-  const uint64_t *planes;
-  const uint16_t *scales;
-  int64_t n, nsb, sub, blk0, blk_end;
-  bool host_store;
-};
-
-// The sampling pass runs few workgroups, too few to hide the direct kernel's
-// per-channel scalar-load latency: it takes the staged kernel, which issues a
-// chunk's loads together (same scores bit for bit).
 template <int G, int MODE>
-void launch_g(const ScanCall &c, int64_t tiles, int64_t stride, const Emit &em, hipStream_t st) {
-  dim3 grid((unsigned)tiles, (unsigned)c.BH);
-  if (c.host_store || MODE == kEmitSample)
-    scan_staged_kernel<G, MODE><<<grid, 256, 0, st>>>(c.q, c.D, c.t, c.act, c.nact, c.planes, c.scales, c.n, c.nsb,
-                                                      c.sub, c.blk0, c.blk_end, stride, em);
+__global__ __launch_bounds__(256) void scan_staged_kernel(ScanArgs a, Emit em) {
+  __shared__ QShared<G> qs;
+  __shared__ StagedShared<G> st;
+  __shared__ EmitShared<G> es;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t bh = blockIdx.y;
+  const int64_t tile = a.tile0 + (int64_t)blockIdx.x * a.tile_stride;
+  const int64_t tb0 = tile * kTB;
+  load_qw<G>(qs, a, bh, tb0, false);
+  __syncthreads();
+  float acc[kGB][G];
+#pragma unroll
+  for (int r = 0; r < kGB; ++r)
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[r][g] = 0.0f;
+  // the whole workgroup takes part in staging, so the range test is per tile
+  if (tb0 < a.blk_end && tb0 + kTB > a.blk0) {
+    staged_class<1, G>(a, qs, st, bh, tb0, wave, lane, acc);
+    staged_class<2, G>(a, qs, st, bh, tb0, wave, lane, acc);
+    staged_class<3, G>(a, qs, st, bh, tb0, wave, lane, acc);
+    staged_class<4, G>(a, qs, st, bh, tb0, wave, lane, acc);
+  }
+  emit_group<G, MODE>(em, es, acc, bh, tb0 + wave * kGB, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
+}
+
+// --------------------------------------------------------------------- launch
+template <int G, int MODE>
+void launch_g(const ScanArgs &a, int64_t tiles, int64_t BH, bool staged, const Emit &em, hipStream_t st) {
+  dim3 grid((unsigned)tiles, (unsigned)BH);
+  if (staged)
+    scan_staged_kernel<G, MODE><<<grid, 256, 0, st>>>(a, em);
   else
-    scan_direct_kernel<G, MODE><<<grid, 256, 0, st>>>(c.q, c.D, c.t, c.act, c.nact, c.planes, c.scales, c.n, c.nsb,
-                                                      c.sub, c.blk0, c.blk_end, stride, em);
+    scan_direct_kernel<G, MODE><<<grid, 256, 0, st>>>(a, em);
 }
 
 template <int MODE>
-int launch_scan(const ScanCall &c, int64_t tiles, int64_t stride, const Emit &em, hipStream_t st) {
+int launch_scan(const ScanArgs &a, int64_t G, int64_t tiles, int64_t BH, bool staged, const Emit &em,
+                hipStream_t st) {
   if (tiles <= 0) return FATHOM_OK;
-  switch (c.G) {
-    case 1: launch_g<1, MODE>(c, tiles, stride, em, st); break;
-    case 2: launch_g<2, MODE>(c, tiles, stride, em, st); break;
-    case 3: launch_g<3, MODE>(c, tiles, stride, em, st); break;
-    case 4: launch_g<4, MODE>(c, tiles, stride, em, st); break;
-    case 5: launch_g<5, MODE>(c, tiles, stride, em, st); break;
-    case 6: launch_g<6, MODE>(c, tiles, stride, em, st); break;
-    case 7: launch_g<7, MODE>(c, tiles, stride, em, st); break;
-    default: launch_g<8, MODE>(c, tiles, stride, em, st); break;
+  switch (G) {
+    case 1: launch_g<1, MODE>(a, tiles, BH, staged, em, st); break;
+    case 2: launch_g<2, MODE>(a, tiles, BH, staged, em, st); break;
+    case 3: launch_g<3, MODE>(a, tiles, BH, staged, em, st); break;
+    case 4: launch_g<4, MODE>(a, tiles, BH, staged, em, st); break;
+    case 5: launch_g<5, MODE>(a, tiles, BH, staged, em, st); break;
+    case 6: launch_g<6, MODE>(a, tiles, BH, staged, em, st); break;
+    case 7: launch_g<7, MODE>(a, tiles, BH, staged, em, st); break;
+    default: launch_g<8, MODE>(a, tiles, BH, staged, em, st); break;
   }
-  return launch_status((c.host_store || MODE == kEmitSample) ? "scan_staged_kernel" : "scan_direct_kernel");
+  return launch_status(staged ? "scan_staged_kernel" : "scan_direct_kernel");
 }
 
-// Stores in pinned host memory take the staged kernel (whole-run PCIe reads);
-// device memory takes the direct kernel.
-bool is_host_memory(const void *p) {
+// Stores in pinned host memory take the staged kernel (whole-run PCIe reads),
+// as do superblock sizes that do not hold whole 8-block groups.
+bool use_staged(const void *planes, int64_t sub) {
+  if (sub % kGB != 0) return true;
   hipPointerAttribute_t attr;
-  hipError_t e = hipPointerGetAttributes(&attr, p);
+  hipError_t e = hipPointerGetAttributes(&attr, planes);
   if (e != hipSuccess) {
     (void)hipGetLastError();
     return true;
@@ -447,18 +459,37 @@ bool is_host_memory(const void *p) {
   return attr.type == hipMemoryTypeHost;
 }
 
-int check_scan(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t, const int32_t *act,
-               const int32_t *nact, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
-               const char *who) {
-  if (!q || !t || !act || !nact || !planes_sb || !scales_sb) return fail(FATHOM_ERR_INVALID, "%s: null pointer", who);
+int check_scan(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
+               const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, const char *who) {
+  if (!q || !cls || !clsn || !planes_sb || !scales_sb) return fail(FATHOM_ERR_INVALID, "%s: null pointer", who);
   if (BH < 1 || BH > 65535) return fail(FATHOM_ERR_INVALID, "%s: BH=%lld outside [1, 65535]", who, (long long)BH);
   if (G < 1 || G > 8) return fail(FATHOM_ERR_INVALID, "%s: G=%lld outside [1, 8]", who, (long long)G);
   if (D < 1 || D > kMaxD) return fail(FATHOM_ERR_INVALID, "%s: D=%lld outside [1, %d]", who, (long long)D, kMaxD);
-  if (n < 1 || sub < 1) return fail(FATHOM_ERR_INVALID, "%s: n=%lld sub=%lld", who, (long long)n, (long long)sub);
-  if (nsb * sub < cdiv(n, kBlk))
+  if (bmax < 1 || bmax > 8) return fail(FATHOM_ERR_INVALID, "%s: bmax=%d outside [1, 8]", who, bmax);
+  if (n < 1 || n > (1LL << 31) || sub < 1)
+    return fail(FATHOM_ERR_INVALID, "%s: n=%lld sub=%lld unsupported", who, (long long)n, (long long)sub);
+  if (nsb < 1 || nsb * sub < cdiv(n, kBlk))
     return fail(FATHOM_ERR_INVALID, "%s: store holds %lld blocks (nsb=%lld x sub=%lld), n needs %lld", who,
                 (long long)(nsb * sub), (long long)nsb, (long long)sub, (long long)cdiv(n, kBlk));
   return FATHOM_OK;
+}
+
+ScanArgs make_args(const float *q, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax, const void *planes_sb,
+                   const void *scales_sb, int64_t n, int64_t nsb, int64_t sub) {
+  ScanArgs a{};
+  a.q = q;
+  a.cls = cls;
+  a.clsn = clsn;
+  a.planes = static_cast<const uint64_t *>(planes_sb);
+  a.scales = static_cast<const uint16_t *>(scales_sb);
+  a.n = n;
+  a.nsb = nsb;
+  a.sub = sub;
+  a.D = (int)D;
+  a.bmax = bmax;
+  a.ncls = bmax < 4 ? bmax : 4;
+  a.tile_stride = 1;
+  return a;
 }
 
 }  // namespace
@@ -466,11 +497,11 @@ int check_scan(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t
 
 using namespace fathom;
 
-extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t,
-                                  const int32_t *act, const int32_t *nact, const void *planes_sb,
-                                  const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t blk0,
-                                  int64_t blk1, float *out, void *stream) {
-  int rc = check_scan(q, BH, G, D, t, act, nact, planes_sb, scales_sb, n, nsb, sub, "scan_planes");
+extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
+                                  const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
+                                  int64_t n, int64_t nsb, int64_t sub, int64_t blk0, int64_t blk1, float *out,
+                                  void *stream) {
+  int rc = check_scan(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, "scan_planes");
   if (rc) return rc;
   if (!out) return fail(FATHOM_ERR_INVALID, "scan_planes: null output");
   if (blk0 < 0 || blk1 < blk0)
@@ -478,13 +509,14 @@ extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t
   const int64_t nblk = cdiv(n, kBlk);
   const int64_t blk_end = blk1 < nblk ? blk1 : nblk;
   if (blk_end <= blk0) return FATHOM_OK;
-  const int64_t tiles = cdiv(blk_end - blk0, kTB);
-  if (tiles > 0x7FFFFFFF) return fail(FATHOM_ERR_INVALID, "scan_planes: too many tiles");
-  ScanCall c{q, BH, G, (int)D, t, act, nact, static_cast<const uint64_t *>(planes_sb),
-             static_cast<const uint16_t *>(scales_sb), n, nsb, sub, blk0, blk_end, is_host_memory(planes_sb)};
+  ScanArgs a = make_args(q, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub);
+  a.blk0 = blk0;
+  a.blk_end = blk_end;
+  a.tile0 = blk0 / kTB;
+  const int64_t tiles = cdiv(blk_end, kTB) - a.tile0;
   Emit em{};
   em.out = out;
-  return launch_scan<kEmitScores>(c, tiles, 1, em, (hipStream_t)stream);
+  return launch_scan<kEmitScores>(a, G, tiles, BH, use_staged(planes_sb, sub), em, (hipStream_t)stream);
 }
 
 extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink,
@@ -494,11 +526,11 @@ extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_
   return topk_layout(BH * G, n, k, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
 
-extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t, const int32_t *act,
-                                const int32_t *nact, const void *planes_sb, const void *scales_sb, int64_t n,
-                                int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
-                                int64_t *idx, void *workspace, size_t workspace_bytes, void *stream) {
-  int rc = check_scan(q, BH, G, D, t, act, nact, planes_sb, scales_sb, n, nsb, sub, "scan_topk");
+extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
+                                const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
+                                int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink,
+                                int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_scan(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, "scan_topk");
   if (rc) return rc;
   if (!idx) return fail(FATHOM_ERR_INVALID, "scan_topk: null output");
   const int64_t rows = BH * G;
@@ -516,14 +548,18 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   em.sink = sink;
   em.lstart = (m - local) > 0 ? (m - local) : 0;
   const int64_t nblk = cdiv(n, kBlk);
-  const int64_t tiles = cdiv(nblk, kTB);
-  ScanCall c{q, BH, G, (int)D, t, act, nact, static_cast<const uint64_t *>(planes_sb),
-             static_cast<const uint16_t *>(scales_sb), n, nsb, sub, 0, nblk, is_host_memory(planes_sb)};
-  rc = launch_scan<kEmitSample>(c, topk_sample_tiles(n, S), S, em, st);
+  const bool staged = use_staged(planes_sb, sub);
+  ScanArgs a = make_args(q, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub);
+  a.blk0 = 0;
+  a.blk_end = nblk;
+  a.tile0 = 0;
+  a.tile_stride = S;
+  rc = launch_scan<kEmitSample>(a, G, topk_sample_tiles(n, S), BH, staged, em, st);
   if (rc) return rc;
   rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, em.sel, st);
   if (rc) return rc;
-  rc = launch_scan<kEmitFilter>(c, tiles, 1, em, st);
+  a.tile_stride = 1;
+  rc = launch_scan<kEmitFilter>(a, G, cdiv(nblk, kTB), BH, staged, em, st);
   if (rc) return rc;
   return launch_finalize(rows, m, k, sink, local, em.sel, idx, st);
 }

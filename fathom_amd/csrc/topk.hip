@@ -6,11 +6,14 @@
 // The selection runs select -> filter -> finalize (topk_internal.hpp); the
 // fused scan+top-k path replaces `filter` by the scan kernel's own emission.
 //
-// Radix rounds (8-bit digits, most significant first) build LDS histograms
-// with wave-aggregated updates -- the leader lane of each distinct digit in a
-// wave adds the popcount of its ballot -- so the few hot exponent buckets of a
-// score row cost one atomic per wave and digit.  A round ends the search as
-// soon as the chosen bucket holds exactly the elements still needed.
+// Selection of the need-th largest value of a set (range_select): the active
+// values lie in [lo, hi]; a 2048-bin LDS histogram of (v - lo) >> s, with s
+// chosen so the bins span exactly that range, locates the bin holding the
+// need-th largest; the range shrinks to that bin (by >= 11 bits) and the
+// search repeats until the bin holds exactly the values still needed.  Bins
+// follow the values' actual spread, so a row's candidates -- all packed just
+// above a threshold -- still spread over many bins (few atomic collisions),
+// and a 64-bit K64 needs at most six rounds.
 #include "topk_internal.hpp"
 
 namespace fathom {
@@ -24,100 +27,128 @@ constexpr int64_t kFilterChunk = 16384;
 constexpr uint32_t kFilterLocal = 2048;  // LDS candidates per filter workgroup
 constexpr int kCandLds = 16384;          // candidates selected in LDS (128 KB)
 constexpr int kMaxK = 2048;              // largest kk
+constexpr int kBins = 2048;
+constexpr int kMaxWaves = 16;            // waves of a 1024-thread workgroup
 
-__device__ __forceinline__ void wave_hist_add(uint32_t *hist, uint32_t dg, bool act, int lane) {
-  uint64_t rem = __ballot(act);
-  while (rem) {
-    const int leader = __ffsll((unsigned long long)rem) - 1;
-    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)dg, leader);
-    const uint64_t m = __ballot(act && dg == d) & rem;
-    if (lane == leader) atomicAdd(&hist[d], (uint32_t)__popcll(m));
-    rem &= ~m;
-  }
-}
-
-template <typename K>
-struct SelShared {
-  uint32_t hist[256];
-  K prefix;
-  uint32_t need;
-  uint32_t done;
+struct RangeShared {
+  uint32_t hist[kBins];
+  uint64_t wmin[kMaxWaves], wmax[kMaxWaves];
+  uint32_t wsum[kMaxWaves];
+  uint64_t lo, hi, thr;
+  uint32_t need, done;
 };
 
-template <typename K>
-__device__ __forceinline__ void sel_begin(SelShared<K> &sh, uint32_t need) {
-  if (threadIdx.x == 0) {
-    sh.prefix = 0;
-    sh.need = need;
-    sh.done = 0u;
-  }
-  for (int d = threadIdx.x; d < 256; d += blockDim.x) sh.hist[d] = 0u;
-  __syncthreads();
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, o, kWave);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, kWave);
+  return ((uint64_t)hi << 32) | lo;
 }
 
-// After the histogram of a round: wave 0 picks the digit holding the need-th
-// largest element, then the histogram is cleared for the next round.
-template <typename K>
-__device__ __forceinline__ void sel_pick(SelShared<K> &sh, int shift) {
-  const int tid = threadIdx.x;
-  __syncthreads();
-  if (tid < 64) {
-    uint32_t h[4];
-    uint32_t s = 0;
+// Smallest value >= lo of the need-th largest element among cnt values read
+// through get(i) (all threads of the workgroup call it).  Returns thr with
+// #{v >= thr} >= need, equality when the values are distinct; thr = 0 when
+// there are fewer than need values.
+template <typename Get>
+__device__ uint64_t range_select(Get get, int64_t cnt, uint32_t need, RangeShared &sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  if (cnt < (int64_t)need || need == 0) return 0ull;
+  // value range
+  uint64_t mn = ~0ull, mx = 0ull;
+  for (int64_t i = tid; i < cnt; i += blockDim.x) {
+    const uint64_t v = get(i);
+    mn = v < mn ? v : mn;
+    mx = v > mx ? v : mx;
+  }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      h[u] = sh.hist[4 * tid + u];
-      s += h[u];
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t a = shfl_xor_u64(mn, o), b = shfl_xor_u64(mx, o);
+    mn = a < mn ? a : mn;
+    mx = b > mx ? b : mx;
+  }
+  if (lane == 0) {
+    sh.wmin[wave] = mn;
+    sh.wmax[wave] = mx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t a = ~0ull, b = 0ull;
+    for (int w = 0; w < nw; ++w) {
+      a = sh.wmin[w] < a ? sh.wmin[w] : a;
+      b = sh.wmax[w] > b ? sh.wmax[w] : b;
     }
-    uint32_t incl = s;  // inclusive suffix sum over lanes (digits above)
+    sh.lo = a;
+    sh.hi = b;
+    sh.need = need;
+    sh.done = 0u;
+    sh.thr = a;
+  }
+  __syncthreads();
+  for (;;) {
+    const uint64_t lo = sh.lo, hi = sh.hi;
+    const uint32_t nd = sh.need;
+    const uint64_t R = hi - lo;
+    const int bl = R ? 64 - __clzll((long long)R) : 0;
+    const int s = bl > 11 ? bl - 11 : 0;
+    const int nb = (int)(R >> s) + 1;
+    for (int b = tid; b < nb; b += blockDim.x) sh.hist[b] = 0u;
+    __syncthreads();
+    for (int64_t i = tid; i < cnt; i += blockDim.x) {
+      const uint64_t v = get(i);
+      if (v >= lo && v <= hi) atomicAdd(&sh.hist[(v - lo) >> s], 1u);
+    }
+    __syncthreads();
+    // inclusive suffix sums over the bins (thread t owns bins 2t, 2t + 1)
+    const int b0 = 2 * tid;
+    const uint32_t h0 = b0 < nb ? sh.hist[b0] : 0u, h1 = b0 + 1 < nb ? sh.hist[b0 + 1] : 0u;
+    const uint32_t x = h0 + h1;
+    uint32_t incl = x;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const uint32_t v = __shfl_down(incl, o, kWave);
-      if (tid + o < 64) incl += v;
+      if (lane + o < 64) incl += v;
     }
-    uint32_t above = incl - s;
-    const uint32_t nd = sh.need;
-    const K pre = sh.prefix;
-#pragma unroll
-    for (int u = 3; u >= 0; --u) {
-      if (above < nd && above + h[u] >= nd) {
-        sh.prefix = pre | ((K)(4 * tid + u) << shift);
-        sh.need = nd - above;
-        if (h[u] == nd - above) sh.done = 1u;
-      }
-      above += h[u];
+    if (lane == 0) sh.wsum[wave] = incl;
+    __syncthreads();
+    uint32_t later = 0u;
+    for (int w = wave + 1; w < nw; ++w) later += sh.wsum[w];
+    const uint32_t above = incl - x + later;  // values in bins above b0 + 1
+    int bsel = -1;
+    uint32_t nsel = 0u, hsel = 0u;
+    if (above < nd && above + h1 >= nd) {
+      bsel = b0 + 1;
+      nsel = nd - above;
+      hsel = h1;
+    } else if (above + h1 < nd && above + h1 + h0 >= nd) {
+      bsel = b0;
+      nsel = nd - above - h1;
+      hsel = h0;
     }
-  }
-  __syncthreads();
-  for (int d = tid; d < 256; d += blockDim.x) sh.hist[d] = 0u;
-  __syncthreads();
-}
-
-// Exact need-th largest of the values held M per thread (count = M * blockDim
-// values, all taking part): radix rounds over registers.
-template <int M>
-__device__ uint32_t select_small(const uint32_t (&v)[M], uint32_t need, SelShared<uint32_t> &sh) {
-  const int lane = threadIdx.x & 63;
-  sel_begin(sh, need);
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    const uint32_t pre = sh.prefix;
-    const uint32_t hmask = shift == 24 ? 0u : (0xFFFFFFFFu << (shift + 8));
-#pragma unroll
-    for (int u = 0; u < M; ++u) wave_hist_add(sh.hist, (v[u] >> shift) & 255u, (v[u] & hmask) == (pre & hmask), lane);
-    sel_pick(sh, shift);
+    __syncthreads();  // every thread has read lo/hi/need
+    if (bsel >= 0) {
+      const uint64_t nlo = lo + ((uint64_t)bsel << s);
+      const uint64_t width = s ? (((uint64_t)1 << s) - 1ull) : 0ull;
+      sh.lo = nlo;
+      sh.hi = (hi - nlo) > width ? nlo + width : hi;
+      sh.need = nsel;
+      sh.thr = nlo;
+      sh.done = (hsel == nsel || s == 0) ? 1u : 0u;
+    }
+    __syncthreads();
     if (sh.done) break;
   }
-  return sh.prefix;
+  return sh.thr;
 }
 
-// Lower bound T on the need-th largest of the kSelPer keys per thread (zeros
-// for slots past the sample): each thread keeps its M largest keys and T is the
-// need-th largest of those M * blockDim values.  Those are need distinct
-// sample elements >= T, so T <= the sample's need-th largest <= the row's.
-// With M * blockDim >= 2 need, T lands near the sample's (1-2) * need-th
-// largest, at a fraction of the cost of an exact selection over the sample.
+__device__ __forceinline__ uint32_t masked_key(const float *row, int64_t i, int64_t sink, int64_t lstart) {
+  return (i < sink || i >= lstart) ? kKeyNegInf : score_key(row[i]);
+}
+
+// Threshold of a row from its sampled keys: each thread keeps its M largest
+// keys and T is the kk-th largest of those M * 1024 values.  They are kk
+// elements of the sample >= T, so T <= the sample's kk-th largest <= the row's:
+// every element of the row's top kk has key >= T.
 template <int M>
-__device__ uint32_t select_bound(const uint32_t (&v)[kSelPer], uint32_t need, SelShared<uint32_t> &sh) {
+__device__ uint32_t sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint64_t *vals, RangeShared &sh) {
   uint32_t top[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) top[i] = 0u;
@@ -131,16 +162,17 @@ __device__ uint32_t select_bound(const uint32_t (&v)[kSelPer], uint32_t need, Se
       top[i] = hi;
     }
   }
-  return select_small<M>(top, need, sh);
-}
-
-__device__ __forceinline__ uint32_t masked_key(const float *row, int64_t i, int64_t sink, int64_t lstart) {
-  return (i < sink || i >= lstart) ? kKeyNegInf : score_key(row[i]);
+#pragma unroll
+  for (int i = 0; i < M; ++i) vals[threadIdx.x * M + i] = (uint64_t)top[i] << 32;
+  __syncthreads();
+  const uint64_t t = range_select([&](int64_t i) { return vals[i]; }, (int64_t)M * kSelThreads, kk, sh);
+  return (uint32_t)(t >> 32);
 }
 
 __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t *__restrict__ samp,
                                                                   int64_t samp_cap, uint32_t kk, TopkSel s) {
-  __shared__ SelShared<uint32_t> sh;
+  __shared__ RangeShared sh;
+  __shared__ uint64_t vals[4 * kSelThreads];
   const int64_t row = blockIdx.x;
   const uint32_t *src = samp + row * samp_cap;
   uint32_t v[kSelPer];
@@ -152,11 +184,11 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
   uint32_t thr = 0u;  // fewer samples than kk: every element is a candidate
   if (samp_cap >= (int64_t)kk) {
     if (2 * kk <= kSelThreads)
-      thr = select_bound<1>(v, kk, sh);
+      thr = sample_bound<1>(v, kk, vals, sh);
     else if (kk <= kSelThreads)
-      thr = select_bound<2>(v, kk, sh);
+      thr = sample_bound<2>(v, kk, vals, sh);
     else
-      thr = select_bound<4>(v, kk, sh);
+      thr = sample_bound<4>(v, kk, vals, sh);
   }
   if (threadIdx.x == 0) {
     s.thr[row] = thr;
@@ -177,6 +209,9 @@ __global__ __launch_bounds__(256) void sample_scores_kernel(const float *__restr
   }
 }
 
+// Candidates of score rows (keys >= the row's threshold), 4 scores per thread
+// and step when rows are 16-byte aligned.
+template <bool VEC>
 __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const float *__restrict__ scores, int64_t n,
                                                                        int64_t sink, int64_t lstart, TopkSel s) {
   __shared__ uint64_t lbuf[kFilterLocal];
@@ -190,47 +225,42 @@ __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const flo
   __syncthreads();
   const int64_t start = (int64_t)blockIdx.x * kFilterChunk;
   const int64_t end = min(start + kFilterChunk, n);
-  for (int64_t i0 = start; i0 < end; i0 += kFilterThreads) {
-    const int64_t i = i0 + tid;
-    const bool in = i < end;
-    const uint32_t key = in ? masked_key(rs, i, sink, lstart) : 0u;
-    wave_append_local(in && key >= thr, k64_of(key, i), &lcnt, lbuf, kFilterLocal, &s.cand_cnt[row], cand,
-                      (uint64_t)s.cand_cap, lane);
+  if (VEC) {
+    for (int64_t i0 = start; i0 < end; i0 += 4 * kFilterThreads) {
+      const int64_t i = i0 + 4 * tid;
+      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < end) f = *reinterpret_cast<const float4 *>(rs + i);
+      const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t iu = i + u;
+        const bool in = iu < end;
+        const uint32_t key = in ? ((iu < sink || iu >= lstart) ? kKeyNegInf : score_key(fv[u])) : 0u;
+        wave_append_local(in && key >= thr, k64_of(key, iu), &lcnt, lbuf, kFilterLocal, &s.cand_cnt[row], cand,
+                          (uint64_t)s.cand_cap, lane);
+      }
+    }
+  } else {
+    for (int64_t i0 = start; i0 < end; i0 += kFilterThreads) {
+      const int64_t i = i0 + tid;
+      const bool in = i < end;
+      const uint32_t key = in ? masked_key(rs, i, sink, lstart) : 0u;
+      wave_append_local(in && key >= thr, k64_of(key, i), &lcnt, lbuf, kFilterLocal, &s.cand_cnt[row], cand,
+                        (uint64_t)s.cand_cap, lane);
+    }
   }
   __syncthreads();
   flush_local(&lcnt, lbuf, kFilterLocal, &s.cand_cnt[row], cand, (uint64_t)s.cand_cap, &lbase);
 }
 
-// Exact kk-th largest K64 among cnt candidates read through get(i).
-template <typename Get>
-__device__ uint64_t select_k64(Get get, int64_t cnt, uint32_t need, SelShared<uint64_t> &sh) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  sel_begin(sh, need);
-  for (int shift = 56; shift >= 0; shift -= 8) {
-    const uint64_t pre = sh.prefix;
-    const uint64_t hmask = shift == 56 ? 0ull : (~0ull << (shift + 8));
-    for (int64_t i0 = 0; i0 < cnt; i0 += kFinThreads) {
-      const int64_t i = i0 + tid;
-      uint64_t v = 0ull;
-      bool act = false;
-      if (i < cnt) {
-        v = get(i);
-        act = (v & hmask) == (pre & hmask);
-      }
-      wave_hist_add(sh.hist, (uint32_t)(v >> shift) & 255u, act, lane);
-    }
-    sel_pick(sh, shift);
-    if (sh.done) break;
-  }
-  return sh.prefix;
-}
-
+// Exact top kk of a row's candidates, sorted by K64 descending (score
+// descending, index ascending), then the sink and local positions.
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_t k, int64_t sink, int64_t local,
                                                                TopkSel s, int64_t *__restrict__ idx) {
   constexpr int kPer = kCandLds / kFinThreads;
   __shared__ uint64_t cl[kCandLds];
-  __shared__ uint64_t ss[kMaxK + 8];
-  __shared__ SelShared<uint64_t> sh;
+  __shared__ uint64_t ss[kMaxK];
+  __shared__ RangeShared sh;
   __shared__ uint32_t s_cnt;
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
@@ -252,16 +282,10 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
       if (i < cnt) cl[i] = v[u];
     }
   }
-  __syncthreads();
-  uint64_t thr = 0ull;
-  if (cnt >= kk) {
-    if (in_lds)
-      thr = select_k64([&](int64_t i) { return cl[i]; }, cnt, (uint32_t)kk, sh);
-    else
-      thr = select_k64([&](int64_t i) { return gc[i]; }, cnt, (uint32_t)kk, sh);
-  }
   if (tid == 0) s_cnt = 0u;
   __syncthreads();
+  const uint64_t thr = in_lds ? range_select([&](int64_t i) { return cl[i]; }, cnt, (uint32_t)kk, sh)
+                              : range_select([&](int64_t i) { return gc[i]; }, cnt, (uint32_t)kk, sh);
   for (int64_t i = tid; i < cnt; i += kFinThreads) {
     const uint64_t v = in_lds ? cl[i] : gc[i];
     if (v >= thr) {
@@ -270,26 +294,29 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
     }
   }
   __syncthreads();
-  // the selected keys are distinct: each one's output position is the number
-  // of selected keys above it (every lane of a wave reads the same ss[j])
-  const int got = (int)min(s_cnt, (uint32_t)kMaxK);
-  for (int i = got + tid; i < ((got + 7) & ~7); i += kFinThreads) ss[i] = 0ull;  // pad to 8 (zero ranks below all)
+  const int got = (int)min(min(s_cnt, (uint32_t)kMaxK), (uint32_t)kk);
+  int P = 1;
+  while (P < got) P <<= 1;
+  for (int i = got + tid; i < P; i += kFinThreads) ss[i] = 0ull;  // zero sorts below every K64
   __syncthreads();
-  for (int i = tid; i < got; i += kFinThreads) {
-    const uint64_t v = ss[i];
-    int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-    for (int j = 0; j < got; j += 8) {  // independent LDS reads in flight
-      const uint64_t a0 = ss[j], a1 = ss[j + 1], a2 = ss[j + 2], a3 = ss[j + 3];
-      const uint64_t a4 = ss[j + 4], a5 = ss[j + 5], a6 = ss[j + 6], a7 = ss[j + 7];
-      r0 += (a0 > v) + (a4 > v);
-      r1 += (a1 > v) + (a5 > v);
-      r2 += (a2 > v) + (a6 > v);
-      r3 += (a3 > v) + (a7 > v);
+  // bitonic sort of ss[0, P), descending
+  for (int kb = 2; kb <= P; kb <<= 1) {
+    for (int j = kb >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < P; i += kFinThreads) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t a = ss[i], b = ss[ixj];
+          if (((i & kb) == 0) ? (a < b) : (a > b)) {
+            ss[i] = b;
+            ss[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
     }
-    const int rank = (r0 + r1) + (r2 + r3);
-    if (rank < kk) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)v);
   }
-  for (int i = got + tid; i < (int)kk; i += kFinThreads) out[i] = 0;
+  for (int i = tid; i < (int)kk; i += kFinThreads)
+    out[i] = i < got ? (int64_t)(0xFFFFFFFFu - (uint32_t)ss[i]) : 0;
   for (int i = tid; i < (int)(sink + local); i += kFinThreads)
     out[kk + i] = (i < sink) ? (int64_t)i : (int64_t)(m - local + (i - sink));
 }
@@ -345,8 +372,11 @@ int launch_sample_scores(const float *scores, int64_t rows, int64_t n, int64_t S
 
 int launch_filter_scores(const float *scores, int64_t rows, int64_t n, int64_t sink, int64_t lstart, TopkSel s,
                          hipStream_t st) {
-  filter_scores_kernel<<<dim3((unsigned)cdiv(n, kFilterChunk), (unsigned)rows), kFilterThreads, 0, st>>>(
-      scores, n, sink, lstart, s);
+  const dim3 grid((unsigned)cdiv(n, kFilterChunk), (unsigned)rows);
+  if (n % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0)
+    filter_scores_kernel<true><<<grid, kFilterThreads, 0, st>>>(scores, n, sink, lstart, s);
+  else
+    filter_scores_kernel<false><<<grid, kFilterThreads, 0, st>>>(scores, n, sink, lstart, s);
   return launch_status("filter_scores_kernel");
 }
 

@@ -99,17 +99,18 @@ int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D,
 
 /*
  * PlaneStore.scan (kernels/bitplane.py:319-338, scan_planes_cls_kernel :275-307):
- * out[bh, g, tok] = sum_j q[bh, g, j] * value_{t_j}(tok, j) for the 64-token
- * blocks [blk0, blk1) (tokens < n); other tokens of `out` are not written.
+ * out[bh, g, tok] = sum_j q[bh, g, j] * value_{t_j}(tok, j) over the channels of
+ * the plan's depth classes 1..min(bmax, 4), for the 64-token blocks [blk0, blk1)
+ * (tokens < n); other tokens of `out` are not written.
  *   q         [BH, G, D] float32, 1 <= G <= 8, D <= 256
- *   t, act, nact  from fathom_make_plan (bmax <= 4)
+ *   cls, clsn from fathom_make_plan ([BH, bmax, D] and [BH, bmax] int32)
  *   planes_sb [BH, nsb, D, 4, sub] uint64, scales_sb [BH, nsb, D, sub] fp16
  *             (HBM, or mapped pinned host memory: the scan then reads over PCIe)
  *   out       [BH, G, n] float32
  */
-int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t, const int32_t *act,
-                       const int32_t *nact, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb,
-                       int64_t sub, int64_t blk0, int64_t blk1, float *out, void *stream);
+int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn,
+                       int bmax, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
+                       int64_t blk0, int64_t blk1, float *out, void *stream);
 
 /*
  * Fused scan + sink/local top-k: the selection of fathom_scan_planes followed by
@@ -122,9 +123,9 @@ int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const i
  * fathom_scan_topk_workspace_bytes(BH, G, n, k, sink, local) bytes.
  */
 size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink, int64_t local);
-int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int8_t *t, const int32_t *act,
-                     const int32_t *nact, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb,
-                     int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace,
+int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn,
+                     int bmax, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
+                     int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace,
                      size_t workspace_bytes, void *stream);
 
 /*
