@@ -30,6 +30,9 @@ COMMON_FLAGS = [
     "-fno-gpu-flush-denormals-to-zero",
     # no packed-FP32 instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the scan's 4x4x1 accumulations update in place
+    # (the AGPR form copies the accumulator around every MFMA of a loop)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas",
 ]
 

@@ -4,28 +4,34 @@
 //   s = sum_j q_gj * a_bj * 2^(1 - t_j) * x_j(i),   x = c_t - (2^t - 1) / 2,
 // where c_t is the top-t-bit code and a_bj the block absmax.  This is the
 // reference's dequantised value (c_t + 0.5 - 2^(t-1)) * a / 2^(t-1)
-// (kernels/bitplane.py:34-42) with the constant term folded into x: x is the
-// sum over the t plane bits of +-2^(t-2-p), so it is built from the plane
-// words alone by t v_cndmask selections between +-(4, 2, 1, 0.5) -- all inline
-// constants -- and t-1 adds, exactly.
+// (kernels/bitplane.py:34-42) with the constant term folded into x.  Each
+// factor is exact up to the final products: the kernel builds y = a * x' with
+// x' = -x for depth 1 (x' = +-0.5 from the bit as a sign) and x' = 2x for
+// deeper channels (x' = 2c_t - 2^t + 1, an integer), and the head weights
+// w_gj = -q_gj (depth 1) or q_gj * 2^(-t_j) absorb the sign and the power of
+// two, so w * y is exactly q * a * 2^(1-t) * x.
 //
-// Lane = token: a 64-bit plane word holds one bit per lane of a wave64.
-// A workgroup owns a tile of 32 blocks (2048 tokens) of one row bh; each of
-// its 4 waves owns 8 consecutive blocks ("group") and works alone after the
-// workgroup has put q_gj * 2^(1-t_j) for all listed channels in LDS.
-// Channels are visited by depth class (the plan's cls lists), so the depth is
-// a compile-time constant of the inner loop.  Two kernels reach the planes:
-//  * direct (store in HBM, sub % 8 == 0): the group's plane words are 8
-//    consecutive words of each (channel, plane) and its 8 fp16 scales 16
-//    consecutive bytes, read by scalar loads into SGPRs; each word is the lane
-//    mask of a v_cndmask (no per-lane bit extraction) and each scale feeds a
-//    v_fma_mix (fp16 operand, no conversion): per (channel, block) the VALU
-//    work is 2t + G instructions;
-//  * staged (store in mapped host memory, or any other sub): a chunk of
-//    channels' words and scales is copied to LDS with coalesced vector loads,
-//    so PCIe reads are whole (channel, plane) runs, and lanes extract bits.
-// Both build the same exact x, multiply by the same scale and accumulate in
-// the same channel order: their scores are bit-identical.
+// Layout of the work: a workgroup (4 waves) owns a tile of 32 blocks (2048
+// tokens) of one row bh; wave w owns blocks 8w..8w+7, lane = token.  The
+// plan's channels are visited in chunks of at most 16 (channel, plane) units
+// of one depth class.  A chunk's plane words (32 blocks each) and scales are
+// read with coalesced vector loads (every (channel, plane) run of the tile is
+// whole 128-byte segments: HBM, or PCIe for a store in mapped host memory)
+// and stored in LDS with each word split into its low dword (tokens 0-31) and
+// high dword (tokens 32-63), so a lane reads only the dwords holding its own
+// bits, four blocks per 16-byte LDS read.  Chunks are double buffered: the
+// loads of chunk k + 1 are in flight while chunk k is computed.
+//
+// Per (channel, block) the VALU extracts the lane's t bits and forms y (3
+// instructions at depth 1, 2t + 2 deeper); the head contraction acc_g += w_gj
+// * y runs on the matrix cores: one v_mfma_f32_4x4x1_16b_f32 per (channel,
+// block) multiplies the lane's y (B operand: lane = token) by the four heads'
+// weights (A operand: lane l holds head l & 3) and adds into four fp32
+// accumulators per lane (head h in component h).  Each step is an fp32 fused
+// multiply-add, the operation of v_fmac_f32: the score is one fp32 FMA chain
+// over the channels in plan order, whatever the store's location, so scans of
+// a store in HBM and of the same store in host memory are bit-identical.
+// G > 4 takes a second MFMA for heads 4..7.
 //
 // Output modes: scores [BH, G, n] (PlaneStore.scan), sampled keys (every S-th
 // tile, for the top-k threshold), or candidate emission (key >= threshold ->
@@ -40,9 +46,10 @@ constexpr int kGB = 8;             // blocks per wave
 constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kTB = kGB * kWaves;  // blocks per tile
 constexpr int kMaxD = 256;
-constexpr int kCH = 16;            // channels per staged chunk
-constexpr uint32_t kRowLocal = 128;  // LDS candidates per (workgroup, row)
+constexpr int kUnits = 16;         // (channel, plane) units per chunk
 static_assert(kTB * kBlk == kTileTok, "scan tile and top-k sample tile must agree");
+constexpr int kThreads = 64 * kWaves;
+static_assert(kUnits == 2 * (kThreads / kTB), "each thread stages two units of one block");
 
 enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2 };
 
@@ -67,116 +74,173 @@ struct ScanArgs {
   int D, bmax, ncls;       // classes 1..ncls are scanned (ncls = min(bmax, 4))
 };
 
-typedef unsigned int u32x16 __attribute__((ext_vector_type(16)));
-typedef unsigned int u32x8 __attribute__((ext_vector_type(8)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Wave-uniform loads through the constant address space: scalar loads into
-// SGPRs (the store, plan and queries are read-only for the kernel's lifetime).
+// SGPRs (the plan is read-only for the kernel's lifetime).
 template <typename T>
 __device__ __forceinline__ T ld_uniform(const T *p) {
   return *(const __attribute__((address_space(4))) T *)(p);
 }
 
-__device__ __forceinline__ int64_t sgpr64(int64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
+// ----------------------------------------------------------------- head weights
+// w_gj for every listed channel, QS floats per channel (heads >= G are zero),
+// so the MFMA A operand of lane l is w[j][4h + (l & 3)].
 template <int G>
 struct QShared {
-  float qw[kMaxD * G];  // q_gj * 2^(1 - t_j) for listed channels, [channel][head]
+  static constexpr int QS = G <= 4 ? 4 : 8;
+  float w[kMaxD * QS];
 };
 
-// Workgroup prologue: the depth-scaled query weights of every listed channel.
-// With prefetch, it also touches (one dword each) every plane and scale line
-// the tile's four groups will read, so the waves' scalar loads find them in
-// L2 instead of waiting on HBM one channel at a time; the returned value is
-// only there to keep those loads alive.
+// Per-channel head operand: the lane's MFMA A value(s).
 template <int G>
-__device__ __forceinline__ uint32_t load_qw(QShared<G> &sh, const ScanArgs &a, int64_t bh, int64_t tb0,
-                                            bool prefetch) {
-  uint32_t pf = 0u;
-  const int64_t nblk_store = a.nsb * a.sub;
-  for (int c = 1; c <= a.ncls; ++c) {
-    const int nc = min(max(a.clsn[bh * a.bmax + c - 1], 0), a.D);
-    const int32_t *lst = a.cls + (bh * a.bmax + c - 1) * a.D;
-    for (int i = threadIdx.x; i < nc * G; i += 256) {
-      const int ci = i / G, g = i - ci * G;
-      const int j = lst[ci];
-      if (j >= 0 && j < a.D) sh.qw[j * G + g] = ldexpf(a.q[(bh * G + g) * a.D + j], 1 - c);
-    }
-    if (!prefetch) continue;
-    // items: (channel, plane or scale, group) -- c planes + 1 scale line per group
-    for (int i = threadIdx.x; i < nc * (c + 1) * kWaves; i += 256) {
-      const int w = i % kWaves, p = (i / kWaves) % (c + 1), ci = i / (kWaves * (c + 1));
-      const int j = lst[ci];
-      const int64_t b = tb0 + w * kGB;
-      if (j < 0 || j >= a.D || b >= nblk_store) continue;
-      const int64_t sb = (int64_t)((uint64_t)b / (uint64_t)a.sub);
-      const int64_t off = b - sb * a.sub;
-      if (p < c)
-        pf ^= *reinterpret_cast<const uint32_t *>(a.planes + ((bh * a.nsb + sb) * a.D + j) * 4 * a.sub + p * a.sub + off);
-      else
-        pf ^= *reinterpret_cast<const uint32_t *>(a.scales + ((bh * a.nsb + sb) * a.D + j) * a.sub + (off & ~1));
-    }
+struct QOp {
+  static constexpr int NQ = (G + 3) / 4;
+  float a[NQ];
+};
+
+template <int G>
+__device__ __forceinline__ QOp<G> load_qop(const QShared<G> &qs, int j, int lane) {
+  QOp<G> o;
+#pragma unroll
+  for (int h = 0; h < QOp<G>::NQ; ++h) o.a[h] = qs.w[j * QShared<G>::QS + 4 * h + (lane & 3)];
+  return o;
+}
+
+// Four fp32 accumulators per lane and head quad: component h of v[b][hq] is the
+// score of head 4*hq + h for the lane's token of block b.
+template <int G>
+struct Acc {
+  static constexpr int NQ = (G + 3) / 4;
+  f32x4 v[kGB][NQ];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int b = 0; b < kGB; ++b)
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) v[b][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  return pf;
+  __device__ __forceinline__ float get(int b, int g) const { return v[b][g >> 2][g & 3]; }
+};
+
+template <int G>
+__device__ __forceinline__ void accum(Acc<G> &acc, int b, const QOp<G> &q, float y) {
+#pragma unroll
+  for (int h = 0; h < QOp<G>::NQ; ++h) acc.v[b][h] = __builtin_amdgcn_mfma_f32_4x4x1f32(q.a[h], y, acc.v[b][h], 0, 0, 0);
 }
 
-// Exact symmetric code x = c - (2^C - 1)/2 of a lane's token from its C plane
-// words (word p is the lane mask of a select between +-2^(C-2-p)).
+// ----------------------------------------------------------------- value of a lane
+// y = a * x' of the lane's token from the C dwords holding its plane bits (bit
+// l31 of each) and the block's staged scale pair (P, Q):
+//  * depth 1: y = -a * x = (bit ? -a/2 : +a/2), the bit put into the sign of
+//    P = a/2 (a >= 0);
+//  * deeper: y = 2a * x = c * P + Q with P = 2a, Q = -(2^C - 1) a and c the
+//    C-bit code: one fused multiply-add of exact operands (c < 16, a fp16).
 template <int C>
-__device__ __forceinline__ float sym_code(const uint64_t *w) {
-#define FATHOM_SEL(p, v) (__builtin_amdgcn_inverse_ballot_w64(w[p]) ? (v) : -(v))
-  if (C == 1) return FATHOM_SEL(0, 0.5f);
-  if (C == 2) return FATHOM_SEL(0, 1.0f) + FATHOM_SEL(C > 1 ? 1 : 0, 0.5f);
-  if (C == 3) return (FATHOM_SEL(0, 2.0f) + FATHOM_SEL(C > 1 ? 1 : 0, 1.0f)) + FATHOM_SEL(C > 2 ? 2 : 0, 0.5f);
-  return (FATHOM_SEL(0, 4.0f) + FATHOM_SEL(C > 1 ? 1 : 0, 2.0f)) +
-         (FATHOM_SEL(C > 2 ? 2 : 0, 1.0f) + FATHOM_SEL(C > 3 ? 3 : 0, 0.5f));
-#undef FATHOM_SEL
-}
-
-// Same value from the integer code (staged kernel): exact in fp32.
-template <int C>
-__device__ __forceinline__ float sym_from_int(uint32_t code) {
-  return (float)code - (float)((1 << C) - 1) * 0.5f;
-}
-
-// a * x with a given as fp16 bits (v_fma_mix_f32: the fp16 operand needs no
-// conversion; + 0 keeps it one rounding, as a product).
-__device__ __forceinline__ float scaled(uint16_t a_bits, float x) {
-  return fmaf(__half2float(__ushort_as_half(a_bits)), x, 0.0f);
+__device__ __forceinline__ float lane_value(const uint32_t (&dw)[C], int l31, float P, float Q) {
+  if (C == 1) return __uint_as_float(((dw[0] << (31 - l31)) & 0x80000000u) | __float_as_uint(P));
+  uint32_t c = __builtin_amdgcn_ubfe(dw[0], l31, 1);
+#pragma unroll
+  for (int p = 1; p < C; ++p) c = (c << 1) + __builtin_amdgcn_ubfe(dw[p], l31, 1);
+  return fmaf((float)c, P, Q);
 }
 
 // --------------------------------------------------------------------- emission
 template <int G>
 struct EmitShared {
-  uint64_t lbuf[G][kRowLocal];
-  uint32_t lcnt[G];
-  uint32_t lbase[G];
+  uint32_t wcnt[G];   // candidates of the workgroup per head
+  uint32_t gbase[G];  // their first slot in the row's global list
 };
 
-template <int G, int MODE>
-__device__ __forceinline__ void emit_group(const Emit &em, EmitShared<G> &es, const float (&acc)[kGB][G],
-                                           int64_t bh, int64_t gb0, int64_t blk0, int64_t blk_end, int64_t n,
-                                           int wave, int lane, int64_t samp_tile) {
+// Threshold of a row as a float for "key >= thr": every element whose key is
+// >= thr has !(v < thr_f) (thr at or below -inf's key: everything passes; thr
+// in the NaN range: NaN and +inf pass -- extra candidates never change the
+// exact selection, they only cost time).
+__device__ __forceinline__ float threshold_value(uint32_t thr) {
+  if (thr <= kKeyNegInf) return -INFINITY;
+  if (thr > 0xFF800000u) return INFINITY;  // above +inf's key
+  return key_value(thr);
+}
+
+// Candidate emission of a wave's 8 blocks: count the passing tokens per head
+// (one compare + ballot per (block, head)), reserve the wave's slots with one
+// LDS atomic per head and the workgroup's with one global atomic per head,
+// then write each passing token's K64 straight to the row's list.
+template <int G>
+__device__ __forceinline__ void emit_filter(const Emit &em, EmitShared<G> &es, const Acc<G> &acc, int64_t bh,
+                                            int64_t gb0, int64_t blk0, int64_t blk_end, int64_t n, int lane) {
   const int tid = threadIdx.x;
-  if (MODE == kEmitFilter) {
-    if (tid < G) es.lcnt[tid] = 0u;
-    __syncthreads();
-  }
+  if (tid < G) es.wcnt[tid] = 0u;
+  const int64_t t0 = gb0 * kBlk, t1 = t0 + kGB * kBlk;
+  // no per-lane validity or sink/local masking anywhere in the wave's blocks
+  const bool plain = gb0 >= blk0 && gb0 + kGB <= blk_end && t1 <= n && t0 >= em.sink && t1 <= em.lstart;
   float thr_f[G];
-  bool thr_all[G];
-  if (MODE == kEmitFilter) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const uint32_t thr = em.sel.thr[bh * G + g];
-      thr_all[g] = thr == 0u;  // fewer samples than kk: every valid token is a candidate
-      thr_f[g] = key_value(thr);
+  for (int g = 0; g < G; ++g) thr_f[g] = threshold_value(ld_uniform(em.sel.thr + bh * G + g));
+  auto masked_value = [&](int r, int g, bool &valid) -> float {
+    const float v = acc.get(r, g);
+    if (plain) {
+      valid = true;
+      return v;
     }
+    const int64_t b = gb0 + r, tok = b * kBlk + lane;
+    valid = b >= blk0 && b < blk_end && tok < n;
+    return (tok < em.sink || tok >= em.lstart) ? -INFINITY : v;
+  };
+  uint32_t cnt[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    cnt[g] = 0u;
+#pragma unroll
+    for (int r = 0; r < kGB; ++r) {
+      bool valid;
+      const float vm = masked_value(r, g, valid);
+      cnt[g] += (uint32_t)__popcll(__ballot(valid && !(vm < thr_f[g])));
+    }
+  }
+  __syncthreads();  // counters cleared
+  uint32_t wbase[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    uint32_t o = 0u;
+    if (lane == 0 && cnt[g]) o = atomicAdd(&es.wcnt[g], cnt[g]);
+    wbase[g] = __builtin_amdgcn_readfirstlane(o);
+  }
+  __syncthreads();
+  if (tid < G) {
+    const uint32_t c = es.wcnt[tid];
+    es.gbase[tid] = c ? atomicAdd(&em.sel.cand_cnt[bh * G + tid], c) : 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (cnt[g] == 0u) continue;
+    const int64_t row = bh * G + g;
+    uint64_t *dst = em.sel.cand + row * em.sel.cand_cap;
+    uint64_t off = (uint64_t)es.gbase[g] + wbase[g];
+#pragma unroll
+    for (int r = 0; r < kGB; ++r) {
+      bool valid;
+      const float vm = masked_value(r, g, valid);
+      const bool pass = valid && !(vm < thr_f[g]);
+      const uint64_t m = __ballot(pass);
+      if (m == 0ull) continue;
+      const uint64_t slot = off + (uint64_t)__popcll(m & ((1ull << lane) - 1ull));
+      if (pass && slot < (uint64_t)em.sel.cand_cap) {
+        const int64_t tok = (gb0 + r) * kBlk + lane;
+        dst[slot] = k64_of(vm == -INFINITY ? kKeyNegInf : score_key(vm), tok);
+      }
+      off += (uint64_t)__popcll(m);
+    }
+  }
+}
+
+template <int G, int MODE>
+__device__ __forceinline__ void emit_group(const Emit &em, EmitShared<G> &es, const Acc<G> &acc, int64_t bh,
+                                           int64_t gb0, int64_t blk0, int64_t blk_end, int64_t n, int wave, int lane,
+                                           int64_t samp_tile) {
+  if (MODE == kEmitFilter) {
+    emit_filter<G>(em, es, acc, bh, gb0, blk0, blk_end, n, lane);
+    return;
   }
 #pragma unroll
   for (int r = 0; r < kGB; ++r) {
@@ -185,278 +249,234 @@ __device__ __forceinline__ void emit_group(const Emit &em, EmitShared<G> &es, co
     const bool valid = b >= blk0 && b < blk_end && tok < n;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float v = acc[r][g];
+      const float v = acc.get(r, g);
       const int64_t row = bh * G + g;
       if (MODE == kEmitScores) {
         if (valid) em.out[row * n + tok] = v;
       } else {
         const bool masked = tok < em.sink || tok >= em.lstart;
-        if (MODE == kEmitSample) {
-          const uint32_t key = valid ? (masked ? kKeyNegInf : score_key(v)) : 0u;
-          em.samp[row * em.samp_cap + samp_tile * kTileTok + (wave * kGB + r) * kBlk + lane] = key;
-        } else {
-          // key >= thr tested on floats: thr_f is the value whose key is thr
-          const float vm = masked ? -INFINITY : v;
-          const bool pass = valid && (thr_all[g] || vm >= thr_f[g] || vm != vm);
-          wave_append_local(pass, pass ? k64_of(masked ? kKeyNegInf : score_key(v), tok) : 0ull, &es.lcnt[g],
-                            es.lbuf[g], kRowLocal, &em.sel.cand_cnt[row], em.sel.cand + row * em.sel.cand_cap,
-                            (uint64_t)em.sel.cand_cap, lane);
-        }
+        const uint32_t key = valid ? (masked ? kKeyNegInf : score_key(v)) : 0u;
+        em.samp[row * em.samp_cap + samp_tile * kTileTok + (wave * kGB + r) * kBlk + lane] = key;
       }
     }
   }
-  if (MODE == kEmitFilter) {
-    // one reservation per row, all rows at once, then one copy pass
-    __syncthreads();
-    if (tid < G) {
-      const uint32_t nloc = min(es.lcnt[tid], kRowLocal);
-      es.lbase[tid] = nloc ? atomicAdd(&em.sel.cand_cnt[bh * G + tid], nloc) : 0u;
-    }
-    __syncthreads();
-    for (int e = tid; e < G * (int)kRowLocal; e += 256) {
-      const int g = e / (int)kRowLocal, i = e % (int)kRowLocal;
-      const uint32_t nloc = min(es.lcnt[g], kRowLocal);
-      const uint64_t slot = (uint64_t)es.lbase[g] + i;
-      if ((uint32_t)i < nloc && slot < (uint64_t)em.sel.cand_cap)
-        em.sel.cand[(bh * G + g) * em.sel.cand_cap + slot] = es.lbuf[g][i];
-    }
-  }
 }
 
-// --------------------------------------------------------------------- direct (HBM) kernel
-// HB blocks per load group: 8 for depth <= 2, 4 for deeper classes (at most
-// 32 SGPRs of plane words live per group).
-template <int C>
-struct Depth {
-  static constexpr int HB = C <= 2 ? 8 : 4;
+// --------------------------------------------------------------------- tile kernel
+// One chunk of the plan: channels [i0, i0 + m) of depth class c + 1, staged as
+// m * (c + 1) (channel, plane) units (unit u = channel slot * (c + 1) + plane).
+struct Chunk {
+  int c, i0, m;
 };
 
-template <int HB>
-struct WordVec;
-template <>
-struct WordVec<8> {
-  typedef u32x16 W;
-  typedef u32x4 S;
+// Channels per chunk of class index c (depth c + 1): 16, 8, 5, 4.
+__host__ __device__ constexpr int chunk_channels(int c) { return kUnits / (c + 1); }
+
+__device__ __forceinline__ Chunk chunk_at(const int (&nc)[4], int k) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int cpc = chunk_channels(c);
+    const int nk = (nc[c] + cpc - 1) / cpc;
+    if (k < nk) return Chunk{c, k * cpc, min(cpc, nc[c] - k * cpc)};
+    k -= nk;
+  }
+  return Chunk{0, 0, 0};
+}
+
+// u / (c + 1) for u < 16 without a division
+__device__ __forceinline__ int unit_channel(int u, int c) {
+  return c == 0 ? u : c == 1 ? (u >> 1) : c == 2 ? ((u * 11) >> 5) : (u >> 2);
+}
+
+// A staged chunk: low and high dword of each unit's 32 block words, and the
+// scale pair (P, Q) of each channel slot's 32 blocks.
+struct ChunkBuf {
+  uint32_t lo[kUnits][kTB];
+  uint32_t hi[kUnits][kTB];
+  float2 sc[kUnits][kTB];
 };
-template <>
-struct WordVec<4> {
-  typedef u32x8 W;
-  typedef u32x2 S;
-};
 
-// One channel of depth C over the wave's 8 blocks: pj = its plane-0 word of the
-// group's first block (plane p at + p*sub), sj = its first fp16 scale.
-template <int C, int G>
-__device__ __forceinline__ void direct_channel(const uint64_t *pj, const uint16_t *sj, int64_t sub, const float *qv,
-                                               float (&acc)[kGB][G]) {
-  constexpr int HB = Depth<C>::HB;
-  typedef typename WordVec<HB>::W WV;
-  typedef typename WordVec<HB>::S SV;
-#pragma unroll
-  for (int h = 0; h < kGB / HB; ++h) {
-    // keeps the next half's loads below this half's use (merged loads would
-    // need twice the SGPRs)
-    if (h > 0) __builtin_amdgcn_sched_barrier(0);
-    WV wv[C];
-#pragma unroll
-    for (int p = 0; p < C; ++p) wv[p] = ld_uniform(reinterpret_cast<const WV *>(pj + p * sub + h * HB));
-    const SV sv = ld_uniform(reinterpret_cast<const SV *>(sj + h * HB));
-#pragma unroll
-    for (int r = 0; r < HB; ++r) {
-      uint64_t w[C];
-#pragma unroll
-      for (int p = 0; p < C; ++p) w[p] = ((uint64_t)wv[p][2 * r + 1] << 32) | wv[p][2 * r];
-      const float x = sym_code<C>(w);
-      const uint32_t sd = sv[r >> 1];
-      const float u = scaled((uint16_t)((r & 1) ? (sd >> 16) : (sd & 0xFFFFu)), x);
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[h * HB + r][g] = fmaf(qv[g], u, acc[h * HB + r][g]);
-    }
-  }
-}
-
-template <int C, int G>
-__device__ __forceinline__ void direct_class(const ScanArgs &a, const QShared<G> &qs, int64_t bh, const uint64_t *pw,
-                                             const uint16_t *ps, float (&acc)[kGB][G]) {
-  if (C > a.ncls) return;
-  const int nc = min(max(ld_uniform(a.clsn + bh * a.bmax + C - 1), 0), a.D);
-  const int32_t *lst = a.cls + (bh * a.bmax + C - 1) * a.D;
-  int jn = nc > 0 ? ld_uniform(lst) : 0;
-  for (int i = 0; i < nc; ++i) {
-    const int j = jn;
-    if (i + 1 < nc) jn = ld_uniform(lst + i + 1);
-    if ((unsigned)j >= (unsigned)a.D) continue;
-    float qv[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) qv[g] = qs.qw[j * G + g];
-    direct_channel<C, G>(pw + (int64_t)j * 4 * a.sub, ps + (int64_t)j * a.sub, a.sub, qv, acc);
-  }
-}
-
-template <int G, int MODE>
-__global__ __launch_bounds__(256) void scan_direct_kernel(ScanArgs a, Emit em) {
-  __shared__ QShared<G> qs;
-  __shared__ EmitShared<G> es;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t bh = blockIdx.y;
-  const int64_t tile = a.tile0 + (int64_t)blockIdx.x * a.tile_stride;
-  const int64_t gb0 = tile * kTB + wave * kGB;  // first block of this wave's group
-  const uint32_t pf = load_qw<G>(qs, a, bh, tile * kTB, true);
-  __syncthreads();
-  float acc[kGB][G];
-#pragma unroll
-  for (int r = 0; r < kGB; ++r)
-#pragma unroll
-    for (int g = 0; g < G; ++g) acc[r][g] = 0.0f;
-  // groups outside the emitted range or past the store are not read
-  if (gb0 < a.blk_end && gb0 + kGB > a.blk0 && gb0 < a.nsb * a.sub) {
-    const int64_t sb = sgpr64(gb0 / a.sub);
-    const int64_t off = gb0 - sb * a.sub;
-    const uint64_t *pw = a.planes + (bh * a.nsb + sb) * a.D * 4 * a.sub + off;
-    const uint16_t *ps = a.scales + (bh * a.nsb + sb) * a.D * a.sub + off;
-    direct_class<1, G>(a, qs, bh, pw, ps, acc);
-    direct_class<2, G>(a, qs, bh, pw, ps, acc);
-    direct_class<3, G>(a, qs, bh, pw, ps, acc);
-    direct_class<4, G>(a, qs, bh, pw, ps, acc);
-  }
-  asm volatile("" ::"v"(pf));  // the prefetch loads retire here
-  emit_group<G, MODE>(em, es, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
-}
-
-// --------------------------------------------------------------------- staged kernel
 template <int G>
-struct StagedShared {
-  uint64_t w[kCH * 4 * kTB];   // [channel][plane][block]
-  uint16_t s[kCH * kTB];       // [channel][block]
-  int ch[kCH];
+struct TileShared {
+  QShared<G> qs;
+  uint8_t lst[4][kMaxD];  // the plan's class lists, clamped to [0, D)
+  ChunkBuf buf[2];
 };
 
+// The words and scales one thread stages: block bi = tid % 32 of units and
+// channel slots tid / 32 and tid / 32 + 8.
+struct Staged {
+  uint64_t w[2];
+  uint16_t s[2];
+};
+
+// pbase / sbase: element offsets of the thread's block in planes / scales with
+// the channel term left out (channel j adds j * 4 * sub / j * sub).
+__device__ __forceinline__ void load_chunk(Staged &r, const ScanArgs &a, const uint8_t (*lst)[kMaxD], const Chunk &ck,
+                                           int slot, bool inb, int64_t pbase, int64_t sbase) {
+  const int C = ck.c + 1;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int u = slot + 8 * h;
+    r.w[h] = 0ull;
+    r.s[h] = 0;
+    if (inb && u < ck.m * C) {
+      const int ci = unit_channel(u, ck.c), p = u - ci * C;
+      const int j = lst[ck.c][ck.i0 + ci];
+      r.w[h] = a.planes[pbase + ((int64_t)j * 4 + p) * a.sub];
+    }
+    if (inb && u < ck.m) {
+      const int j = lst[ck.c][ck.i0 + u];
+      r.s[h] = a.scales[sbase + (int64_t)j * a.sub];
+    }
+  }
+}
+
+__device__ __forceinline__ void store_chunk(ChunkBuf &b, const Staged &r, int c, int slot, int bi) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int u = slot + 8 * h;
+    b.lo[u][bi] = (uint32_t)r.w[h];
+    b.hi[u][bi] = (uint32_t)(r.w[h] >> 32);
+    const float a = __half2float(__ushort_as_half(r.s[h]));
+    b.sc[u][bi] = c == 0 ? make_float2(0.5f * a, 0.0f) : make_float2(2.0f * a, -(float)((2 << c) - 1) * a);
+  }
+}
+
+// The wave's 8 blocks of every channel of a staged chunk of depth C, in list
+// order, four blocks per half: one 16-byte LDS read per (plane, half) brings the
+// lane's four dwords, two more the four scale pairs.
 template <int C, int G>
-__device__ __forceinline__ void staged_class(const ScanArgs &a, const QShared<G> &qs, StagedShared<G> &st, int64_t bh,
-                                             int64_t tb0, int wave, int lane, float (&acc)[kGB][G]) {
-  if (C > a.ncls) return;
-  const int tid = threadIdx.x;
-  const int nc = min(max(a.clsn[bh * a.bmax + C - 1], 0), a.D);
-  const int32_t *lst = a.cls + (bh * a.bmax + C - 1) * a.D;
-  const int64_t nblk_store = a.nsb * a.sub;
-  for (int c0 = 0; c0 < nc; c0 += kCH) {
-    const int na = min(kCH, nc - c0);
-    __syncthreads();  // the previous chunk is consumed
-    if (tid < na) {
-      const int j = lst[c0 + tid];
-      st.ch[tid] = (j >= 0 && j < a.D) ? j : -1;
-    }
-    __syncthreads();
-    // consecutive threads read consecutive blocks of one (channel, plane):
-    // contiguous words within each superblock
-    for (int idx = tid; idx < na * C * kTB; idx += 256) {
-      const int bi = idx % kTB, p = (idx / kTB) % C, ci = idx / (C * kTB);
-      const int j = st.ch[ci];
-      const int64_t b = tb0 + bi;
-      uint64_t v = 0ull;
-      if (j >= 0 && b < nblk_store) {
-        const int64_t sb = b / a.sub;
-        v = a.planes[((bh * a.nsb + sb) * a.D + j) * 4 * a.sub + p * a.sub + (b - sb * a.sub)];
+__device__ __forceinline__ void compute_chunk(const ChunkBuf &b, const QShared<G> &qs, const uint8_t *lst, int m,
+                                              int wave, int lane, Acc<G> &acc) {
+  const int l31 = lane & 31;
+  const uint32_t *wl = (lane < 32 ? &b.lo[0][0] : &b.hi[0][0]) + wave * kGB;
+  for (int ci = 0; ci < m; ++ci) {
+    const QOp<G> q = load_qop<G>(qs, lst[ci], lane);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const float4 s01 = *reinterpret_cast<const float4 *>(&b.sc[ci][wave * kGB + 4 * hf]);
+      const float4 s23 = *reinterpret_cast<const float4 *>(&b.sc[ci][wave * kGB + 4 * hf + 2]);
+      const float P[4] = {s01.x, s01.z, s23.x, s23.z}, Q[4] = {s01.y, s01.w, s23.y, s23.w};
+      uint4 dq[C];
+#pragma unroll
+      for (int p = 0; p < C; ++p) dq[p] = *reinterpret_cast<const uint4 *>(wl + (ci * C + p) * kTB + 4 * hf);
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint32_t dw[C];
+#pragma unroll
+        for (int p = 0; p < C; ++p) dw[p] = r == 0 ? dq[p].x : r == 1 ? dq[p].y : r == 2 ? dq[p].z : dq[p].w;
+        y[r] = lane_value<C>(dw, l31, P[r], Q[r]);
       }
-      st.w[(ci * 4 + p) * kTB + bi] = v;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) accum<G>(acc, 4 * hf + r, q, y[r]);
     }
-    for (int idx = tid; idx < na * kTB; idx += 256) {
-      const int bi = idx % kTB, ci = idx / kTB;
-      const int j = st.ch[ci];
-      const int64_t b = tb0 + bi;
-      uint16_t v = 0;
-      if (j >= 0 && b < nblk_store) {
-        const int64_t sb = b / a.sub;
-        v = a.scales[((bh * a.nsb + sb) * a.D + j) * a.sub + (b - sb * a.sub)];
-      }
-      st.s[ci * kTB + bi] = v;
-    }
-    __syncthreads();
-    for (int ci = 0; ci < na; ++ci) {
-      const int j = st.ch[ci];
-      if (j < 0) continue;
-      float qv[G];
+  }
+}
+
+// Workgroup prologue: the plan's class lists and the head weights in LDS
+// (w = -q at depth 1, q * 2^-t deeper: see lane_value).
+template <int G>
+__device__ __forceinline__ void tile_prologue(TileShared<G> &sh, const ScanArgs &a, const int (&nc)[4], int64_t bh) {
+  constexpr int QS = QShared<G>::QS;
+  const int pre1 = nc[0], pre2 = pre1 + nc[1], pre3 = pre2 + nc[2], tot = pre3 + nc[3];
+  for (int e = threadIdx.x; e < tot; e += kThreads) {
+    const int c = (e >= pre1) + (e >= pre2) + (e >= pre3);
+    const int i = e - (c == 0 ? 0 : c == 1 ? pre1 : c == 2 ? pre2 : pre3);
+    const int jr = a.cls[(bh * a.bmax + c) * a.D + i];
+    const int j = min(max(jr, 0), a.D - 1);  // memory-safe; make_plan lists only valid channels
+    sh.lst[c][i] = (uint8_t)j;
 #pragma unroll
-      for (int g = 0; g < G; ++g) qv[g] = qs.qw[j * G + g];
-#pragma unroll
-      for (int r = 0; r < kGB; ++r) {
-        const int bi = wave * kGB + r;
-        uint32_t code = 0;
-#pragma unroll
-        for (int p = 0; p < C; ++p) code = (code << 1) | (uint32_t)((st.w[(ci * 4 + p) * kTB + bi] >> lane) & 1ull);
-        const float u = scaled(st.s[ci * kTB + bi], sym_from_int<C>(code));
-#pragma unroll
-        for (int g = 0; g < G; ++g) acc[r][g] = fmaf(qv[g], u, acc[r][g]);
-      }
+    for (int g = 0; g < QS; ++g) {
+      const float qv = g < G ? a.q[(bh * G + g) * a.D + j] : 0.0f;
+      sh.qs.w[j * QS + g] = c == 0 ? -qv : ldexpf(qv, -(c + 1));
     }
   }
 }
 
 template <int G, int MODE>
-__global__ __launch_bounds__(256) void scan_staged_kernel(ScanArgs a, Emit em) {
-  __shared__ QShared<G> qs;
-  __shared__ StagedShared<G> st;
+__global__ __launch_bounds__(kThreads) void scan_tile_kernel(ScanArgs a, Emit em) {
+  __shared__ TileShared<G> sh;
   __shared__ EmitShared<G> es;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
   const int64_t tile = a.tile0 + (int64_t)blockIdx.x * a.tile_stride;
   const int64_t tb0 = tile * kTB;
-  load_qw<G>(qs, a, bh, tb0, false);
-  __syncthreads();
-  float acc[kGB][G];
+  int nc[4];
 #pragma unroll
-  for (int r = 0; r < kGB; ++r)
+  for (int c = 0; c < 4; ++c) nc[c] = c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
+  tile_prologue<G>(sh, a, nc, bh);
+  // the thread's staging block
+  const int bi = tid & (kTB - 1), slot = tid / kTB;
+  const int64_t b = tb0 + bi;
+  const bool inb = b < a.nsb * a.sub;
+  const int64_t sb = inb ? b / a.sub : 0;
+  const int64_t off = b - sb * a.sub;
+  const int64_t pbase = (bh * a.nsb + sb) * a.D * 4 * a.sub + off;
+  const int64_t sbase = (bh * a.nsb + sb) * a.D * a.sub + off;
+  Acc<G> acc;
+  acc.zero();
+  int nk = 0;
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[r][g] = 0.0f;
-  // the whole workgroup takes part in staging, so the range test is per tile
-  if (tb0 < a.blk_end && tb0 + kTB > a.blk0) {
-    staged_class<1, G>(a, qs, st, bh, tb0, wave, lane, acc);
-    staged_class<2, G>(a, qs, st, bh, tb0, wave, lane, acc);
-    staged_class<3, G>(a, qs, st, bh, tb0, wave, lane, acc);
-    staged_class<4, G>(a, qs, st, bh, tb0, wave, lane, acc);
+  for (int c = 0; c < 4; ++c) nk += (nc[c] + chunk_channels(c) - 1) / chunk_channels(c);
+  if (tb0 < a.blk_end && tb0 + kTB > a.blk0 && nk > 0) {  // uniform over the workgroup
+    Staged r;
+    __syncthreads();  // class lists and weights ready
+    Chunk nxt = chunk_at(nc, 0);
+    load_chunk(r, a, sh.lst, nxt, slot, inb, pbase, sbase);
+    store_chunk(sh.buf[0], r, nxt.c, slot, bi);
+    __syncthreads();
+    int k = 0;
+    // classes in order, each a loop over its chunks with the depth known at
+    // compile time; the next chunk (possibly of the next class) is loaded
+    // while the current one is computed
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      constexpr int kC[4] = {1, 2, 3, 4};
+      const int cpc = chunk_channels(c);
+      for (int i0 = 0; i0 < nc[c]; i0 += cpc, ++k) {
+        const bool more = k + 1 < nk;
+        if (more) {
+          nxt = chunk_at(nc, k + 1);
+          load_chunk(r, a, sh.lst, nxt, slot, inb, pbase, sbase);
+        }
+        const ChunkBuf &cb = sh.buf[k & 1];
+        const int m = min(cpc, nc[c] - i0);
+        if (c == 0) compute_chunk<kC[0], G>(cb, sh.qs, sh.lst[0] + i0, m, wave, lane, acc);
+        if (c == 1) compute_chunk<kC[1], G>(cb, sh.qs, sh.lst[1] + i0, m, wave, lane, acc);
+        if (c == 2) compute_chunk<kC[2], G>(cb, sh.qs, sh.lst[2] + i0, m, wave, lane, acc);
+        if (c == 3) compute_chunk<kC[3], G>(cb, sh.qs, sh.lst[3] + i0, m, wave, lane, acc);
+        if (more) store_chunk(sh.buf[(k + 1) & 1], r, nxt.c, slot, bi);
+        __syncthreads();
+      }
+    }
   }
   emit_group<G, MODE>(em, es, acc, bh, tb0 + wave * kGB, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
 }
 
 // --------------------------------------------------------------------- launch
 template <int G, int MODE>
-void launch_g(const ScanArgs &a, int64_t tiles, int64_t BH, bool staged, const Emit &em, hipStream_t st) {
-  dim3 grid((unsigned)tiles, (unsigned)BH);
-  if (staged)
-    scan_staged_kernel<G, MODE><<<grid, 256, 0, st>>>(a, em);
-  else
-    scan_direct_kernel<G, MODE><<<grid, 256, 0, st>>>(a, em);
+void launch_g(const ScanArgs &a, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
+  scan_tile_kernel<G, MODE><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
 }
 
 template <int MODE>
-int launch_scan(const ScanArgs &a, int64_t G, int64_t tiles, int64_t BH, bool staged, const Emit &em,
-                hipStream_t st) {
+int launch_scan(const ScanArgs &a, int64_t G, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
   if (tiles <= 0) return FATHOM_OK;
   switch (G) {
-    case 1: launch_g<1, MODE>(a, tiles, BH, staged, em, st); break;
-    case 2: launch_g<2, MODE>(a, tiles, BH, staged, em, st); break;
-    case 3: launch_g<3, MODE>(a, tiles, BH, staged, em, st); break;
-    case 4: launch_g<4, MODE>(a, tiles, BH, staged, em, st); break;
-    case 5: launch_g<5, MODE>(a, tiles, BH, staged, em, st); break;
-    case 6: launch_g<6, MODE>(a, tiles, BH, staged, em, st); break;
-    case 7: launch_g<7, MODE>(a, tiles, BH, staged, em, st); break;
-    default: launch_g<8, MODE>(a, tiles, BH, staged, em, st); break;
+    case 1: launch_g<1, MODE>(a, tiles, BH, em, st); break;
+    case 2: launch_g<2, MODE>(a, tiles, BH, em, st); break;
+    case 3: launch_g<3, MODE>(a, tiles, BH, em, st); break;
+    case 4: launch_g<4, MODE>(a, tiles, BH, em, st); break;
+    case 5: launch_g<5, MODE>(a, tiles, BH, em, st); break;
+    case 6: launch_g<6, MODE>(a, tiles, BH, em, st); break;
+    case 7: launch_g<7, MODE>(a, tiles, BH, em, st); break;
+    default: launch_g<8, MODE>(a, tiles, BH, em, st); break;
   }
-  return launch_status(staged ? "scan_staged_kernel" : "scan_direct_kernel");
-}
-
-// Stores in pinned host memory take the staged kernel (whole-run PCIe reads),
-// as do superblock sizes that do not hold whole 8-block groups.
-bool use_staged(const void *planes, int64_t sub) {
-  if (sub % kGB != 0) return true;
-  hipPointerAttribute_t attr;
-  hipError_t e = hipPointerGetAttributes(&attr, planes);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return true;
-  }
-  return attr.type == hipMemoryTypeHost;
+  return launch_status("scan_tile_kernel");
 }
 
 int check_scan(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
@@ -516,7 +536,7 @@ extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t
   const int64_t tiles = cdiv(blk_end, kTB) - a.tile0;
   Emit em{};
   em.out = out;
-  return launch_scan<kEmitScores>(a, G, tiles, BH, use_staged(planes_sb, sub), em, (hipStream_t)stream);
+  return launch_scan<kEmitScores>(a, G, tiles, BH, em, (hipStream_t)stream);
 }
 
 extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink,
@@ -548,18 +568,17 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   em.sink = sink;
   em.lstart = (m - local) > 0 ? (m - local) : 0;
   const int64_t nblk = cdiv(n, kBlk);
-  const bool staged = use_staged(planes_sb, sub);
   ScanArgs a = make_args(q, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub);
   a.blk0 = 0;
   a.blk_end = nblk;
   a.tile0 = 0;
   a.tile_stride = S;
-  rc = launch_scan<kEmitSample>(a, G, topk_sample_tiles(n, S), BH, staged, em, st);
+  rc = launch_scan<kEmitSample>(a, G, topk_sample_tiles(n, S), BH, em, st);
   if (rc) return rc;
   rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, em.sel, st);
   if (rc) return rc;
   a.tile_stride = 1;
-  rc = launch_scan<kEmitFilter>(a, G, cdiv(nblk, kTB), BH, staged, em, st);
+  rc = launch_scan<kEmitFilter>(a, G, cdiv(nblk, kTB), BH, em, st);
   if (rc) return rc;
   return launch_finalize(rows, m, k, sink, local, em.sel, idx, st);
 }
