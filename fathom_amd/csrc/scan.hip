@@ -57,8 +57,9 @@ struct Emit {
   float *out;        // scores [BH, G, n]
   uint32_t *samp;    // sampled keys [BH*G, samp_cap]
   int64_t samp_cap;
-  TopkSel sel;       // threshold + candidate lists
+  TopkSel sel;       // thresholds + candidate lists
   int64_t sink, lstart;
+  int fallback;      // candidate mode: the fallback pass (threshold T_lo, rows whose first pass found < kk)
 };
 
 struct ScanArgs {
@@ -136,8 +137,8 @@ __device__ __forceinline__ void accum(Acc<G> &acc, int b, const QOp<G> &q, float
 //  * deeper: y = 2a * x = c * P + Q with P = 2a, Q = -(2^C - 1) a and c the
 //    C-bit code: one fused multiply-add of exact operands (c < 16, a fp16).
 template <int C>
-__device__ __forceinline__ float lane_value(const uint32_t (&dw)[C], int l31, float P, float Q) {
-  if (C == 1) return __uint_as_float(((dw[0] << (31 - l31)) & 0x80000000u) | __float_as_uint(P));
+__device__ __forceinline__ float lane_value(const uint32_t (&dw)[C], int l31, uint32_t sign, float P, float Q) {
+  if (C == 1) return __uint_as_float(((dw[0] << (31 - l31)) & sign) | __float_as_uint(P));
   uint32_t c = __builtin_amdgcn_ubfe(dw[0], l31, 1);
 #pragma unroll
   for (int p = 1; p < C; ++p) c = (c << 1) + __builtin_amdgcn_ubfe(dw[p], l31, 1);
@@ -173,9 +174,16 @@ __device__ __forceinline__ void emit_filter(const Emit &em, EmitShared<G> &es, c
   const int64_t t0 = gb0 * kBlk, t1 = t0 + kGB * kBlk;
   // no per-lane validity or sink/local masking anywhere in the wave's blocks
   const bool plain = gb0 >= blk0 && gb0 + kGB <= blk_end && t1 <= n && t0 >= em.sink && t1 <= em.lstart;
+  // the pass's threshold per head; in the fallback pass, heads whose first pass
+  // found kk candidates emit nothing
   float thr_f[G];
+  bool skip[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) thr_f[g] = threshold_value(ld_uniform(em.sel.thr + bh * G + g));
+  for (int g = 0; g < G; ++g) {
+    skip[g] = em.fallback && ld_uniform(em.sel.cand_cnt + bh * G + g) >= em.sel.kk;
+    thr_f[g] = threshold_value(ld_uniform((em.fallback ? em.sel.thr_lo : em.sel.thr) + bh * G + g));
+  }
+  uint32_t *const gcnt = em.fallback ? em.sel.cand2_cnt : em.sel.cand_cnt;
   auto masked_value = [&](int r, int g, bool &valid) -> float {
     const float v = acc.get(r, g);
     if (plain) {
@@ -190,6 +198,7 @@ __device__ __forceinline__ void emit_filter(const Emit &em, EmitShared<G> &es, c
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     cnt[g] = 0u;
+    if (skip[g]) continue;
 #pragma unroll
     for (int r = 0; r < kGB; ++r) {
       bool valid;
@@ -208,7 +217,7 @@ __device__ __forceinline__ void emit_filter(const Emit &em, EmitShared<G> &es, c
   __syncthreads();
   if (tid < G) {
     const uint32_t c = es.wcnt[tid];
-    es.gbase[tid] = c ? atomicAdd(&em.sel.cand_cnt[bh * G + tid], c) : 0u;
+    es.gbase[tid] = c ? atomicAdd(&gcnt[bh * G + tid], c) : 0u;
   }
   __syncthreads();
 #pragma unroll
@@ -288,19 +297,22 @@ __device__ __forceinline__ int unit_channel(int u, int c) {
   return c == 0 ? u : c == 1 ? (u >> 1) : c == 2 ? ((u * 11) >> 5) : (u >> 2);
 }
 
-// A staged chunk: low and high dword of each unit's 32 block words, and the
-// scale pair (P, Q) of each channel slot's 32 blocks.
+// A staged chunk: low and high dword of each unit's 32 block words, the scale
+// pair (P, Q) of each channel slot's 32 blocks, and each slot's head weights.
+template <int G>
 struct ChunkBuf {
-  uint32_t lo[kUnits][kTB];
-  uint32_t hi[kUnits][kTB];
-  float2 sc[kUnits][kTB];
+  alignas(16) uint32_t lo[kUnits][kTB];
+  alignas(16) uint32_t hi[kUnits][kTB];
+  alignas(16) float P[kUnits][kTB];
+  alignas(16) float Q[kUnits][kTB];
+  alignas(16) float w[kUnits][QShared<G>::QS];
 };
 
 template <int G>
 struct TileShared {
   QShared<G> qs;
   uint8_t lst[4][kMaxD];  // the plan's class lists, clamped to [0, D)
-  ChunkBuf buf[2];
+  ChunkBuf<G> buf[2];
 };
 
 // The words and scales one thread stages: block bi = tid % 32 of units and
@@ -332,14 +344,21 @@ __device__ __forceinline__ void load_chunk(Staged &r, const ScanArgs &a, const u
   }
 }
 
-__device__ __forceinline__ void store_chunk(ChunkBuf &b, const Staged &r, int c, int slot, int bi) {
+// Writes a loaded chunk to LDS; the head weights of its channel slots come from
+// the workgroup's weight table (thread (slot, bi < QS) copies slot's weight bi).
+template <int G>
+__device__ __forceinline__ void store_chunk(ChunkBuf<G> &b, const Staged &r, const QShared<G> &qs,
+                                            const uint8_t (*lst)[kMaxD], const Chunk &ck, int slot, int bi) {
+  constexpr int QS = QShared<G>::QS;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int u = slot + 8 * h;
     b.lo[u][bi] = (uint32_t)r.w[h];
     b.hi[u][bi] = (uint32_t)(r.w[h] >> 32);
     const float a = __half2float(__ushort_as_half(r.s[h]));
-    b.sc[u][bi] = c == 0 ? make_float2(0.5f * a, 0.0f) : make_float2(2.0f * a, -(float)((2 << c) - 1) * a);
+    b.P[u][bi] = ck.c == 0 ? 0.5f * a : 2.0f * a;
+    b.Q[u][bi] = ck.c == 0 ? 0.0f : -(float)((2 << ck.c) - 1) * a;
+    if (bi < QS && u < ck.m) b.w[u][bi] = qs.w[lst[ck.c][ck.i0 + u] * QS + bi];
   }
 }
 
@@ -347,17 +366,21 @@ __device__ __forceinline__ void store_chunk(ChunkBuf &b, const Staged &r, int c,
 // order, four blocks per half: one 16-byte LDS read per (plane, half) brings the
 // lane's four dwords, two more the four scale pairs.
 template <int C, int G>
-__device__ __forceinline__ void compute_chunk(const ChunkBuf &b, const QShared<G> &qs, const uint8_t *lst, int m,
-                                              int wave, int lane, Acc<G> &acc) {
+__device__ __forceinline__ void compute_chunk(const ChunkBuf<G> &b, int m, int wave, int lane, uint32_t sign,
+                                              Acc<G> &acc) {
+  constexpr int QS = QShared<G>::QS;
   const int l31 = lane & 31;
   const uint32_t *wl = (lane < 32 ? &b.lo[0][0] : &b.hi[0][0]) + wave * kGB;
   for (int ci = 0; ci < m; ++ci) {
-    const QOp<G> q = load_qop<G>(qs, lst[ci], lane);
+    QOp<G> q;
+#pragma unroll
+    for (int h = 0; h < QOp<G>::NQ; ++h) q.a[h] = b.w[ci][4 * h + (lane & 3)];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const float4 s01 = *reinterpret_cast<const float4 *>(&b.sc[ci][wave * kGB + 4 * hf]);
-      const float4 s23 = *reinterpret_cast<const float4 *>(&b.sc[ci][wave * kGB + 4 * hf + 2]);
-      const float P[4] = {s01.x, s01.z, s23.x, s23.z}, Q[4] = {s01.y, s01.w, s23.y, s23.w};
+      const float4 P4 = *reinterpret_cast<const float4 *>(&b.P[ci][wave * kGB + 4 * hf]);
+      float4 Q4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (C > 1) Q4 = *reinterpret_cast<const float4 *>(&b.Q[ci][wave * kGB + 4 * hf]);
+      const float P[4] = {P4.x, P4.y, P4.z, P4.w}, Q[4] = {Q4.x, Q4.y, Q4.z, Q4.w};
       uint4 dq[C];
 #pragma unroll
       for (int p = 0; p < C; ++p) dq[p] = *reinterpret_cast<const uint4 *>(wl + (ci * C + p) * kTB + 4 * hf);
@@ -367,7 +390,7 @@ __device__ __forceinline__ void compute_chunk(const ChunkBuf &b, const QShared<G
         uint32_t dw[C];
 #pragma unroll
         for (int p = 0; p < C; ++p) dw[p] = r == 0 ? dq[p].x : r == 1 ? dq[p].y : r == 2 ? dq[p].z : dq[p].w;
-        y[r] = lane_value<C>(dw, l31, P[r], Q[r]);
+        y[r] = lane_value<C>(dw, l31, sign, P[r], Q[r]);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) accum<G>(acc, 4 * hf + r, q, y[r]);
@@ -405,6 +428,12 @@ __global__ __launch_bounds__(kThreads) void scan_tile_kernel(ScanArgs a, Emit em
   const int64_t bh = blockIdx.y;
   const int64_t tile = a.tile0 + (int64_t)blockIdx.x * a.tile_stride;
   const int64_t tb0 = tile * kTB;
+  if (MODE == kEmitFilter && em.fallback) {  // uniform: skip the tile unless one of its rows needs the pass
+    bool need = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) need |= ld_uniform(em.sel.cand_cnt + bh * G + g) < em.sel.kk;
+    if (!need) return;
+  }
   int nc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) nc[c] = c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
@@ -424,10 +453,13 @@ __global__ __launch_bounds__(kThreads) void scan_tile_kernel(ScanArgs a, Emit em
   for (int c = 0; c < 4; ++c) nk += (nc[c] + chunk_channels(c) - 1) / chunk_channels(c);
   if (tb0 < a.blk_end && tb0 + kTB > a.blk0 && nk > 0) {  // uniform over the workgroup
     Staged r;
+    // the sign-bit mask as an opaque VGPR value (VOP3 encodings take no literal)
+    uint32_t sign;
+    asm("v_mov_b32 %0, 0x80000000" : "=v"(sign));
     __syncthreads();  // class lists and weights ready
     Chunk nxt = chunk_at(nc, 0);
     load_chunk(r, a, sh.lst, nxt, slot, inb, pbase, sbase);
-    store_chunk(sh.buf[0], r, nxt.c, slot, bi);
+    store_chunk<G>(sh.buf[0], r, sh.qs, sh.lst, nxt, slot, bi);
     __syncthreads();
     int k = 0;
     // classes in order, each a loop over its chunks with the depth known at
@@ -443,13 +475,13 @@ __global__ __launch_bounds__(kThreads) void scan_tile_kernel(ScanArgs a, Emit em
           nxt = chunk_at(nc, k + 1);
           load_chunk(r, a, sh.lst, nxt, slot, inb, pbase, sbase);
         }
-        const ChunkBuf &cb = sh.buf[k & 1];
+        const ChunkBuf<G> &cb = sh.buf[k & 1];
         const int m = min(cpc, nc[c] - i0);
-        if (c == 0) compute_chunk<kC[0], G>(cb, sh.qs, sh.lst[0] + i0, m, wave, lane, acc);
-        if (c == 1) compute_chunk<kC[1], G>(cb, sh.qs, sh.lst[1] + i0, m, wave, lane, acc);
-        if (c == 2) compute_chunk<kC[2], G>(cb, sh.qs, sh.lst[2] + i0, m, wave, lane, acc);
-        if (c == 3) compute_chunk<kC[3], G>(cb, sh.qs, sh.lst[3] + i0, m, wave, lane, acc);
-        if (more) store_chunk(sh.buf[(k + 1) & 1], r, nxt.c, slot, bi);
+        if (c == 0) compute_chunk<kC[0], G>(cb, m, wave, lane, sign, acc);
+        if (c == 1) compute_chunk<kC[1], G>(cb, m, wave, lane, sign, acc);
+        if (c == 2) compute_chunk<kC[2], G>(cb, m, wave, lane, sign, acc);
+        if (c == 3) compute_chunk<kC[3], G>(cb, m, wave, lane, sign, acc);
+        if (more) store_chunk<G>(sh.buf[(k + 1) & 1], r, sh.qs, sh.lst, nxt, slot, bi);
         __syncthreads();
       }
     }
@@ -565,6 +597,8 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   Emit em{};
   int64_t S = 1;
   topk_layout(rows, n, k, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
+  em.sel.kk = (uint32_t)kk;
+  const int64_t r_hi = topk_hi_rank(n, S, kk);
   em.sink = sink;
   em.lstart = (m - local) > 0 ? (m - local) : 0;
   const int64_t nblk = cdiv(n, kBlk);
@@ -575,10 +609,15 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   a.tile_stride = S;
   rc = launch_scan<kEmitSample>(a, G, topk_sample_tiles(n, S), BH, em, st);
   if (rc) return rc;
-  rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, em.sel, st);
+  rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, r_hi, em.sel, st);
   if (rc) return rc;
   a.tile_stride = 1;
   rc = launch_scan<kEmitFilter>(a, G, cdiv(nblk, kTB), BH, em, st);
   if (rc) return rc;
+  if (r_hi < kk) {  // T_hi may exceed a row's kk-th largest key: rows with < kk candidates scan again with T_lo
+    em.fallback = 1;
+    rc = launch_scan<kEmitFilter>(a, G, cdiv(nblk, kTB), BH, em, st);
+    if (rc) return rc;
+  }
   return launch_finalize(rows, m, k, sink, local, em.sel, idx, st);
 }

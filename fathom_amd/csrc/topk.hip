@@ -143,12 +143,14 @@ __device__ __forceinline__ uint32_t masked_key(const float *row, int64_t i, int6
   return (i < sink || i >= lstart) ? kKeyNegInf : score_key(row[i]);
 }
 
-// Threshold of a row from its sampled keys: each thread keeps its M largest
-// keys and T is the kk-th largest of those M * 1024 values.  They are kk
-// elements of the sample >= T, so T <= the sample's kk-th largest <= the row's:
-// every element of the row's top kk has key >= T.
+// Thresholds of a row from its sampled keys: each thread keeps its M largest
+// keys; T_lo is the kk-th largest of those M * 1024 values.  They are kk
+// elements of the sample >= T_lo, so T_lo <= the sample's kk-th largest <= the
+// row's: every element of the row's top kk has key >= T_lo.  T_hi is the
+// r_hi-th largest of the same values (r_hi <= kk, so T_hi >= T_lo).
 template <int M>
-__device__ uint32_t sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint64_t *vals, RangeShared &sh) {
+__device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t r_hi, uint64_t *vals,
+                             RangeShared &sh, uint32_t &t_lo, uint32_t &t_hi) {
   uint32_t top[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) top[i] = 0u;
@@ -166,11 +168,18 @@ __device__ uint32_t sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint
   for (int i = 0; i < M; ++i) vals[threadIdx.x * M + i] = (uint64_t)top[i] << 32;
   __syncthreads();
   const uint64_t t = range_select([&](int64_t i) { return vals[i]; }, (int64_t)M * kSelThreads, kk, sh);
-  return (uint32_t)(t >> 32);
+  t_lo = (uint32_t)(t >> 32);
+  t_hi = t_lo;
+  if (r_hi < kk) {
+    __syncthreads();
+    const uint64_t th = range_select([&](int64_t i) { return vals[i]; }, (int64_t)M * kSelThreads, r_hi, sh);
+    t_hi = (uint32_t)(th >> 32);
+  }
 }
 
 __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t *__restrict__ samp,
-                                                                  int64_t samp_cap, uint32_t kk, TopkSel s) {
+                                                                  int64_t samp_cap, uint32_t kk, uint32_t r_hi,
+                                                                  TopkSel s) {
   __shared__ RangeShared sh;
   __shared__ uint64_t vals[4 * kSelThreads];
   const int64_t row = blockIdx.x;
@@ -181,18 +190,20 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
     const int64_t i = threadIdx.x + (int64_t)u * kSelThreads;
     v[u] = i < samp_cap ? src[i] : 0u;
   }
-  uint32_t thr = 0u;  // fewer samples than kk: every element is a candidate
+  uint32_t t_lo = 0u, t_hi = 0u;  // fewer samples than kk: every element is a candidate
   if (samp_cap >= (int64_t)kk) {
     if (2 * kk <= kSelThreads)
-      thr = sample_bound<1>(v, kk, vals, sh);
+      sample_bound<1>(v, kk, r_hi, vals, sh, t_lo, t_hi);
     else if (kk <= kSelThreads)
-      thr = sample_bound<2>(v, kk, vals, sh);
+      sample_bound<2>(v, kk, r_hi, vals, sh, t_lo, t_hi);
     else
-      thr = sample_bound<4>(v, kk, vals, sh);
+      sample_bound<4>(v, kk, r_hi, vals, sh, t_lo, t_hi);
   }
   if (threadIdx.x == 0) {
-    s.thr[row] = thr;
+    s.thr[row] = t_hi;
+    s.thr_lo[row] = t_lo;
     s.cand_cnt[row] = 0u;
+    s.cand2_cnt[row] = 0u;
   }
 }
 
@@ -213,13 +224,16 @@ __global__ __launch_bounds__(256) void sample_scores_kernel(const float *__restr
 // and step when rows are 16-byte aligned.
 template <bool VEC>
 __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const float *__restrict__ scores, int64_t n,
-                                                                       int64_t sink, int64_t lstart, TopkSel s) {
+                                                                       int64_t sink, int64_t lstart, TopkSel s,
+                                                                       bool fallback) {
   __shared__ uint64_t lbuf[kFilterLocal];
   __shared__ uint32_t lcnt, lbase;
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t row = blockIdx.y;
+  if (fallback && s.cand_cnt[row] >= s.kk) return;  // the first pass holds the row's top kk
   const float *rs = scores + row * n;
-  const uint32_t thr = s.thr[row];
+  const uint32_t thr = fallback ? s.thr_lo[row] : s.thr[row];
+  uint32_t *cnt = fallback ? &s.cand2_cnt[row] : &s.cand_cnt[row];
   uint64_t *cand = s.cand + row * s.cand_cap;
   if (tid == 0) lcnt = 0u;
   __syncthreads();
@@ -236,7 +250,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const flo
         const int64_t iu = i + u;
         const bool in = iu < end;
         const uint32_t key = in ? ((iu < sink || iu >= lstart) ? kKeyNegInf : score_key(fv[u])) : 0u;
-        wave_append_local(in && key >= thr, k64_of(key, iu), &lcnt, lbuf, kFilterLocal, &s.cand_cnt[row], cand,
+        wave_append_local(in && key >= thr, k64_of(key, iu), &lcnt, lbuf, kFilterLocal, cnt, cand,
                           (uint64_t)s.cand_cap, lane);
       }
     }
@@ -245,12 +259,12 @@ __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const flo
       const int64_t i = i0 + tid;
       const bool in = i < end;
       const uint32_t key = in ? masked_key(rs, i, sink, lstart) : 0u;
-      wave_append_local(in && key >= thr, k64_of(key, i), &lcnt, lbuf, kFilterLocal, &s.cand_cnt[row], cand,
+      wave_append_local(in && key >= thr, k64_of(key, i), &lcnt, lbuf, kFilterLocal, cnt, cand,
                         (uint64_t)s.cand_cap, lane);
     }
   }
   __syncthreads();
-  flush_local(&lcnt, lbuf, kFilterLocal, &s.cand_cnt[row], cand, (uint64_t)s.cand_cap, &lbase);
+  flush_local(&lcnt, lbuf, kFilterLocal, cnt, cand, (uint64_t)s.cand_cap, &lbase);
 }
 
 // Exact top kk of a row's candidates, sorted by K64 descending (score
@@ -265,7 +279,8 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t kk = k - sink - local;
-  const int64_t cnt = min((int64_t)s.cand_cnt[row], s.cand_cap);
+  const uint32_t c1 = s.cand_cnt[row];  // the fallback pass ran for rows whose first pass found < kk
+  const int64_t cnt = min((int64_t)(c1 >= s.kk ? c1 : s.cand2_cnt[row]), s.cand_cap);
   const uint64_t *gc = s.cand + row * s.cand_cap;
   int64_t *out = idx + row * k;
   const bool in_lds = cnt <= kCandLds;
@@ -333,16 +348,18 @@ __global__ __launch_bounds__(256) void fixed_only_kernel(int64_t rows, int64_t m
 }  // namespace
 
 size_t topk_sel_layout(int64_t rows, int64_t cand_cap, char *base, TopkSel *s) {
-  const size_t thr_b = ws_align((size_t)rows * 4);
-  const size_t cnt_b = ws_align((size_t)rows * 4);
+  const size_t row_b = ws_align((size_t)rows * 4);  // thr, thr_lo, cand_cnt, cand2_cnt
   const size_t cand_b = ws_align((size_t)rows * (size_t)cand_cap * 8);
   if (s) {
     s->thr = reinterpret_cast<uint32_t *>(base);
-    s->cand_cnt = reinterpret_cast<uint32_t *>(base + thr_b);
-    s->cand = reinterpret_cast<uint64_t *>(base + thr_b + cnt_b);
+    s->thr_lo = reinterpret_cast<uint32_t *>(base + row_b);
+    s->cand_cnt = reinterpret_cast<uint32_t *>(base + 2 * row_b);
+    s->cand2_cnt = reinterpret_cast<uint32_t *>(base + 3 * row_b);
+    s->cand = reinterpret_cast<uint64_t *>(base + 4 * row_b);
     s->cand_cap = cand_cap;
+    s->kk = 0u;
   }
-  return thr_b + cnt_b + cand_b;
+  return 4 * row_b + cand_b;
 }
 
 size_t topk_layout(int64_t rows, int64_t n, int64_t k, char *base, uint32_t **samp, int64_t *samp_cap, TopkSel *sel,
@@ -357,9 +374,10 @@ size_t topk_layout(int64_t rows, int64_t n, int64_t k, char *base, uint32_t **sa
   return samp_b + topk_sel_layout(rows, n, base ? base + samp_b : nullptr, sel);
 }
 
-int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, TopkSel s, hipStream_t st) {
+int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, int64_t r_hi, TopkSel s,
+                       hipStream_t st) {
   if (samp_cap > kMaxSample) return fail(FATHOM_ERR_INVALID, "select: %lld sampled keys exceed %lld", (long long)samp_cap, (long long)kMaxSample);
-  select_keys_kernel<<<(unsigned)rows, kSelThreads, 0, st>>>(samp, samp_cap, (uint32_t)kk, s);
+  select_keys_kernel<<<(unsigned)rows, kSelThreads, 0, st>>>(samp, samp_cap, (uint32_t)kk, (uint32_t)r_hi, s);
   return launch_status("select_keys_kernel");
 }
 
@@ -371,12 +389,12 @@ int launch_sample_scores(const float *scores, int64_t rows, int64_t n, int64_t S
 }
 
 int launch_filter_scores(const float *scores, int64_t rows, int64_t n, int64_t sink, int64_t lstart, TopkSel s,
-                         hipStream_t st) {
+                         bool fallback, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(n, kFilterChunk), (unsigned)rows);
   if (n % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0)
-    filter_scores_kernel<true><<<grid, kFilterThreads, 0, st>>>(scores, n, sink, lstart, s);
+    filter_scores_kernel<true><<<grid, kFilterThreads, 0, st>>>(scores, n, sink, lstart, s, fallback);
   else
-    filter_scores_kernel<false><<<grid, kFilterThreads, 0, st>>>(scores, n, sink, lstart, s);
+    filter_scores_kernel<false><<<grid, kFilterThreads, 0, st>>>(scores, n, sink, lstart, s, fallback);
   return launch_status("filter_scores_kernel");
 }
 
@@ -431,12 +449,18 @@ extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t
   uint32_t *samp = nullptr;
   int64_t samp_cap = 0, S = 1;
   topk_layout(rows, n, k, static_cast<char *>(workspace), &samp, &samp_cap, &s, &S);
+  s.kk = (uint32_t)kk;
   const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
+  const int64_t r_hi = topk_hi_rank(n, S, kk);
   rc = launch_sample_scores(scores, rows, n, S, sink, lstart, samp, samp_cap, st);
   if (rc) return rc;
-  rc = launch_select_keys(samp, rows, samp_cap, kk, s, st);
+  rc = launch_select_keys(samp, rows, samp_cap, kk, r_hi, s, st);
   if (rc) return rc;
-  rc = launch_filter_scores(scores, rows, n, sink, lstart, s, st);
+  rc = launch_filter_scores(scores, rows, n, sink, lstart, s, false, st);
   if (rc) return rc;
+  if (r_hi < kk) {  // T_hi may exceed a row's kk-th largest key
+    rc = launch_filter_scores(scores, rows, n, sink, lstart, s, true, st);
+    if (rc) return rc;
+  }
   return launch_finalize(rows, m, k, sink, local, s, idx, st);
 }

@@ -1,16 +1,22 @@
 // Selection machinery shared by the standalone top-k and the fused scan+top-k.
 //
-// Exact top-kk of a row in three steps:
-//   select    the exact kk-th largest key T of a sample of the row (tiles of
-//             1024 tokens, every S-th tile).  A sample is a subset of the row,
-//             so T never exceeds the row's kk-th largest key: every element of
-//             the top kk has key >= T;
-//   filter    elements with key >= T are appended to the row's candidate list
-//             (about S * kk of them for a representative sample);
+// Exact top-kk of a row in four steps:
+//   select    from a sample of the row (tiles of 2048 tokens, every S-th
+//             tile): T_lo, a lower bound of the sample's kk-th largest key,
+//             and T_hi, a lower bound of its r-th largest, r = about
+//             kAlpha * kk * (sample size / n).  A sample is a subset of the
+//             row, so T_lo never exceeds the row's kk-th largest key; T_hi is
+//             a guess that about kAlpha * kk elements of the row reach;
+//   filter    elements with key >= T_hi are appended to the row's candidate
+//             list.  If at least kk were appended, T_hi <= the row's kk-th
+//             largest key and the list holds the whole top kk;
+//   fallback  rows with fewer than kk candidates (a sample that was not
+//             representative) are filtered again with T_lo, into the same list
+//             under a second counter; other rows skip the pass;
 //   finalize  one workgroup per row selects the exact kk largest candidates by
 //             K64 = key << 32 | (0xFFFFFFFF - index) and writes them sorted.
-// Exactness never depends on the sample: a poor sample only yields more
-// candidates (the list holds a whole row, so it cannot overflow).
+// Exactness never depends on the sample: a poor sample only costs a fallback
+// pass or more candidates (the list holds a whole row, so it cannot overflow).
 #pragma once
 #include "common.hpp"
 
@@ -19,11 +25,16 @@ namespace fathom {
 constexpr int64_t kTileTok = 2048;  // tokens per scan tile (32 blocks)
 constexpr int64_t kMaxSample = 65536; // sampled keys per row (held in registers by select)
 
+constexpr int64_t kAlpha = 4;  // expected first-pass candidates per row, in units of kk
+
 struct TopkSel {
-  uint32_t *thr;       // [rows] threshold key
-  uint32_t *cand_cnt;  // [rows] candidates appended
-  uint64_t *cand;      // [rows, cand_cap] K64 candidates
+  uint32_t *thr;        // [rows] first-pass threshold key T_hi
+  uint32_t *thr_lo;     // [rows] safe threshold key T_lo
+  uint32_t *cand_cnt;   // [rows] candidates of the first pass
+  uint32_t *cand2_cnt;  // [rows] candidates of the fallback pass
+  uint64_t *cand;       // [rows, cand_cap] K64 candidates (of the pass in effect)
   int64_t cand_cap;
+  uint32_t kk;
 };
 
 // Sample stride in tiles: about 8192 / kk expected candidates per row while
@@ -41,6 +52,18 @@ inline int64_t topk_tile_stride(int64_t n, int64_t kk) {
 
 inline int64_t topk_sample_tiles(int64_t n, int64_t S) { return cdiv(cdiv(n, kTileTok), S); }
 
+// Rank in the sample of the first-pass threshold: about kAlpha * kk of the row's
+// n elements are expected at or above it (kk when the sample is the row).
+inline int64_t topk_hi_rank(int64_t n, int64_t S, int64_t kk) {
+  int64_t sampled = 0;
+  for (int64_t t = 0, nt = topk_sample_tiles(n, S); t < nt; ++t) {
+    const int64_t left = n - t * S * kTileTok;
+    sampled += left < kTileTok ? (left > 0 ? left : 0) : kTileTok;
+  }
+  const int64_t r = (kAlpha * kk * sampled + n - 1) / n;
+  return r < 1 ? 1 : (r > kk ? kk : r);
+}
+
 // 256-byte section alignment inside workspaces
 inline size_t ws_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -53,11 +76,14 @@ size_t topk_sel_layout(int64_t rows, int64_t cand_cap, char *base, TopkSel *s);
 size_t topk_layout(int64_t rows, int64_t n, int64_t k, char *base, uint32_t **samp, int64_t *samp_cap, TopkSel *sel,
                    int64_t *S_out);
 
-int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, TopkSel s, hipStream_t st);
+// T_lo (rank kk) and T_hi (rank r_hi <= kk) of every row's sample; clears the counters.
+int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, int64_t r_hi, TopkSel s,
+                       hipStream_t st);
 int launch_sample_scores(const float *scores, int64_t rows, int64_t n, int64_t S, int64_t sink, int64_t lstart,
                          uint32_t *samp, int64_t samp_cap, hipStream_t st);
+// First pass (fallback = false) or fallback pass (rows whose first pass found fewer than kk).
 int launch_filter_scores(const float *scores, int64_t rows, int64_t n, int64_t sink, int64_t lstart, TopkSel s,
-                         hipStream_t st);
+                         bool fallback, hipStream_t st);
 int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, TopkSel s, int64_t *idx,
                     hipStream_t st);
 // kk == 0: only the sink and local positions are written.

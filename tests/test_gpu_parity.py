@@ -234,6 +234,26 @@ def test_topk_huge_tie_bucket_slow_path():
     _topk_case(np.ones((1, 70000), np.float32), 300, 4, 32)
 
 
+@pytest.mark.parametrize("order", ["falling", "rising", "front_block"])
+def test_topk_tight_threshold_fallback(order):
+    """Score orders the sampled tiles misrepresent: falling scores put the row's
+    top in sampled tile 0, so the tight first-pass threshold admits fewer than
+    kk elements and the fallback pass runs; the result stays exact."""
+    print(f"[topk] order={order}", flush=True)
+    n = 120000
+    idx = np.arange(n, dtype=np.float32)
+    if order == "falling":
+        row = -idx
+    elif order == "rising":
+        row = idx.copy()
+    else:  # a large block of equal top scores at the start, noise after
+        row = np.random.default_rng(4).standard_normal(n).astype(np.float32)
+        row[: 3000] = 10.0
+    rows = np.stack([row, row[::-1].copy()])[None].astype(np.float32)
+    _topk_case(rows, 512, 4, 32)
+    _topk_case(rows, 2048, 4, 32)
+
+
 def test_topk_config3_rows():
     print("[topk] 32 x 1M", flush=True)
     rng = np.random.default_rng(3)
@@ -364,6 +384,29 @@ def test_scan_topk_fused_host_resident():
     finally:
         off.free_host(hp1)
         off.free_host(hp2)
+
+
+@pytest.mark.parametrize("direction", [1.0, -1.0])
+def test_scan_topk_fallback_pass(direction):
+    """Fused path with scores falling (or rising) along the sequence: a falling
+    row has its top kk inside the first sampled tile, so the tight threshold
+    falls short and the fallback scan runs; the result equals the unfused one."""
+    print(f"[fused-fallback] direction={direction}", flush=True)
+    BH, n, d = 2, 90000, 128
+    K = torch.zeros(BH, n, d)
+    K[:, :, 0] = torch.linspace(1, -1, n)[None] * 3.0 * direction
+    K[:, :, 1] = torch.randn(BH, n) * 0.01
+    st = bp.PlaneStore(K.to(DEV))
+    q = torch.zeros(BH, 4, d)
+    q[:, :, 0] = 1.0
+    q[:, 1::2, 1] = 1.0
+    g = torch.ones(BH, d)
+    g[:, 0] = 1000.0
+    g[:, 1] = 10.0
+    plan = bp.make_plan(g.to(DEV), 6.0)
+    ref = bp.sink_local_topk(st.scan(q.to(DEV), plan), 512)
+    got = st.scan_topk(q.to(DEV), plan, 512)
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
 
 
 def test_scan_topk_adversarial_order():
