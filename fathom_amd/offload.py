@@ -10,6 +10,11 @@
   recent tokens (index >= n) come from a device buffer.
 * select_and_gather: plan -> scan -> sink/local top-k -> union gather, the
   selection half of offload_attn (scripts/B_e2e_offload_v2.py:163-242).
+* gather_runs / host_store / copy_index: the copy-index path
+  (scripts/B_e2e_offload_v2.py:62-71, 190-197, 267): a store in the
+  whole-sequence layout (SUB = nblk) in mapped host memory, whose plan-selected
+  runs (first t planes and the scales of every listed channel) are copied into
+  an HBM staging store of the same layout and scanned there.
 """
 import ctypes
 import math
@@ -50,6 +55,74 @@ def host_mapped(t, coherent=True):
 
 def free_host(hp):
     _lib.call("fathom_host_free", ctypes.c_void_p(hp))
+
+
+def gather_runs(src, dst, off, ln, nrun, max_len, CH=4096):
+    """Copy run r (4-byte words [off[r], off[r] + ln[r]) of src) to the same words of
+    dst for r < nrun[0]; off/ln [R] and nrun [1] are device tensors, so no host sync
+    -- scripts/B_e2e_offload_v2.py:62-71.  src/dst: tensors or DevPtr; CH is the
+    reference's launch parameter (accepted, unused)."""
+    _need_gpu(off, ln, nrun)
+    off64 = off.contiguous().to(torch.int64)
+    ln64 = ln.contiguous().to(torch.int64)
+    nr = nrun.contiguous().to(torch.int32)
+    _lib.call("fathom_gather_runs", ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), _ptr(off64),
+              _ptr(ln64), _ptr(nr), int(off64.shape[0]), int(max_len), _stream(off.device))
+
+
+def host_store(store):
+    """A copy of a whole-sequence-layout PlaneStore (built with bitplane.SUB = nblk)
+    whose planes and scales live in mapped pinned host memory: the returned store's
+    planes32 / scales_k are DevPtr objects, as the reference's offload does
+    (scripts/B_e2e_offload_v2.py:267, 296-309).  Returns (store, host pointers to
+    free with free_host)."""
+    if store.nsb != 1:
+        raise ValueError("copy-index stores use the whole-sequence layout: build them with bitplane.SUB = nblk")
+    from .bitplane import PlaneStore
+    _, pl, h1 = host_mapped(store.planes_k)
+    try:
+        _, sc, h2 = host_mapped(store.scales_k)
+    except Exception:
+        free_host(h1)
+        raise
+    hs = PlaneStore.__new__(PlaneStore)
+    hs.BH, hs.n, hs.nsb, hs.sub = store.BH, store.n, store.nsb, store.sub
+    hs.code, hs.scales_blk = None, None
+    hs.planes32, hs.scales_k = pl, sc
+    return hs, (h1, h2)
+
+
+def staging_store(store, device=None):
+    """An HBM PlaneStore with store's shape and whole-sequence layout, planes and
+    scales zeroed: the target of copy_index."""
+    if store.nsb != 1:
+        raise ValueError("copy-index stores use the whole-sequence layout: build them with bitplane.SUB = nblk")
+    from .bitplane import PlaneStore
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    st = PlaneStore.__new__(PlaneStore)
+    st.BH, st.n, st.nsb, st.sub = store.BH, store.n, 1, store.sub
+    st.code, st.scales_blk = None, None
+    st.planes_k = torch.zeros(store.BH, 1, D, 4, store.sub, dtype=torch.int64, device=dev)
+    st.scales_k = torch.zeros(store.BH, 1, D, store.sub, dtype=torch.float16, device=dev)
+    st.planes32 = st.planes_k.view(torch.int32)
+    return st
+
+
+def copy_index(src, staging, plan):
+    """Stage the plan's runs -- the first t planes of every listed channel and its
+    scales -- from src (a host_store) into staging (an HBM PlaneStore of the same
+    whole-sequence layout), at the same offsets; no host sync
+    (scripts/B_e2e_offload_v2.py:190-197).  Scanning staging afterwards equals
+    scanning the full store."""
+    t = plan["t"]
+    _need_gpu(t)
+    tt = t.contiguous().to(torch.int8)
+    if src.nsb != 1 or staging.nsb != 1 or (src.BH, src.n, src.sub) != (staging.BH, staging.n, staging.sub):
+        raise ValueError("copy_index needs two whole-sequence-layout stores of the same shape")
+    BH, d = tt.shape
+    _lib.call("fathom_copy_index", _ptr(tt), BH, d, int(staging.sub), ctypes.c_void_p(src.planes32.data_ptr()),
+              ctypes.c_void_p(src.scales_k.data_ptr()), ctypes.c_void_p(staging.planes32.data_ptr()),
+              ctypes.c_void_p(staging.scales_k.data_ptr()), _stream(tt.device))
 
 
 def gather_rows(src, cap, idx, BH, dtype=torch.bfloat16, d=D):

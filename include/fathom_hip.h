@@ -167,6 +167,30 @@ int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t n, c
                         void *Vout, int32_t *n_unique, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * gather_runs (scripts/B_e2e_offload_v2.py:62-71, gather_runs_kernel): copy run r,
+ * the 4-byte words [off[r], off[r] + len[r]) of src, to the same words of dst,
+ * for r < *nrun (off, len [R] int64 and nrun [1] int32 in device memory, so the
+ * run list can be built on the device without a host sync; len <= 0 skips a
+ * run).  src is usually mapped host memory, dst HBM; max_len bounds every
+ * len[r] (words); R <= 65535; src and dst 4-byte aligned.
+ */
+int fathom_gather_runs(const void *src, void *dst, const int64_t *off, const int64_t *len, const int32_t *nrun,
+                       int64_t R, int64_t max_len, void *stream);
+
+/*
+ * The copy-index gather of a plan (scripts/B_e2e_offload_v2.py:190-197: the run
+ * list of every (bh, channel) slot -- first t planes, and the scales of active
+ * channels -- passed to gather_runs for planes and scales).  Stores in the
+ * whole-sequence layout (sub = nblk, nsb = 1): planes [BH, 1, D, 4, nblk]
+ * uint64 and scales [BH, 1, D, nblk] fp16.  For every slot with t > 0 the first
+ * min(t, 4) planes and the scales are copied from *_src (usually mapped host
+ * memory) to the same offsets of *_dst (HBM staging); other bytes of *_dst are
+ * left unchanged.  t [BH, D] int8 (device); BH * D <= 65535.
+ */
+int fathom_copy_index(const int8_t *t, int64_t BH, int64_t D, int64_t nblk, const void *planes_src,
+                      const void *scales_src, void *planes_dst, void *scales_dst, void *stream);
+
+/*
  * Pinned, GPU-mapped host memory (scripts/B_e2e_offload_v2.py:33-39,
  * host_mapped / free_host through cudaHostAlloc(flags=3) and
  * cudaHostGetDevicePointer).  coherent != 0 asks for fine-grained (coherent)

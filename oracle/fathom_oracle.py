@@ -40,6 +40,10 @@ Parity status per function (how each is pinned; the tests hold the checks):
   The reference (torch.topk) leaves tie order unspecified: parity unpinned
   for ties, the build defines lowest index first.
 * gather_rows / gather_union: pure-Python loops; dedup changes traffic only.
+* gather_runs / copy_index_runs: pure-Python word loops; the copy-index run
+  list equals, slot by slot, the reference's offp/lenp/offs/lens formulas
+  (hand-computed example in the tests), and scanning the staged copy equals
+  scanning the full store (the reference's own PLANES_CHECK criterion).
 * sketch_planes_scores (CPU baseline): equals scan_planes on fp32-scaled codes.
 """
 import math
@@ -392,6 +396,32 @@ def gather_union(idx, n, Ksrc, Vsrc, Krec=None, Vrec=None):
             Vs[b, rec] = Vrec[b, r]
         nu[b] = len(np.unique(flat[b, host]))
     return Ks.reshape(BH, G, k, D), Vs.reshape(BH, G, k, D), nu
+
+
+def gather_runs(src, dst, off, ln, nrun):
+    """Copy run r, words [off[r], off[r] + ln[r]) of src, to the same words of dst
+    for r < nrun; runs with ln <= 0 are skipped (scripts/B_e2e_offload_v2.py:62-71).
+    src, dst: 1-D word arrays (dst is copied, not modified)."""
+    out = np.array(dst, copy=True)
+    for r in range(int(nrun)):
+        o, l = int(off[r]), int(ln[r])
+        for w in range(max(l, 0)):
+            out[o + w] = src[o + w]
+    return out
+
+
+def copy_index_runs(t, nblk, D):
+    """The copy-index run list of a plan t [BH, D] over whole-sequence stores
+    (scripts/B_e2e_offload_v2.py:190-197), in 4-byte words: slot s = bh * D + j
+    has the plane run (s * 4 * nblk * 2, min(t, 4) * nblk * 2) and the scale run
+    (s * nblk / 2, [t > 0] * nblk / 2) (nblk even)."""
+    t = np.asarray(t, np.int64).reshape(-1)
+    slot = np.arange(t.size, dtype=np.int64)
+    offp = slot * (4 * nblk * 2)
+    lenp = np.clip(t, 0, 4) * (nblk * 2)
+    offs = slot * (nblk // 2)
+    lens = (t > 0).astype(np.int64) * (nblk // 2)
+    return offp, lenp, offs, lens
 
 
 # ----------------------------------------------------------------------------- CPU baseline (sketch path)

@@ -304,6 +304,80 @@ def test_gather_union_matches_oracle(host):
 
 
 # ----------------------------------------------------------------------------- end to end
+@pytest.mark.parametrize("host", [False, True])
+def test_gather_runs_matches_oracle(host):
+    """Random runs (empty, negative-length and beyond-nrun ones included) from HBM
+    or mapped host memory into a pre-filled device buffer."""
+    print(f"[gather_runs] host={host}", flush=True)
+    rng = np.random.default_rng(11)
+    W, R = 50000, 40
+    src = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, W, dtype=np.int64).astype(np.int32))
+    dst0 = torch.full((W,), -7, dtype=torch.int32)
+    starts = rng.integers(0, W - 3000, R)
+    lens = rng.integers(-5, 3000, R)
+    lens[:4] = 0
+    nrun = R - 3
+    ref = O.gather_runs(src.numpy(), dst0.numpy(), starts, lens, nrun)
+    dst = dst0.to(DEV)
+    hp = None
+    try:
+        if host:
+            _, s_src, hp = off.host_mapped(src)
+        else:
+            s_src = src.to(DEV)
+        off.gather_runs(s_src, dst, torch.from_numpy(starts).to(DEV), torch.from_numpy(lens).to(DEV),
+                        torch.tensor([nrun], dtype=torch.int32, device=DEV), int(max(lens.max(), 0)))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(dst.cpu().numpy(), ref)
+    finally:
+        if hp:
+            off.free_host(hp)
+
+
+def _whole_sequence_store(x):
+    nb = math.ceil(x["n"] / 64)
+    bp.SUB = nb
+    try:
+        return bp.PlaneStore(x["K"].to(DEV))
+    finally:
+        bp.SUB = 16
+
+
+@pytest.mark.parametrize("cfg,n,BH", [(2, 40000, 2), (4, 20001, 2), (1, 16384, None)])
+def test_copy_index_staging_equals_store(cfg, n, BH):
+    """The copy-index path: the plan's runs copied from mapped host memory into a
+    zeroed HBM staging store; scanning the staging store equals scanning the full
+    store bit for bit (the reference's PLANES_CHECK, scripts/B_e2e_offload_v2.py:
+    184-202, at tolerance 0), fused top-k included, and no other word is written."""
+    print(f"[copy_index] cfg={cfg} n={n} BH={BH}", flush=True)
+    x = W.config_inputs(cfg, n=n, BH=BH)
+    st = _whole_sequence_store(x)
+    plan = bp.make_plan(x["g"].to(DEV), x["budget"])
+    q = x["q"].to(DEV)
+    hs, hps = off.host_store(st)
+    try:
+        stg = off.staging_store(st)
+        off.copy_index(hs, stg, plan)
+        torch.testing.assert_close(stg.scan(q, plan), st.scan(q, plan), rtol=0, atol=0)
+        k = min(512, x["n"] - 40)
+        torch.testing.assert_close(stg.scan_topk(q, plan, k), st.scan_topk(q, plan, k), rtol=0, atol=0)
+        t = plan["t"].cpu().numpy()
+        nb = st.sub
+        offp, lenp, offs, lens = O.copy_index_runs(t, nb, 128)
+        ref_p = O.gather_runs(st.planes_k.view(torch.int32).cpu().numpy().ravel(),
+                              np.zeros(st.planes_k.numel() * 2, np.int32), offp, lenp, len(offp))
+        np.testing.assert_array_equal(stg.planes_k.view(torch.int32).cpu().numpy().ravel(), ref_p)
+        sc_words = st.scales_k.view(torch.int16).cpu().numpy().ravel()
+        got_sc = stg.scales_k.view(torch.int16).cpu().numpy().ravel()
+        for s_ in range(t.size):
+            on = t.ravel()[s_] > 0
+            seg = slice(s_ * nb, (s_ + 1) * nb)
+            np.testing.assert_array_equal(got_sc[seg], sc_words[seg] if on else 0)
+    finally:
+        for h in hps:
+            off.free_host(h)
+
+
 def test_config1_pipeline_matches_oracle():
     """Config 1 end to end: store, plan, scan, sink/local top-k on the GPU vs the oracle."""
     x = W.config_inputs(1)

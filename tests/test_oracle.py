@@ -319,3 +319,42 @@ def test_gather_rows_and_union():
     np.testing.assert_array_equal(r[0, 0], Ks[0, 3])
     assert (r[0, 1] == 0).all() and (r[1, 2] == 0).all()
     np.testing.assert_array_equal(r[1, 0], Ks[1, 49])
+
+
+def test_gather_runs_and_copy_index_runs_known_answer():
+    """Hand-computed: runs [2, 5) and [9, 10) of a 12-word store, a skipped run
+    (len 0) and a run past nrun; the copy-index run list of a 2x2 plan with
+    nblk = 4 written out from the reference's formulas (B_e2e_offload_v2.py:193)."""
+    src = np.arange(100, 112, dtype=np.int32)
+    dst = np.full(12, -1, np.int32)
+    got = O.gather_runs(src, dst, off=[2, 9, 0, 6], ln=[3, 1, 0, 2], nrun=3)
+    exp = np.array([-1, -1, 102, 103, 104, -1, -1, -1, -1, 109, -1, -1], np.int32)
+    np.testing.assert_array_equal(got, exp)
+    t = np.array([[2, 0], [5, 1]])
+    offp, lenp, offs, lens = O.copy_index_runs(t, nblk=4, D=2)
+    np.testing.assert_array_equal(offp, [0, 32, 64, 96])     # slot * 4 planes * 4 blocks * 2 words
+    np.testing.assert_array_equal(lenp, [16, 0, 32, 8])      # min(t, 4) * 4 blocks * 2 words
+    np.testing.assert_array_equal(offs, [0, 2, 4, 6])        # slot * 4 halves / 2
+    np.testing.assert_array_equal(lens, [2, 0, 2, 2])
+
+
+def test_copy_index_runs_cover_exactly_the_scanned_words():
+    """The runs of a plan are exactly the words a scan of the whole-sequence store
+    reads: every plane word of a listed channel at depth < t, every scale of a
+    listed channel, nothing else (checked by marking words on a tiny store)."""
+    rng = np.random.default_rng(7)
+    BH, D, nblk = 2, 6, 4
+    t = rng.integers(0, 5, size=(BH, D))
+    offp, lenp, offs, lens = O.copy_index_runs(t, nblk, D)
+    words = np.zeros(BH * D * 4 * nblk * 2, np.int32)
+    src = np.ones_like(words)
+    mark = O.gather_runs(src, words, offp, lenp, len(offp)).reshape(BH, D, 4, nblk * 2)
+    for b in range(BH):
+        for j in range(D):
+            for p in range(4):
+                assert (mark[b, j, p] == (1 if p < t[b, j] else 0)).all()
+    sc = O.gather_runs(np.ones(BH * D * nblk // 2, np.int32), np.zeros(BH * D * nblk // 2, np.int32), offs, lens,
+                       len(offs)).reshape(BH, D, nblk // 2)
+    for b in range(BH):
+        for j in range(D):
+            assert (sc[b, j] == (1 if t[b, j] > 0 else 0)).all()
