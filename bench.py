@@ -318,7 +318,8 @@ def main():
         "stage_ms": {k: round(v, 4) for k, v in st.items()},
         "scan_topk_ms": scan_topk_ms,
         "unfused_scan_plus_topk_ms": st["scan"] + st["topk"],
-        "roofline": {"bound": "hbm", "kernel": "scan_planes_kernel", "achieved": achieved, "peak": HBM_PEAK_GBPS,
+        "roofline": {"bound": "hbm", "kernel": "scan_tile_kernel<4, 0> (PlaneStore.scan)", "achieved": achieved,
+                     "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": hbm["scan_bytes"]},
         "host_resident": host,
