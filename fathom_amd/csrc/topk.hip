@@ -44,6 +44,61 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Descending bitonic sort of the 64 values of a wave (one per lane), in
+// registers: 21 compare-exchange stages over lane shuffles.
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
+#pragma unroll
+  for (int kb = 2; kb <= 64; kb <<= 1) {
+#pragma unroll
+    for (int j = kb >> 1; j > 0; j >>= 1) {
+      const uint64_t w = shfl_xor_u64(v, j);
+      const bool keep_max = ((lane & j) == 0) == ((lane & kb) == 0);
+      v = keep_max ? (v > w ? v : w) : (v < w ? v : w);
+    }
+  }
+  return v;
+}
+
+// Number of values > x in a run of 64 sorted descending (binary search).
+__device__ __forceinline__ int count_greater64(const uint64_t *run, uint64_t x) {
+  int lo = 0, hi = 64;
+#pragma unroll
+  for (int it = 0; it < 7; ++it) {
+    if (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (run[mid] > x) lo = mid + 1; else hi = mid;
+    }
+  }
+  return lo;
+}
+
+// Ranks (0 = largest) of up to E * 1024 distinct nonzero values: thread t holds
+// elements t + 1024 e (zero = padding).  Each wave sorts its 64-value runs in
+// registers; a value's rank is its position in its own run plus the number of
+// larger values in every other run.  runs: LDS scratch of E * 1024 values.
+// Returns the sorted value held at the same slot and its rank.
+template <int E>
+__device__ void run_ranks(uint64_t (&v)[E], int (&rank)[E], uint64_t *runs, int nvals) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int nruns = (nvals + 63) >> 6;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    v[e] = wave_sort_desc(v[e], lane);
+    runs[t + 1024 * e] = v[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int own = (t + 1024 * e) >> 6;
+    int r = lane;
+    if (v[e] != 0ull) {
+      for (int q = 0; q < nruns; ++q)
+        if (q != own) r += count_greater64(runs + 64 * q, v[e]);
+    }
+    rank[e] = v[e] != 0ull ? r : 0x7FFFFFFF;
+  }
+}
+
 // Smallest value >= lo of the need-th largest element among cnt values read
 // through get(i) (all threads of the workgroup call it).  Returns thr with
 // #{v >= thr} >= need, equality when the values are distinct; thr = 0 when
@@ -144,13 +199,13 @@ __device__ __forceinline__ uint32_t masked_key(const float *row, int64_t i, int6
 }
 
 // Thresholds of a row from its sampled keys: each thread keeps its M largest
-// keys; T_lo is the kk-th largest of those M * 1024 values.  They are kk
-// elements of the sample >= T_lo, so T_lo <= the sample's kk-th largest <= the
-// row's: every element of the row's top kk has key >= T_lo.  T_hi is the
-// r_hi-th largest of the same values (r_hi <= kk, so T_hi >= T_lo).
+// keys (2 kk <= 1024 M); T_lo is the kk-th largest of those M * 1024 values.
+// They are kk elements of the sample >= T_lo, so T_lo <= the sample's kk-th
+// largest <= the row's: every element of the row's top kk has key >= T_lo.
+// T_hi is the r_hi-th largest of the same values (r_hi <= kk, so T_hi >= T_lo).
 template <int M>
 __device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t r_hi, uint64_t *vals,
-                             RangeShared &sh, uint32_t &t_lo, uint32_t &t_hi) {
+                             uint32_t *s_thr, uint32_t &t_lo, uint32_t &t_hi) {
   uint32_t top[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) top[i] = 0u;
@@ -164,24 +219,28 @@ __device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t
       top[i] = hi;
     }
   }
+  // ranks of the M * 1024 candidates (key << 32 | slot: distinct, nonzero);
+  // the keys of ranks kk - 1 and r_hi - 1 are the thresholds
+  uint64_t w[M];
+  int rk[M];
 #pragma unroll
-  for (int i = 0; i < M; ++i) vals[threadIdx.x * M + i] = (uint64_t)top[i] << 32;
-  __syncthreads();
-  const uint64_t t = range_select([&](int64_t i) { return vals[i]; }, (int64_t)M * kSelThreads, kk, sh);
-  t_lo = (uint32_t)(t >> 32);
-  t_hi = t_lo;
-  if (r_hi < kk) {
-    __syncthreads();
-    const uint64_t th = range_select([&](int64_t i) { return vals[i]; }, (int64_t)M * kSelThreads, r_hi, sh);
-    t_hi = (uint32_t)(th >> 32);
+  for (int i = 0; i < M; ++i) w[i] = ((uint64_t)top[i] << 32) | (uint32_t)(threadIdx.x + 1024 * i + 1);
+  run_ranks<M>(w, rk, vals, M * kSelThreads);
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    if (rk[i] == (int)kk - 1) s_thr[0] = (uint32_t)(w[i] >> 32);
+    if (rk[i] == (int)r_hi - 1) s_thr[1] = (uint32_t)(w[i] >> 32);
   }
+  __syncthreads();
+  t_lo = s_thr[0];
+  t_hi = r_hi < kk ? s_thr[1] : t_lo;
 }
 
 __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t *__restrict__ samp,
                                                                   int64_t samp_cap, uint32_t kk, uint32_t r_hi,
                                                                   TopkSel s) {
-  __shared__ RangeShared sh;
   __shared__ uint64_t vals[4 * kSelThreads];
+  __shared__ uint32_t s_thr[2];
   const int64_t row = blockIdx.x;
   const uint32_t *src = samp + row * samp_cap;
   uint32_t v[kSelPer];
@@ -193,11 +252,11 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
   uint32_t t_lo = 0u, t_hi = 0u;  // fewer samples than kk: every element is a candidate
   if (samp_cap >= (int64_t)kk) {
     if (2 * kk <= kSelThreads)
-      sample_bound<1>(v, kk, r_hi, vals, sh, t_lo, t_hi);
+      sample_bound<1>(v, kk, r_hi, vals, s_thr, t_lo, t_hi);
     else if (kk <= kSelThreads)
-      sample_bound<2>(v, kk, r_hi, vals, sh, t_lo, t_hi);
+      sample_bound<2>(v, kk, r_hi, vals, s_thr, t_lo, t_hi);
     else
-      sample_bound<4>(v, kk, r_hi, vals, sh, t_lo, t_hi);
+      sample_bound<4>(v, kk, r_hi, vals, s_thr, t_lo, t_hi);
   }
   if (threadIdx.x == 0) {
     s.thr[row] = t_hi;
@@ -299,6 +358,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   }
   if (tid == 0) s_cnt = 0u;
   __syncthreads();
+  // the exact kk largest first (range selection), then their ranks
   const uint64_t thr = in_lds ? range_select([&](int64_t i) { return cl[i]; }, cnt, (uint32_t)kk, sh)
                               : range_select([&](int64_t i) { return gc[i]; }, cnt, (uint32_t)kk, sh);
   for (int64_t i = tid; i < cnt; i += kFinThreads) {
@@ -309,29 +369,18 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
     }
   }
   __syncthreads();
-  const int got = (int)min(min(s_cnt, (uint32_t)kMaxK), (uint32_t)kk);
-  int P = 1;
-  while (P < got) P <<= 1;
-  for (int i = got + tid; i < P; i += kFinThreads) ss[i] = 0ull;  // zero sorts below every K64
-  __syncthreads();
-  // bitonic sort of ss[0, P), descending
-  for (int kb = 2; kb <= P; kb <<= 1) {
-    for (int j = kb >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < P; i += kFinThreads) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t a = ss[i], b = ss[ixj];
-          if (((i & kb) == 0) ? (a < b) : (a > b)) {
-            ss[i] = b;
-            ss[ixj] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-  for (int i = tid; i < (int)kk; i += kFinThreads)
-    out[i] = i < got ? (int64_t)(0xFFFFFFFFu - (uint32_t)ss[i]) : 0;
+  const int nv = (int)min(min(s_cnt, (uint32_t)kMaxK), (uint32_t)kk);
+  uint64_t v2[2];  // zero: padding (below every K64)
+  v2[0] = tid < nv ? ss[tid] : 0ull;
+  v2[1] = tid + kFinThreads < nv ? ss[tid + kFinThreads] : 0ull;
+  __syncthreads();  // cl is the rank scratch from here
+  int rk[2];
+  run_ranks<2>(v2, rk, cl, nv);
+  const int got = nv < (int)kk ? nv : (int)kk;
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+    if (rk[e] < got) out[rk[e]] = (int64_t)(0xFFFFFFFFu - (uint32_t)v2[e]);
+  for (int i = got + tid; i < (int)kk; i += kFinThreads) out[i] = 0;
   for (int i = tid; i < (int)(sink + local); i += kFinThreads)
     out[kk + i] = (i < sink) ? (int64_t)i : (int64_t)(m - local + (i - sink));
 }
