@@ -36,6 +36,9 @@ PROTOTYPES = {
     "fathom_gather_union_workspace_bytes": (_sz, [_i64, _i64]),
     "fathom_gather_union": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
                                    _vp, _sz, _vp]),
+    "fathom_gather_attention_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "fathom_gather_attention": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64,
+                                       ctypes.c_float, _vp, _vp, _vp, _sz, _vp]),
     "fathom_gather_runs": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fathom_copy_index": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "fathom_host_alloc_mapped": (_i32, [_sz, _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),

@@ -168,6 +168,49 @@ def gather_union(idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, dtype=torch.bflo
     return Ks, Vs, nu
 
 
+def gather_attention(q, idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, scale=None):
+    """Exact attention over the selected rows, fused with their union gather:
+    out[bh, g] = softmax(scale * q[bh, g] . K[idx[bh, g]]) . V[idx[bh, g]] in fp32
+    over bf16 rows of D = 128 (scripts/B_kernel_bench.py:22-27;
+    scripts/B_e2e_offload_v2.py:228-244).  Row sources as in gather_union: tokens
+    < n from Ksrc/Vsrc [BH, cap, D] (tensor or DevPtr, HBM or mapped host), tokens
+    >= n from Krec/Vrec, negative tokens as zero rows; each distinct token of a row
+    is read once.  scale defaults to D ** -0.5.  Returns (out [BH, G, D] fp32,
+    n_unique [BH] int32)."""
+    _need_gpu(q, idx)
+    BH, G, k = idx.shape
+    if q.shape != (BH, G, D):
+        raise ValueError(f"gather_attention: q {tuple(q.shape)} must be [BH, G, {D}] = [{BH}, {G}, {D}]")
+    for name, t in (("Ksrc", Ksrc), ("Vsrc", Vsrc), ("Krec", Krec), ("Vrec", Vrec)):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError(f"gather_attention: {name} must hold bf16 rows, got {t.dtype}")
+    dev = q.device
+    qf = q.float().contiguous()
+    flat = idx.contiguous().to(torch.int64)
+    out = torch.empty(BH, G, D, device=dev, dtype=torch.float32)
+    nu = torch.empty(BH, device=dev, dtype=torch.int32)
+    nbytes = _lib.lib().fathom_gather_attention_workspace_bytes(BH, G, k)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    nrec = 0
+    if Krec is not None:
+        Krec = Krec.reshape(BH, -1, D).contiguous()
+        Vrec = Vrec.reshape(BH, -1, D).contiguous()
+        nrec = Krec.shape[1]
+    sc = float(D) ** -0.5 if scale is None else float(scale)
+    _lib.call("fathom_gather_attention", _ptr(qf), _ptr(flat), BH, G, k, int(n), ctypes.c_void_p(Ksrc.data_ptr()),
+              ctypes.c_void_p(Vsrc.data_ptr()), int(cap), _ptr(Krec), _ptr(Vrec), nrec, sc, _ptr(out), _ptr(nu),
+              _ptr(ws), nbytes, _stream(dev))
+    return out, nu
+
+
+def gather_attn(q, Kc, Vc, idx):
+    """Drop-in for scripts/B_kernel_bench.py:22 gather_attn: q [BH, G, D] fp32,
+    Kc/Vc [BH, n, D] bf16 (device), idx [BH, G, k] -> [BH, G, D] fp32."""
+    n = Kc.shape[1]
+    out, _ = gather_attention(q, idx, n, Kc.contiguous(), Vc.contiguous(), n)
+    return out
+
+
 def select_and_gather(store, q, var, budget, k, Ksrc, Vsrc, sink=4, local=32, m=None, Krec=None, Vrec=None,
                       dtype=torch.bfloat16):
     """One decode step's selection for all (batch, KV head) rows: g = sum_g q^2 var,

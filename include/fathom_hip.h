@@ -167,6 +167,25 @@ int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t n, c
                         void *Vout, int32_t *n_unique, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Exact attention over the selected rows (scripts/B_kernel_bench.py:22-27
+ * gather_attn; scripts/B_e2e_offload_v2.py:228-244, the gather + attention of
+ * offload_attn): for every query head g of row bh,
+ *   out[bh, g] = softmax_j(scale * q[bh, g] . K[t_j]) . V[t_j]   over the k
+ * positions j of idx[bh, g] (fp32 math on bf16 rows; a token selected twice
+ * counts twice).  Rows come from the same sources as fathom_gather_union
+ * (Ksrc/Vsrc [BH, cap, 128] bf16 for tokens < n, Krec/Vrec [BH, nrec, 128]
+ * for tokens >= n, zero rows for negative tokens), each distinct token of a
+ * row read once.  q [BH, G, 128] fp32, idx [BH, G, k] int64, out [BH, G, 128]
+ * fp32; G <= 8, G*k <= 16384; n_unique as in fathom_gather_union.
+ * workspace: fathom_gather_attention_workspace_bytes(BH, G, k) bytes.
+ */
+size_t fathom_gather_attention_workspace_bytes(int64_t BH, int64_t G, int64_t k);
+int fathom_gather_attention(const float *q, const int64_t *idx, int64_t BH, int64_t G, int64_t k, int64_t n,
+                            const void *Ksrc, const void *Vsrc, int64_t cap, const void *Krec, const void *Vrec,
+                            int64_t nrec, float scale, float *out, int32_t *n_unique, void *workspace,
+                            size_t workspace_bytes, void *stream);
+
+/*
  * gather_runs (scripts/B_e2e_offload_v2.py:62-71, gather_runs_kernel): copy run r,
  * the 4-byte words [off[r], off[r] + len[r]) of src, to the same words of dst,
  * for r < *nrun (off, len [R] int64 and nrun [1] int32 in device memory, so the

@@ -398,6 +398,25 @@ def gather_union(idx, n, Ksrc, Vsrc, Krec=None, Vrec=None):
     return Ks.reshape(BH, G, k, D), Vs.reshape(BH, G, k, D), nu
 
 
+def gather_attention(q, idx, n, Ksrc, Vsrc, Krec=None, Vrec=None, scale=None):
+    """Exact attention over the selected rows (scripts/B_kernel_bench.py:22-27
+    gather_attn; scripts/B_e2e_offload_v2.py:242-244): for query head g of row
+    bh, s_j = scale * q[bh, g] . K[idx[bh, g, j]] over the k positions j (a token
+    selected twice counts twice), out = softmax(s) . V.  Rows as gather_union
+    (float arrays holding the bf16 row values); scale defaults to the float32
+    value of D ** -0.5, as the reference's fp32 multiply uses it.  float64
+    arithmetic.  Returns (out [BH, G, D] float64, n_unique_host [BH])."""
+    Ks, Vs, nu = gather_union(idx, n, Ksrc, Vsrc, Krec, Vrec)
+    q = np.asarray(q, np.float64)
+    D = q.shape[-1]
+    sc = float(np.float32(D ** -0.5)) if scale is None else float(scale)
+    s = np.einsum("bgd,bgkd->bgk", q, Ks.astype(np.float64)) * sc
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p = p / p.sum(-1, keepdims=True)
+    return np.einsum("bgk,bgkd->bgd", p, Vs.astype(np.float64)), nu
+
+
 def gather_runs(src, dst, off, ln, nrun):
     """Copy run r, words [off[r], off[r] + ln[r]) of src, to the same words of dst
     for r < nrun; runs with ln <= 0 are skipped (scripts/B_e2e_offload_v2.py:62-71).

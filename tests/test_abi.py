@@ -37,7 +37,15 @@ def test_library_exports_every_declared_symbol():
 def test_workspace_queries_and_argument_errors_without_gpu():
     L = _lib.lib()
     assert L.fathom_topk_workspace_bytes(32, 1 << 20, 512) >= 32 * (1 << 20) * 8
-    assert L.fathom_gather_union_workspace_bytes(8, 2048) == 8 * 2048 * 8
+    e = 8 * 2048  # per position: chain link, chain start, head counts, distinct-token entry
+    assert L.fathom_gather_union_workspace_bytes(8, 2048) == e * (4 + 4 + 16 + 8) + 256
+    nsplit = 2048 // 32  # partial softmax triples of 32 distinct tokens each
+    assert (L.fathom_gather_attention_workspace_bytes(8, 4, 512)
+            == e * (4 + 4 + 16 + 8) + 256 + 8 * nsplit * 4 * 130 * 4)
+    rc = L.fathom_gather_attention(None, None, 1, 4, 512, 10, None, None, 10, None, None, 0, 1.0, None, None,
+                                   None, 0, None)
+    assert rc == _lib.ERR_INVALID
+    assert L.fathom_gather_attention_workspace_bytes(8, 9, 512) > 0  # G > 8 is rejected by the call itself
     # argument validation happens before any HIP call
     rc = L.fathom_make_plan(None, None, 1, 128, 4, 30, None, None, None, None, None, None, None, None)
     assert rc == _lib.ERR_INVALID and b"null" in L.fathom_last_error()

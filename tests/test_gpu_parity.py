@@ -501,3 +501,97 @@ def test_scan_topk_adversarial_order():
     ref = bp.sink_local_topk(st.scan(q.to(DEV), plan), 512)
     got = st.scan_topk(q.to(DEV), plan, 512)
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
+
+
+# ----------------------------------------------------------------------------- attention over gathered rows
+def _attn_close(got, ref):
+    """fp32 kernel against the float64 oracle: summation order and exp rounding
+    only (scores ~1, k <= 16384 terms)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    bad = err > 1e-4 * np.abs(ref) + 2e-5
+    assert not bad.any(), f"{int(bad.sum())} outputs off; max err {err.max():.3e}"
+
+
+def _torch_gather_attn(q, K, V, idx):
+    """The reference formula in plain torch fp32 on the CPU (scripts/B_kernel_bench.py:22-27)."""
+    BH, G, k = idx.shape
+    d = q.shape[-1]
+    flat = idx.reshape(BH, G * k)
+    Ks = torch.gather(K, 1, flat.unsqueeze(-1).expand(-1, -1, d)).view(BH, G, k, d).float()
+    Vs = torch.gather(V, 1, flat.unsqueeze(-1).expand(-1, -1, d)).view(BH, G, k, d).float()
+    s = torch.einsum("bgd,bgkd->bgk", q, Ks) * d ** -0.5
+    return torch.einsum("bgk,bgkd->bgd", torch.softmax(s, -1), Vs)
+
+
+@pytest.mark.parametrize("host", [False, True])
+@pytest.mark.parametrize("G,k", [(4, 512), (7, 2048), (1, 3), (8, 2000)])
+def test_gather_attention_matches_oracle(host, G, k):
+    print(f"[gather_attention] host={host} G={G} k={k}", flush=True)
+    rng = np.random.default_rng(17 + G)
+    BH, n, nrec = 3, 12000, 5
+    K = torch.randn(BH, n, 128).to(torch.bfloat16)
+    V = torch.randn(BH, n, 128).to(torch.bfloat16)
+    Kr = torch.randn(BH, nrec, 128).to(torch.bfloat16)
+    Vr = torch.randn(BH, nrec, 128).to(torch.bfloat16)
+    q = torch.randn(BH, G, 128)
+    idx = rng.integers(0, min(n, 3 * k), size=(BH, G, k))          # heavy overlap across heads
+    if k >= 8:
+        idx[:, :, -3:] = n + rng.integers(0, nrec + 2, size=(BH, G, 3))
+        idx[0, 0, 1] = -2
+        idx[1, G - 1, :4] = idx[1, G - 1, 4]                        # a token selected 5 times by one head
+    hps = []
+    try:
+        if host:
+            _, Ksrc, h1 = off.host_mapped(K)
+            _, Vsrc, h2 = off.host_mapped(V)
+            hps = [h1, h2]
+        else:
+            Ksrc, Vsrc = K.to(DEV), V.to(DEV)
+        it = torch.from_numpy(idx).to(DEV)
+        out, nu = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, Kr.to(DEV), Vr.to(DEV))
+        out2, _ = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, Kr.to(DEV), Vr.to(DEV))
+        torch.cuda.synchronize()
+        ref, rnu = O.gather_attention(q.numpy(), idx, n, K.float().numpy(), V.float().numpy(),
+                                      Kr.float().numpy(), Vr.float().numpy())
+        _attn_close(out.cpu().numpy(), ref)
+        np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
+        assert torch.equal(out, out2), "two calls on the same input differ"
+    finally:
+        for h in hps:
+            off.free_host(h)
+
+
+def test_gather_attn_dropin_equals_torch_formula():
+    """gather_attn(q, Kc, Vc, idx) against the reference formula in torch fp32."""
+    BH, G, n, k = 4, 4, 9000, 512
+    gen = torch.Generator().manual_seed(4)
+    Kc = torch.randn(BH, n, 128, generator=gen).to(torch.bfloat16)
+    Vc = torch.randn(BH, n, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(BH, G, 128, generator=gen)
+    idx = torch.randint(0, n, (BH, G, k), generator=gen)
+    ref = _torch_gather_attn(q, Kc, Vc, idx)
+    got = off.gather_attn(q.to(DEV), Kc.to(DEV), Vc.to(DEV), idx.to(DEV)).cpu()
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=2e-5)
+
+
+@pytest.mark.parametrize("layer", [0, 7])
+def test_decode_layer_c5(layer):
+    """One layer of the config-5 decode step at a reduced size: plan, fused scan +
+    top-k and the fused gather + attention, against the oracle's attention over the
+    unfused path's index set."""
+    print(f"[decode-c5] layer={layer}", flush=True)
+    x = W.config_inputs(5, device="cpu", n=8192, BH=4, layer=layer)
+    K = x["K"]
+    V = W.synth_values(4, 8192, seed=100 + layer)
+    st = bp.PlaneStore(K.to(DEV))
+    q = x["q"].to(DEV)
+    plan = bp.make_plan(x["g"].to(DEV), x["budget"])
+    idx = st.scan_topk(q, plan, x["k"], x["sink"], x["local"])
+    ref_idx = bp.sink_local_topk(st.scan(q, plan), x["k"], x["sink"], x["local"])
+    torch.testing.assert_close(idx, ref_idx, rtol=0, atol=0)
+    out, nu = off.gather_attention(q, idx, 8192, K.to(DEV), V.to(DEV), 8192)
+    ref, rnu = O.gather_attention(x["q"].numpy(), idx.cpu().numpy(), 8192, K.float().numpy(), V.float().numpy())
+    _attn_close(out.cpu().numpy(), ref)
+    np.testing.assert_array_equal(nu.cpu().numpy(), rnu)

@@ -358,3 +358,59 @@ def test_copy_index_runs_cover_exactly_the_scanned_words():
     for b in range(BH):
         for j in range(D):
             assert (sc[b, j] == (1 if t[b, j] > 0 else 0)).all()
+
+
+# ----------------------------------------------------------------------------- attention over gathered rows
+def test_gather_attention_closed_forms():
+    """Weights fixed by construction, so the expected output is a hand-known mix
+    of V rows: q along e0 and K rows c_j * e0 give scores scale * c_j; choosing
+    c_j = ln(w_j) / scale makes the softmax weights proportional to w_j."""
+    d, n = 8, 6
+    sc = float(np.float32(d ** -0.5))
+    q = np.zeros((1, 2, d))
+    q[0, :, 0] = 1.0
+    w = [1.0, 2.0, 4.0, 1.0, 1.0, 1.0]                       # target weight of each token
+    K = np.zeros((1, n, d))
+    K[0, :, 0] = [math.log(x) / sc for x in w]
+    V = np.arange(n * d, dtype=np.float64).reshape(1, n, d) % 7 - 3.0
+    # head 0: tokens 0, 1, 2 -> weights 1:2:4; head 1: token 1 twice and token 2
+    # once (a duplicate counts per position) -> weights 2+2:4 = 1:1
+    idx = np.array([[[0, 1, 2], [1, 1, 2]]])
+    out, nu = O.gather_attention(q, idx, n, K, V)
+    np.testing.assert_allclose(out[0, 0], (1 * V[0, 0] + 2 * V[0, 1] + 4 * V[0, 2]) / 7.0, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(out[0, 1], (V[0, 1] + V[0, 2]) / 2.0, rtol=1e-12, atol=1e-12)
+    assert nu[0] == 3
+    # a negative token is a zero row: score 0 (weight e^0 = 1) and zero value
+    idx2 = np.array([[[0, 2, -1], [3, 4, 5]]])
+    out2, nu2 = O.gather_attention(q, idx2, n, K, V)
+    np.testing.assert_allclose(out2[0, 0], (1 * V[0, 0] + 4 * V[0, 2] + 0.0) / 6.0, rtol=1e-12, atol=1e-12)
+    # equal scores: the plain mean of the selected rows
+    np.testing.assert_allclose(out2[0, 1], V[0, 3:6].mean(0), rtol=1e-12, atol=1e-12)
+    assert nu2[0] == 5
+    # tokens >= n come from the recent buffer (clamped to its last row)
+    Kr = np.zeros((1, 2, d))
+    Vr = np.full((1, 2, d), 5.0)
+    Vr[0, 1] = -5.0
+    out3, _ = O.gather_attention(q, np.array([[[n, n + 7], [n + 1, n + 1]]]), n, K, V, Kr, Vr)
+    np.testing.assert_allclose(out3[0, 0], np.zeros(d), atol=1e-12)
+    np.testing.assert_allclose(out3[0, 1], np.full(d, -5.0), atol=1e-12)
+
+
+def test_gather_attention_shift_and_scale():
+    """Adding one offset row u to every key shifts all scores of a head by
+    scale * q.u, which softmax ignores; a huge score spread (q x 1e4) puts all
+    the weight on the best-scoring token without overflowing."""
+    rng = np.random.default_rng(3)
+    BH, G, k, n, d = 2, 3, 5, 40, 16
+    q = rng.standard_normal((BH, G, d))
+    K = rng.standard_normal((BH, n, d))
+    V = rng.standard_normal((BH, n, d))
+    idx = rng.integers(0, n, size=(BH, G, k))
+    a, _ = O.gather_attention(q, idx, n, K, V)
+    b, _ = O.gather_attention(q, idx, n, K + rng.standard_normal((BH, 1, d)), V)
+    np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+    c, _ = O.gather_attention(q * 1e4, idx, n, K, V)       # one token dominates per head
+    for bb in range(BH):
+        for g in range(G):
+            s = K[bb, idx[bb, g]] @ q[bb, g]
+            np.testing.assert_allclose(c[bb, g], V[bb, idx[bb, g, int(np.argmax(s))]], rtol=1e-9, atol=1e-9)
