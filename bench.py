@@ -4,15 +4,17 @@ Workload (BASELINE.json metric "scanned tokens/s/GPU (scan+top-k) at 1M ctx"):
 config 3's layer shape -- 8 KV heads, G = 4 query heads per KV head, n = 2^20
 tokens, D = 128, "56-bit" plan (budget B = 48 code bits), k = 512 with 4 sink +
 32 local -- on seeded synthetic bf16 keys.  One step = make_plan -> fused
-scan + sink/local top-k -> union row gather over all 8 KV heads.  The unfused
-pair (scan writing scores, then sink_local_topk) is timed in the same steps and
-must select the same indices.
+scan + sink/local top-k -> exact attention over the selected rows (fused with
+their union gather) over all 8 KV heads.  The unfused pair (scan writing scores,
+then sink_local_topk) and the reference-structured union row gather are timed in
+the same steps; the unfused pair must select the same indices.
 
 `value` counts scanned token*heads per second of scan + top-k with the index
 resident in HBM (n * BH / t_scan_topk).  The roofline object is for the scan
 kernel (one launch, algorithmic bytes = bytes_planes).  The same step with the
 plane index and the K/V rows in mapped pinned host memory (the scan reads over
-PCIe) is reported under "host_resident".
+PCIe) is reported under "host_resident", and config 5's full decode step (36
+layers, batch 4 x 8 KV heads, n = 32768, per-layer budgets) under "decode_step".
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-host] [--no-cpu]
 """
@@ -39,6 +41,7 @@ def parse():
     ap.add_argument("--n", type=int, default=None, help="override the token count (testing only)")
     ap.add_argument("--no-host", action="store_true", help="skip the host-resident measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--stages-only", action="store_true", help="scan + top-k only (for profiling runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the run, launch a plain fp32 device copy kernel of this many MiB 3 times "
@@ -102,8 +105,12 @@ def run_regime(torch, bp, off, x, store, Ksrc, Vsrc, steps, warmup, stages_only=
     def s_gather(o):
         o["rows"] = off.gather_union(o["idx"], n, Ksrc, Vsrc, n)
 
-    names = ["plan", "scan", "topk", "scan_topk"] + ([] if stages_only else ["gather"])
-    fns = {"plan": s_plan, "scan": s_scan, "topk": s_topk, "scan_topk": s_fused, "gather": s_gather}
+    def s_attn(o):
+        o["attn"] = off.gather_attention(q, o["idx"], n, Ksrc, Vsrc, n)
+
+    names = ["plan", "scan", "topk", "scan_topk"] + ([] if stages_only else ["gather", "attn"])
+    fns = {"plan": s_plan, "scan": s_scan, "topk": s_topk, "scan_topk": s_fused, "gather": s_gather,
+           "attn": s_attn}
     timer = StageTimer(torch, names)
     for _ in range(warmup):
         timer.step(fns)
@@ -145,11 +152,11 @@ def run_copy_index(torch, bp, off, x, K_dev, V_dev, steps, warmup):
     del full
     torch.cuda.empty_cache()
     try:
-        names = ["plan", "copy", "scan_topk", "gather"]
+        names = ["plan", "copy", "scan_topk", "attn"]
         fns = {"plan": lambda o: o.__setitem__("plan", bp.make_plan(g, x["budget"])),
                "copy": lambda o: off.copy_index(hs, stg, o["plan"]),
                "scan_topk": lambda o: o.__setitem__("idx", stg.scan_topk(q, o["plan"], k, x["sink"], x["local"])),
-               "gather": lambda o: o.__setitem__("rows", off.gather_union(o["idx"], n, K_dev, V_dev, n))}
+               "attn": lambda o: o.__setitem__("rows", off.gather_attention(q, o["idx"], n, K_dev, V_dev, n))}
         timer = StageTimer(torch, names)
         for _ in range(warmup):
             timer.step(fns)
@@ -160,12 +167,95 @@ def run_copy_index(torch, bp, off, x, K_dev, V_dev, steps, warmup):
         torch.cuda.synchronize()
         st = timer.collect()
         scan_bytes = bp.bytes_planes(out["plan"]["t"], n)
-        uniq = int(out["rows"][2].sum().item())
+        uniq = int(out["rows"][1].sum().item())
         return {"stage_ms": st, "scan_bytes": scan_bytes, "row_bytes": 2 * uniq * 128 * 2, "unique_rows": uniq,
                 "idx": out["idx"]}
     finally:
         for h in hps:
             off.free_host(h)
+
+
+def run_decode_step(torch, bp, off, W, dev, steps, warmup):
+    """Config 5: one decode step of a 36-layer model with every layer's index and
+    K/V rows in HBM -- per layer make_plan (the layer's own budget), fused scan +
+    top-k and exact attention over the selected rows.  As scripts/B_kernel_bench.py
+    does, each stage (over all 36 layers) is captured in a HIP graph and timed
+    around graph replays; the eager time per step is reported beside it.  Every
+    replayed output must equal the eager one bit for bit."""
+    c = W.CONFIGS[5]
+    layers = []
+    for L in range(c["layers"]):
+        x = W.config_inputs(5, device=dev, layer=L)
+        layers.append({"q": x["q"], "g": x["g"], "budget": x["budget"], "K": x["K"],
+                       "V": W.synth_values(x["BH"], x["n"], seed=100 + L, device=dev),
+                       "store": bp.PlaneStore(x["K"], keep_code=False)})
+        del x
+    torch.cuda.synchronize()
+    n, BH, k, sink, local = c["n"], c["BH"], c["k"], c["sink"], c["local"]
+    st = [{} for _ in layers]
+
+    def s_plan():
+        for i, ly in enumerate(layers):
+            st[i]["plan"] = bp.make_plan(ly["g"], ly["budget"])
+
+    def s_scan_topk():
+        for i, ly in enumerate(layers):
+            st[i]["idx"] = ly["store"].scan_topk(ly["q"], st[i]["plan"], k, sink, local)
+
+    def s_attn():
+        for i, ly in enumerate(layers):
+            st[i]["out"] = off.gather_attention(ly["q"], st[i]["idx"], n, ly["K"], ly["V"], n)[0]
+
+    stages = [("plan", s_plan), ("scan_topk", s_scan_topk), ("attn", s_attn)]
+    # eager steps: reference outputs and the per-call (launch-bound) time
+    for _ in range(warmup):
+        for _, fn in stages:
+            fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        for _, fn in stages:
+            fn()
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / steps
+    ref = [(s["idx"].clone(), s["out"].clone()) for s in st]
+    graphs = []
+    for _, fn in stages:
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph):
+            fn()
+        graphs.append(gph)
+    torch.cuda.synchronize()
+    ms = {name: 0.0 for name, _ in stages}
+    evs = []
+    for it in range(warmup + steps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(len(graphs) + 1)]
+        e[0].record()
+        for j, gph in enumerate(graphs):
+            gph.replay()
+            e[j + 1].record()
+        if it >= warmup:
+            evs.append(e)
+    torch.cuda.synchronize()
+    for e in evs:
+        for j, (name, _) in enumerate(stages):
+            ms[name] += e[j].elapsed_time(e[j + 1]) / steps
+    for (ri, ro), s in zip(ref, st):
+        if not (torch.equal(ri, s["idx"]) and torch.equal(ro, s["out"])):
+            raise RuntimeError("decode step: a graph replay differs from the eager step")
+    step_ms = sum(ms.values())
+    scan_bytes = sum(bp.bytes_planes(s["plan"]["t"], n) for s in st)
+    del graphs, layers, st
+    torch.cuda.empty_cache()
+    return {"workload": c["name"], "layers": c["layers"], "BH": BH, "n": n, "k": k,
+            "budgets": [float(b) for b in W.C5_BUDGETS], "timing": "HIP graph per stage over all layers",
+            "ms_per_step": step_ms, "eager_ms_per_step": eager_ms,
+            "stage_ms_per_step": {s: round(v, 4) for s, v in ms.items()},
+            "scanned_tokens_per_s": c["layers"] * BH * n / (ms["scan_topk"] * 1e-3),
+            "scan_bytes_per_step": scan_bytes,
+            "scan_topk_GBps": scan_bytes / (ms["scan_topk"] * 1e-3) / 1e9}
 
 
 def cpu_baseline(x_cpu, reps=3):
@@ -253,7 +343,7 @@ def main():
             hr = run_regime(torch, bp, off, x, hstore, K_dev, V_dev, max(3, a.steps // 2), 2)
             same = bool(torch.equal(hr["idx"], hbm["idx"]))
             hs = hr["stage_ms"]
-            tot = hs["plan"] + hs["scan_topk"] + hs["gather"]
+            tot = hs["plan"] + hs["scan_topk"] + hs["attn"]
             pcie_bytes = hr["scan_bytes"] + hr["row_bytes"]
             # measured pinned H2D copy rate, the reference's memcpy comparison
             src = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
@@ -269,7 +359,7 @@ def main():
             h2d = 4 * src.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9
             ci = run_copy_index(torch, bp, off, x, K_dev, V_dev, max(3, a.steps // 2), 2)
             cs = ci["stage_ms"]
-            ci_tot = cs["plan"] + cs["copy"] + cs["scan_topk"] + cs["gather"]
+            ci_tot = cs["plan"] + cs["copy"] + cs["scan_topk"] + cs["attn"]
             ci_bytes = ci["scan_bytes"] + ci["row_bytes"]
             copy_index = {"stage_ms": {k: round(v, 4) for k, v in cs.items()}, "step_ms": ci_tot,
                           "pcie_bytes_per_step": ci_bytes, "pcie_GBps_step": ci_bytes / (ci_tot * 1e-3) / 1e9,
@@ -301,6 +391,13 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] calibration copy: 3 x {a.calib_copy_mib} MiB read + written")
 
+    decode = None
+    if not a.no_decode and not a.stages_only and a.n is None:
+        del store
+        torch.cuda.empty_cache()
+        decode = run_decode_step(torch, bp, off, W, dev, max(3, a.steps // 2), 2)
+        log(f"[bench] decode step (config 5): {json.dumps(decode)}")
+
     cpu = None
     if not a.no_cpu:
         xs = W.config_inputs(a.config, device="cpu", n=min(x["n"], 1 << 20), BH=1)
@@ -310,7 +407,7 @@ def main():
     rec = {
         "metric": "scanned tokens/s/GPU (scan+top-k) at 1M ctx",
         "value": value, "unit": "token*heads/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": st["plan"] + st["scan_topk"] + st.get("gather", 0.0), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": st["plan"] + st["scan_topk"] + st.get("attn", 0.0), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded lognormal-scaled keys, planted keys; no model weights)",
         "config": {"workload": W.CONFIGS[a.config]["name"] + ", index + rows in HBM", "BH": BH, "G": x["G"],
                    "n": n, "budget_bits": x["budget"], "k": x["k"], "sink": x["sink"], "local": x["local"],
@@ -323,6 +420,7 @@ def main():
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": hbm["scan_bytes"]},
         "host_resident": host,
+        "decode_step": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

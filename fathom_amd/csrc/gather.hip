@@ -16,12 +16,12 @@
 //           recent-token device buffer, or a zero row for negative tokens) and
 //           writes it to every position of its chain, so each distinct host
 //           row crosses PCIe exactly once;
-//   attend  (gather_attention) one wave per distinct token reads the K and V
-//           rows straight into registers and updates a running softmax of
-//           every query head that selected it, weighted by the number of times
-//           that head selected it; workgroups hold 32 distinct tokens and
-//           write partial (max, sum, weighted V) triples that a second kernel
-//           merges in a fixed order.
+//   attend  (gather_attention) workgroups of 128 distinct tokens read each
+//           token's K and V rows once, straight into registers, and form the
+//           softmax numerators of every query head that selected the token,
+//           weighted by the number of times that head selected it; each
+//           workgroup writes a partial (max, sum, weighted V) triple per head
+//           and a second kernel merges a row's triples in split order.
 #include "common.hpp"
 
 namespace fathom {
@@ -35,10 +35,11 @@ constexpr int kHashSlots = 16384;                  // >= kMaxGK: the table never
 constexpr int kMaxHeads = 8;                       // query heads counted per token
 constexpr uint32_t kTokNeg = 0xFFFFFFFEu;          // token key of negative indices
 constexpr int kAttnD = 128;                        // head dimension of gather_attention
-constexpr int kAttnWaves = 4;
-constexpr int kAttnPerWave = 8;                            // distinct tokens per wave
-constexpr int kAttnTok = kAttnWaves * kAttnPerWave;        // distinct tokens per workgroup
-constexpr int kPartStride = kAttnD + 2;                    // (max, sum, weighted V[128])
+constexpr int kAttnWaves = 2;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kAttnTok = kAttnThreads;             // distinct tokens per workgroup (one per thread)
+constexpr int kPartStride = kAttnD + 2;            // (max, sum, weighted V[128])
+constexpr int kMaxSplit = kMaxGK / kAttnTok;       // workgroups per row at most
 
 template <typename V>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const char *__restrict__ src, int64_t cap,
@@ -232,132 +233,194 @@ __device__ __forceinline__ uint32_t head_count(const uint4 &c, int g) {
   return (g & 1) ? (w >> 16) : (w & 0xFFFFu);
 }
 
-// Partial softmax attention of one workgroup's 32 distinct tokens for the G
-// query heads of row bh.  Lane l holds dimensions 2l and 2l + 1 (bf16 rows of
-// 128 elements: one dword of K and one of V per lane and token).
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
 template <int G>
-__global__ __launch_bounds__(kAttnWaves * kWave) void attn_partial_kernel(const float *__restrict__ q, UnionWs w,
-                                                                          int64_t GK, RowSrc rs, float scale,
-                                                                          float *__restrict__ part, int64_t nsplit) {
-  __shared__ float sm[kAttnWaves][G], sl[kAttnWaves][G];
-  __shared__ float2 so[kAttnWaves][G][kWave];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+struct AttnShared {
+  float q[G][kAttnD];            // the row's query heads
+  float p[kAttnTok][G];          // softmax numerators of the workgroup's tokens
+  int64_t vrow[kAttnTok];        // V row offset in bytes from its base (-1: zero row)
+  uint8_t vrec[kAttnTok];        // 1: the row is in the recent buffer
+  float wm[kAttnWaves][G], wl[kAttnWaves][G];
+  float2 o[G][kWave];            // the second wave's weighted V sums
+};
+
+// Partial softmax attention of one workgroup's 128 distinct tokens for the G
+// query heads of row bh, in two phases:
+//   scores  thread t owns distinct token u0 + t: it reads the whole 256-byte K
+//           row (16 x 16-byte loads) and forms q_g . K for every head g with
+//           the query read from LDS (broadcast), so no cross-lane reductions;
+//           the workgroup's max M_g and numerators c_g e^(s - M_g) follow;
+//   values  lane l of each wave owns dimensions 2l and 2l + 1 and sums
+//           p_g(token) V[token] over its wave's 64 tokens (one coalesced
+//           256-byte V row per wave and token, 8 rows in flight).
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4))) void attn_partial_kernel(const float *__restrict__ q, UnionWs w,
+                                                                    int64_t GK, RowSrc rs, float scale,
+                                                                    float *__restrict__ part, int64_t nsplit) {
+  __shared__ AttnShared<G> sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t bh = blockIdx.y, split = blockIdx.x;
   const int64_t U = w.U[bh];
-  float2 qv[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) qv[g] = reinterpret_cast<const float2 *>(q + (bh * G + g) * kAttnD)[lane];
-  float m[G], l[G];
-  float2 o[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.0f;
-    o[g] = make_float2(0.0f, 0.0f);
-  }
-  const int64_t u0 = split * kAttnTok + wave * kAttnPerWave;
-  // every row of the wave in flight before the first use
-  uint32_t kw[kAttnPerWave], vw[kAttnPerWave];
-  uint4 cn[kAttnPerWave];
-#pragma unroll
-  for (int i = 0; i < kAttnPerWave; ++i) {
-    kw[i] = 0u;
-    vw[i] = 0u;
-    cn[i] = make_uint4(0u, 0u, 0u, 0u);
-    const int64_t u = u0 + i;
-    if (u < U) {
-      const uint64_t ent = w.ulist[bh * GK + u];
-      const uint32_t tok = (uint32_t)(ent >> 32);
-      cn[i] = w.cnt[bh * GK + (uint32_t)ent];
-      bool rec;
-      const int64_t row = rs.locate(tok, bh, rec);
-      if (row >= 0) {
-        kw[i] = reinterpret_cast<const uint32_t *>((rec ? rs.Krec : rs.K) + row * rs.row_bytes)[lane];
-        vw[i] = reinterpret_cast<const uint32_t *>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes)[lane];
-      }
+  for (int e = tid; e < G * kAttnD; e += kAttnThreads) sh.q[e / kAttnD][e % kAttnD] = q[bh * G * kAttnD + e];
+  // ---- scores
+  const int64_t u = split * kAttnTok + tid;
+  uint4 cn = make_uint4(0u, 0u, 0u, 0u);
+  const uint4 *krow = nullptr;
+  int64_t vrow = -1;
+  bool rec = false;
+  if (u < U) {
+    const uint64_t ent = w.ulist[bh * GK + u];
+    cn = w.cnt[bh * GK + (uint32_t)ent];
+    const int64_t row = rs.locate((uint32_t)(ent >> 32), bh, rec);
+    if (row >= 0) {
+      krow = reinterpret_cast<const uint4 *>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
+      vrow = row * rs.row_bytes;
     }
   }
+  sh.vrow[tid] = vrow;
+  sh.vrec[tid] = rec ? 1 : 0;
+  // unconditional loads (no branch per load): threads without a row read the
+  // query array instead and their scores are replaced below
+  const uint4 *kp = krow ? krow : reinterpret_cast<const uint4 *>(q);
+  uint4 kv[kAttnD / 8];
 #pragma unroll
-  for (int i = 0; i < kAttnPerWave; ++i) {
-    const float kx = bf16_bits_to_float((uint16_t)(kw[i] & 0xFFFFu)), ky = bf16_bits_to_float((uint16_t)(kw[i] >> 16));
-    const float vx = bf16_bits_to_float((uint16_t)(vw[i] & 0xFFFFu)), vy = bf16_bits_to_float((uint16_t)(vw[i] >> 16));
-    float s[G];
+  for (int j = 0; j < kAttnD / 8; ++j) kv[j] = kp[j];
+  __syncthreads();  // q staged
+  float s[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) s[g] = fmaf(qv[g].y, ky, qv[g].x * kx);
+  for (int g = 0; g < G; ++g) s[g] = 0.0f;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) s[g] += __shfl_xor(s[g], off, kWave);
-    }
+  for (int j = 0; j < kAttnD / 8; ++j) {
+    const uint32_t d4[4] = {kv[j].x, kv[j].y, kv[j].z, kv[j].w};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const uint32_t c = head_count(cn[i], g);
-      if (c) {
-        const float sc = s[g] * scale;
-        const float mn = fmaxf(m[g], sc);
-        const float a = expf(m[g] - mn);
-        const float p = (float)c * expf(sc - mn);
-        l[g] = fmaf(l[g], a, p);
-        o[g].x = fmaf(o[g].x, a, p * vx);
-        o[g].y = fmaf(o[g].y, a, p * vy);
-        m[g] = mn;
+      const float4 qa = *reinterpret_cast<const float4 *>(&sh.q[g][8 * j]);
+      const float4 qb = *reinterpret_cast<const float4 *>(&sh.q[g][8 * j + 4]);
+      const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t h = d4[e >> 1];
+        const float kf = __uint_as_float((e & 1) ? (h & 0xFFFF0000u) : (h << 16));
+        s[g] = fmaf(qq[e], kf, s[g]);
       }
+      // keep the query reads of at most 4 heads in flight (hoisting them all
+      // costs G * 128 registers)
+      if ((g & 3) == 3 || g == G - 1) __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // every head's reductions before any lane-0 branch, so no score is computed late
+  float c[G], wr[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    if (lane == 0) {
-      sm[wave][g] = m[g];
-      sl[wave][g] = l[g];
-    }
-    so[wave][g][lane] = o[g];
+    c[g] = (float)head_count(cn, g);
+    s[g] = c[g] > 0.0f ? (krow ? s[g] * scale : 0.0f) : -INFINITY;  // a zero row scores 0
+    wr[g] = wave_max_f(s[g]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) sh.wm[wave][g] = wr[g];
   }
   __syncthreads();
-  // merge the waves in wave order: thread (g, lane) of the first G waves' slots
-  for (int e = threadIdx.x; e < G * kWave; e += kAttnWaves * kWave) {
-    const int g = e / kWave, ln = e % kWave;
-    float M = -INFINITY;
+  float M[G];
 #pragma unroll
-    for (int v = 0; v < kAttnWaves; ++v) M = fmaxf(M, sm[v][g]);
-    float L = 0.0f;
-    float2 Ov = make_float2(0.0f, 0.0f);
+  for (int g = 0; g < G; ++g) {
+    M[g] = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < kAttnWaves; ++v) {
-      if (sm[v][g] != -INFINITY) {
-        const float wt = expf(sm[v][g] - M);
-        L = fmaf(sl[v][g], wt, L);
-        Ov.x = fmaf(so[v][g][ln].x, wt, Ov.x);
-        Ov.y = fmaf(so[v][g][ln].y, wt, Ov.y);
+    for (int v = 0; v < kAttnWaves; ++v) M[g] = fmaxf(M[g], sh.wm[v][g]);
+    const float p = c[g] > 0.0f ? c[g] * expf(s[g] - M[g]) : 0.0f;
+    sh.p[tid][g] = p;
+    wr[g] = wave_sum_f(p);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) sh.wl[wave][g] = wr[g];
+  }
+  __syncthreads();
+  // ---- values: wave v sums tokens [64 v, 64 v + 64)
+  float2 o[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) o[g] = make_float2(0.0f, 0.0f);
+  const int t0 = wave * kWave;
+#pragma unroll 1
+  for (int r0 = 0; r0 < kWave; r0 += 8) {
+    uint32_t vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // unconditional loads; rows without data read q and are zeroed
+      const int64_t vr = sh.vrow[t0 + r0 + i];
+      const char *vb = vr >= 0 ? (sh.vrec[t0 + r0 + i] ? rs.Vrec : rs.V) + vr : reinterpret_cast<const char *>(q);
+      vv[i] = reinterpret_cast<const uint32_t *>(vb)[lane];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t vi = sh.vrow[t0 + r0 + i] >= 0 ? vv[i] : 0u;
+      const float vx = __uint_as_float(vi << 16), vy = __uint_as_float(vi & 0xFFFF0000u);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = sh.p[t0 + r0 + i][g];
+        o[g].x = fmaf(p, vx, o[g].x);
+        o[g].y = fmaf(p, vy, o[g].y);
       }
     }
-    float *pp = part + ((bh * nsplit + split) * G + g) * kPartStride;
-    if (ln == 0) {
-      pp[0] = M;
-      pp[1] = L;
+  }
+  if (wave == 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) sh.o[g][lane] = o[g];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float *pp = part + ((bh * nsplit + split) * G + g) * kPartStride;
+      if (lane == 0) {
+        pp[0] = M[g];
+        pp[1] = sh.wl[0][g] + sh.wl[1][g];
+      }
+      pp[2 + 2 * lane] = o[g].x + sh.o[g][lane].x;
+      pp[3 + 2 * lane] = o[g].y + sh.o[g][lane].y;
     }
-    pp[2 + 2 * ln] = Ov.x;
-    pp[3 + 2 * ln] = Ov.y;
   }
 }
 
-// out[bh, g, d] = sum_s O_s e^(M_s - M) / sum_s L_s e^(M_s - M), splits in order.
+// out[bh, g, d] = sum_s O_s e^(M_s - M) / sum_s L_s e^(M_s - M) over the
+// row's splits (<= kMaxSplit), in split order.
 __global__ __launch_bounds__(kAttnD) void attn_merge_kernel(const float *__restrict__ part, int64_t G,
                                                             int64_t nsplit, float *__restrict__ out) {
+  __shared__ float wt[kMaxSplit];
+  __shared__ float s_L;
   const int64_t r = blockIdx.x;  // bh * G + g
   const int64_t bh = r / G, g = r % G;
   const int d = threadIdx.x;
-  float M = -INFINITY;
-  for (int64_t s = 0; s < nsplit; ++s) M = fmaxf(M, part[((bh * nsplit + s) * G + g) * kPartStride]);
-  float L = 0.0f, Od = 0.0f;
-  for (int64_t s = 0; s < nsplit; ++s) {
-    const float *pp = part + ((bh * nsplit + s) * G + g) * kPartStride;
-    if (pp[0] != -INFINITY) {
-      const float wt = expf(pp[0] - M);
-      L = fmaf(pp[1], wt, L);
-      Od = fmaf(pp[2 + d], wt, Od);
+  const float *base = part + (bh * nsplit * G + g) * kPartStride;  // split s at + s * G * kPartStride
+  const int64_t sstride = G * kPartStride;
+  if (d < nsplit) wt[d] = base[d * sstride];
+  __syncthreads();
+  if (d == 0) {
+    float M = -INFINITY;
+    for (int s = 0; s < (int)nsplit; ++s) M = fmaxf(M, wt[s]);
+    float L = 0.0f;
+    for (int s = 0; s < (int)nsplit; ++s) {
+      const float e = wt[s] == -INFINITY ? 0.0f : expf(wt[s] - M);
+      wt[s] = e;
+      L = fmaf(base[s * sstride + 1], e, L);
     }
+    s_L = L;
   }
-  out[r * kAttnD + d] = Od / L;
+  __syncthreads();
+  float Od = 0.0f;
+  for (int s0 = 0; s0 < (int)nsplit; s0 += 8) {
+    float ov[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ov[i] = s0 + i < nsplit ? base[(s0 + i) * sstride + 2 + d] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (s0 + i < nsplit) Od = fmaf(ov[i], wt[s0 + i], Od);
+  }
+  out[r * kAttnD + d] = Od / s_L;
 }
 
 int hash_bits(int64_t GK) {
@@ -375,8 +438,8 @@ int launch_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t k, int64_t 
 template <int G>
 void launch_attn_g(const float *q, const UnionWs &w, int64_t BH, int64_t GK, const RowSrc &rs, float scale, float *part,
                    int64_t nsplit, hipStream_t st) {
-  attn_partial_kernel<G><<<dim3((unsigned)nsplit, (unsigned)BH), kAttnWaves * kWave, 0, st>>>(q, w, GK, rs, scale,
-                                                                                               part, nsplit);
+  attn_partial_kernel<G><<<dim3((unsigned)nsplit, (unsigned)BH), kAttnThreads, 0, st>>>(q, w, GK, rs, scale, part,
+                                                                                         nsplit);
 }
 
 }  // namespace

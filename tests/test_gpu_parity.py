@@ -595,3 +595,34 @@ def test_decode_layer_c5(layer):
     ref, rnu = O.gather_attention(x["q"].numpy(), idx.cpu().numpy(), 8192, K.float().numpy(), V.float().numpy())
     _attn_close(out.cpu().numpy(), ref)
     np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
+
+
+def test_decode_layer_graph_replays_equal_eager():
+    """plan -> fused scan + top-k -> gather + attention captured in one HIP graph:
+    every replay (with eager work and synchronisations between replays) equals
+    the eager result bit for bit."""
+    x = W.config_inputs(5, device="cpu", n=6000, BH=2, layer=3)
+    K, q, g = x["K"].to(DEV), x["q"].to(DEV), x["g"].to(DEV)
+    V = W.synth_values(2, 6000, seed=7).to(DEV)
+    st = bp.PlaneStore(K)
+
+    def layer():
+        plan = bp.make_plan(g, x["budget"])
+        idx = st.scan_topk(q, plan, x["k"], x["sink"], x["local"])
+        return idx, off.gather_attention(q, idx, 6000, K, V, 6000)[0]
+
+    ref_idx, ref_out = layer()
+    torch.cuda.synchronize()
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        gi, go = layer()
+    for rep in range(3):
+        gi.zero_()
+        go.zero_()
+        gph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gi, ref_idx), f"replay {rep}: index sets differ"
+        assert torch.equal(go, ref_out), f"replay {rep}: attention output differs"
+        e_idx, e_out = layer()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(e_idx, ref_idx) and torch.equal(e_out, ref_out)
