@@ -27,6 +27,10 @@ PROTOTYPES = {
     "fathom_make_plan": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "fathom_scan_planes": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp, _vp]),
+    "fathom_pack_chan4": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "fathom_quantise_chan4": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "fathom_channel_list": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "fathom_scan_chan4": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "fathom_scan_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "fathom_scan_topk": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _vp, _vp, _sz, _vp]),

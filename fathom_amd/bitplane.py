@@ -33,8 +33,9 @@ BLK, SUB, D = 64, 16, 128
 SBT = BLK * SUB
 
 __all__ = ["BLK", "SUB", "D", "SBT", "quantise_u4", "dequant_planes", "pack_planes", "unpack_planes",
-           "to_superblocks", "bytes_planes", "make_plan", "make_plan_torch", "scan_planes_reference",
-           "PlaneStore", "sink_local_topk"]
+           "to_superblocks", "pack_chan4", "bytes_planes", "bytes_chan4", "make_plan", "make_plan_torch",
+           "channel_list", "scan_planes_reference", "scan_chan4_reference", "PlaneStore", "Chan4Store",
+           "sink_local_topk"]
 
 
 # ----------------------------------------------------------------------------- helpers
@@ -145,6 +146,39 @@ def to_superblocks(planes, scales):
     _lib.call("fathom_to_superblocks", _ptr(planes), _ptr(scales), scales.element_size(), _lead(lead), nb, d, sub,
               _ptr(pl), _ptr(sc), _stream(planes.device))
     return pl, sc
+
+
+def pack_chan4(code):
+    """codes uint8 [..., n, D] -> the channel-major 4-bit store int32 [..., nsb, D, SUB, 8]
+    (word m of a (channel, block) holds tokens 8m..8m+7, nibble k = token 8m + k;
+    zero padded to whole superblocks of SUB blocks) -- kernels/bitplane.py:67-74."""
+    _need_gpu(code)
+    code = code.contiguous().to(torch.uint8)
+    *lead, n, d = code.shape
+    sub = int(SUB)
+    nsb = math.ceil(math.ceil(n / BLK) / sub)
+    words = torch.empty(*lead, nsb, d, sub, 8, dtype=torch.int32, device=code.device)
+    _lib.call("fathom_pack_chan4", _ptr(code), _lead(lead), n, d, sub, _ptr(words), _stream(code.device))
+    return words
+
+
+def bytes_chan4(nact, n):
+    """Bytes a chan4 scan moves: (32 + 2) per listed channel and 64-token block --
+    kernels/bitplane.py:79-80."""
+    nb = math.ceil(n / BLK)
+    return float((nact.float() * (32 + 2) * nb).sum())
+
+
+def channel_list(active):
+    """active bool [BH, D] -> (act int32 [BH, D]: listed channels first, ascending,
+    then the others; nact int32 [BH]) -- kernels/bitplane.py:128-132."""
+    _need_gpu(active)
+    BH, d = active.shape
+    a8 = active.contiguous().to(torch.uint8)
+    act = torch.empty(BH, d, dtype=torch.int32, device=active.device)
+    nact = torch.empty(BH, dtype=torch.int32, device=active.device)
+    _lib.call("fathom_channel_list", _ptr(a8), BH, d, _ptr(act), _ptr(nact), _stream(active.device))
+    return act, nact
 
 
 def bytes_planes(t, n):
@@ -284,6 +318,58 @@ class PlaneStore:
             self.BH * self.nsb * D * int(getattr(self, "sub", SUB)) * 2
 
 
+class Chan4Store:
+    """K [BH, n, D] -> the chan4 baseline store (kernels/bitplane.py:342-355): codes,
+    block scales, chan_k int32 [BH, nsb, D, SUB, 8] and scales_k fp16 [BH, nsb, D, SUB],
+    built in one pass on the GPU.  scan(q, act, nact) reads the nact listed channels
+    of each row at full depth; like PlaneStore, chan_k / scales_k may be replaced by
+    DevPtr objects into mapped host memory."""
+
+    cfg = {"NB": 2, "KK": 1, "num_warps": 1, "num_stages": 1}
+
+    def __init__(self, K, scale_dtype=torch.float16, keep_code=True):
+        _need_gpu(K)
+        self.BH, self.n, d = K.shape
+        if d != D:
+            raise AssertionError(f"Chan4Store needs D == {D}, got {d}")
+        if scale_dtype not in _KDT:
+            raise ValueError(f"scale_dtype {scale_dtype} unsupported")
+        Kc = _key_input(K)
+        dev = K.device
+        nb = math.ceil(self.n / BLK)
+        self.sub = int(SUB)
+        self.nsb = math.ceil(nb / self.sub)
+        self.code = torch.empty(self.BH, self.n, d, dtype=torch.uint8, device=dev) if keep_code else None
+        self.scales_blk = torch.empty(self.BH, nb, d, dtype=scale_dtype, device=dev)
+        self.chan_k = torch.empty(self.BH, self.nsb, d, self.sub, 8, dtype=torch.int32, device=dev)
+        self.scales_k = torch.empty(self.BH, self.nsb, d, self.sub, dtype=torch.float16, device=dev)
+        _lib.call("fathom_quantise_chan4", _ptr(Kc), _KDT[Kc.dtype], self.BH, self.n, d, _KDT[scale_dtype], self.sub,
+                  _ptr(self.code), _ptr(self.scales_blk), _ptr(self.chan_k), _ptr(self.scales_k), _stream(dev))
+
+    def scan(self, q, act, nact, out=None, blocks=None):
+        """q [BH, G, D] fp32, act/nact from channel_list -> scores fp32 [BH, G, n];
+        blocks=(b0, b1) scans only 64-token blocks [b0, b1) into `out`."""
+        _need_gpu(q, act, nact)
+        BH, G, d = q.shape
+        if BH != self.BH:
+            raise AssertionError(f"q has BH={BH}, store has {self.BH}")
+        out = torch.empty(BH, G, self.n, device=q.device, dtype=torch.float32) if out is None else out
+        if out.dtype != torch.float32 or not out.is_contiguous() or tuple(out.shape) != (BH, G, self.n):
+            raise ValueError(f"out must be a contiguous float32 [{BH}, {G}, {self.n}] tensor")
+        nb = math.ceil(self.n / BLK)
+        b0, b1 = (0, nb) if blocks is None else (int(blocks[0]), int(blocks[1]))
+        qc = q.contiguous().float()
+        a32 = act.to(torch.int32).contiguous()
+        n32 = nact.to(torch.int32).contiguous()
+        _lib.call("fathom_scan_chan4", _ptr(qc), BH, G, d, _ptr(a32), _ptr(n32),
+                  ctypes.c_void_p(self.chan_k.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), self.n,
+                  int(self.nsb), int(self.sub), b0, b1, _ptr(out), _stream(q.device))
+        return out
+
+    def nbytes(self):
+        return self.BH * self.nsb * D * self.sub * (32 + 2)
+
+
 def scan_planes_reference(q, code, scales, t):
     """q [BH, G, D], code uint8 [BH, n, D], scales [BH, nblk, D], t [BH, D] ->
     [BH, G, n]: q @ dequant_planes(...)^T per row (kernels/bitplane.py:357-363);
@@ -292,6 +378,17 @@ def scan_planes_reference(q, code, scales, t):
     for b in range(q.shape[0]):
         val = dequant_planes(code[b], scales[b], t[b].long())
         out.append(q[b].float() @ val.T)
+    return torch.stack(out)
+
+
+def scan_chan4_reference(q, code, scales, active):
+    """[BH, G, n] = q @ (full-depth dequantised codes masked to the active channels)^T
+    (kernels/bitplane.py:365-370); dequantisation in the gfx950 kernel, the product a
+    library GEMM."""
+    out = []
+    for b in range(q.shape[0]):
+        val = dequant_planes(code[b], scales[b], torch.full((code.shape[-1],), 4, device=code.device))
+        out.append(q[b].float() @ (val * active[b].float()[None]).T)
     return torch.stack(out)
 
 

@@ -1,4 +1,5 @@
-// Store build: 4-bit quantiser and bit-plane packers (lane = channel layout).
+// Store build: 4-bit quantiser, bit-plane packers and the channel-major
+// nibble store of the chan4 baseline (lane = channel layout).
 //
 // A wave owns 64 consecutive channels of one 64-token block: every key load is
 // a coalesced row segment, each lane keeps its channel's 64 values in
@@ -13,14 +14,25 @@ namespace {
 
 constexpr int kBlocksPerWG = 16;
 
-template <int KDT, int SDT>
+// Nibble words of one (channel, block) of the chan4 store [.., nsb, D, sub, 8]:
+// word m holds tokens 8m..8m+7, nibble k = token 8m + k (kernels/bitplane.py:67-74).
+__device__ __forceinline__ void store_chan4_words(uint32_t *chan_sb, const uint32_t (&cw)[8], int64_t bh, int64_t sb,
+                                                  int64_t bs, int64_t j, int64_t D, int64_t sub, int64_t nsb) {
+  uint4 *dst = reinterpret_cast<uint4 *>(chan_sb + (((bh * nsb + sb) * D + j) * sub + bs) * 8);
+  dst[0] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+  dst[1] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+}
+
+// C4: also (or instead of the planes) write the chan4 nibble store chan_sb.
+template <int KDT, int SDT, bool C4>
 __global__ __launch_bounds__(256) void quantise_pack_kernel(const void *__restrict__ K, int64_t n, int64_t D,
                                                             int64_t nblk, int64_t nblk_cover, int64_t sub,
                                                             int64_t nsb, uint8_t *__restrict__ code,
                                                             void *__restrict__ scales_blk,
                                                             uint64_t *__restrict__ planes_log,
                                                             uint64_t *__restrict__ planes_sb,
-                                                            uint16_t *__restrict__ scales_sb) {
+                                                            uint16_t *__restrict__ scales_sb,
+                                                            uint32_t *__restrict__ chan_sb) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t j = (int64_t)blockIdx.y * 64 + lane;
   const int64_t bh = blockIdx.z;
@@ -29,6 +41,7 @@ __global__ __launch_bounds__(256) void quantise_pack_kernel(const void *__restri
     const int64_t b = (int64_t)blockIdx.x * kBlocksPerWG + r * 4 + wave;
     if (b >= nblk_cover) return;
     uint32_t wl[4] = {0u, 0u, 0u, 0u}, wh[4] = {0u, 0u, 0u, 0u};
+    uint32_t cw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
     uint16_t s16 = 0;  // fp16 bits of the superblock-store scale
     if (b < nblk) {
       const int64_t tok0 = b * kBlk;
@@ -69,6 +82,7 @@ __global__ __launch_bounds__(256) void quantise_pack_kernel(const void *__restri
         const bool real = tok0 + i < n;
         if (code && real) code[base + (int64_t)i * D] = (uint8_t)c;
         const uint32_t cb = real ? (uint32_t)c : 0u;  // pack_planes pads with code 0
+        if (C4) cw[i >> 3] |= cb << (4 * (i & 7));
         if (i < 32) {
           wl[0] |= ((cb >> 3) & 1u) << i;
           wl[1] |= ((cb >> 2) & 1u) << i;
@@ -87,11 +101,14 @@ __global__ __launch_bounds__(256) void quantise_pack_kernel(const void *__restri
         for (int p = 0; p < 4; ++p) P[p] = ((uint64_t)wh[p] << 32) | wl[p];
       }
     }
-    if (planes_sb) {
+    if (planes_sb || C4) {
       const int64_t sb = b / sub, bs = b - (b / sub) * sub;
-      uint64_t *P = planes_sb + ((bh * nsb + sb) * D + j) * 4 * sub + bs;
+      if (planes_sb) {
+        uint64_t *P = planes_sb + ((bh * nsb + sb) * D + j) * 4 * sub + bs;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) P[p * sub] = ((uint64_t)wh[p] << 32) | wl[p];
+        for (int p = 0; p < 4; ++p) P[p * sub] = ((uint64_t)wh[p] << 32) | wl[p];
+      }
+      if (C4) store_chan4_words(chan_sb, cw, bh, sb, bs, j, D, sub, nsb);
       scales_sb[((bh * nsb + sb) * D + j) * sub + bs] = s16;
     }
   }
@@ -127,6 +144,27 @@ __global__ __launch_bounds__(256) void pack_planes_kernel(const uint8_t *__restr
     uint64_t *P = planes + ((bh * nblk + b) * D + j) * 4;
 #pragma unroll
     for (int p = 0; p < 4; ++p) P[p] = ((uint64_t)wh[p] << 32) | wl[p];
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_chan4_kernel(const uint8_t *__restrict__ code, int64_t n, int64_t D,
+                                                         int64_t nblk_cover, int64_t sub, int64_t nsb,
+                                                         uint32_t *__restrict__ chan_sb) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t j = (int64_t)blockIdx.y * 64 + lane;
+  const int64_t bh = blockIdx.z;
+  if (j >= D) return;
+  for (int r = 0; r < kBlocksPerWG / 4; ++r) {
+    const int64_t b = (int64_t)blockIdx.x * kBlocksPerWG + r * 4 + wave;
+    if (b >= nblk_cover) return;
+    const int64_t tok0 = b * kBlk;
+    uint32_t cw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < kBlk; ++i) {
+      const uint32_t cb = (tok0 + i < n) ? (uint32_t)(code[(bh * n + tok0 + i) * D + j] & 15u) : 0u;
+      cw[i >> 3] |= cb << (4 * (i & 7));
+    }
+    store_chan4_words(chan_sb, cw, bh, b / sub, b - (b / sub) * sub, j, D, sub, nsb);
   }
 }
 
@@ -205,26 +243,43 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
   }
 }
 
-template <int KDT>
+template <int KDT, bool C4>
 int launch_quantise(const void *K, int64_t lead, int64_t n, int64_t D, int sdt, int64_t nblk, int64_t cover,
                     int64_t sub, int64_t nsb, uint8_t *code, void *scales_blk, uint64_t *planes_log,
-                    uint64_t *planes_sb, uint16_t *scales_sb, hipStream_t st) {
+                    uint64_t *planes_sb, uint16_t *scales_sb, uint32_t *chan_sb, hipStream_t st) {
   dim3 grid((unsigned)cdiv(cover, kBlocksPerWG), (unsigned)cdiv(D, 64), (unsigned)lead);
   switch (sdt) {
     case FATHOM_DT_F16:
-      quantise_pack_kernel<KDT, FATHOM_DT_F16><<<grid, 256, 0, st>>>(K, n, D, nblk, cover, sub, nsb, code,
-                                                                     scales_blk, planes_log, planes_sb, scales_sb);
+      quantise_pack_kernel<KDT, FATHOM_DT_F16, C4><<<grid, 256, 0, st>>>(
+          K, n, D, nblk, cover, sub, nsb, code, scales_blk, planes_log, planes_sb, scales_sb, chan_sb);
       break;
     case FATHOM_DT_BF16:
-      quantise_pack_kernel<KDT, FATHOM_DT_BF16><<<grid, 256, 0, st>>>(K, n, D, nblk, cover, sub, nsb, code,
-                                                                      scales_blk, planes_log, planes_sb, scales_sb);
+      quantise_pack_kernel<KDT, FATHOM_DT_BF16, C4><<<grid, 256, 0, st>>>(
+          K, n, D, nblk, cover, sub, nsb, code, scales_blk, planes_log, planes_sb, scales_sb, chan_sb);
       break;
     default:
-      quantise_pack_kernel<KDT, FATHOM_DT_F32><<<grid, 256, 0, st>>>(K, n, D, nblk, cover, sub, nsb, code,
-                                                                     scales_blk, planes_log, planes_sb, scales_sb);
+      quantise_pack_kernel<KDT, FATHOM_DT_F32, C4><<<grid, 256, 0, st>>>(
+          K, n, D, nblk, cover, sub, nsb, code, scales_blk, planes_log, planes_sb, scales_sb, chan_sb);
       break;
   }
   return launch_status("quantise_pack_kernel");
+}
+
+template <bool C4>
+int quantise_dispatch(const void *K, int k_dtype, int64_t lead, int64_t n, int64_t D, int sdt, int64_t nblk,
+                      int64_t cover, int64_t sub, int64_t nsb, uint8_t *code, void *scales_blk, uint64_t *planes_log,
+                      uint64_t *planes_sb, uint16_t *scales_sb, uint32_t *chan_sb, hipStream_t st) {
+  switch (k_dtype) {
+    case FATHOM_DT_F16:
+      return launch_quantise<FATHOM_DT_F16, C4>(K, lead, n, D, sdt, nblk, cover, sub, nsb, code, scales_blk,
+                                                planes_log, planes_sb, scales_sb, chan_sb, st);
+    case FATHOM_DT_BF16:
+      return launch_quantise<FATHOM_DT_BF16, C4>(K, lead, n, D, sdt, nblk, cover, sub, nsb, code, scales_blk,
+                                                 planes_log, planes_sb, scales_sb, chan_sb, st);
+    default:
+      return launch_quantise<FATHOM_DT_F32, C4>(K, lead, n, D, sdt, nblk, cover, sub, nsb, code, scales_blk,
+                                                planes_log, planes_sb, scales_sb, chan_sb, st);
+  }
 }
 
 bool valid_dtype(int dt) { return dt == FATHOM_DT_F32 || dt == FATHOM_DT_F16 || dt == FATHOM_DT_BF16; }
@@ -256,18 +311,36 @@ extern "C" int fathom_quantise_pack(const void *K, int k_dtype, int64_t lead, in
   int rc = check_grid(lead, D, cover, "quantise_pack");
   if (rc) return rc;
   if (!code && !scales_blk && !planes_log && !planes_sb) return FATHOM_OK;
-  hipStream_t st = (hipStream_t)stream;
-  switch (k_dtype) {
-    case FATHOM_DT_F16:
-      return launch_quantise<FATHOM_DT_F16>(K, lead, n, D, scale_dtype, nblk, cover, sub, nsb, code, scales_blk,
-                                            planes_log, planes_sb, scales_sb, st);
-    case FATHOM_DT_BF16:
-      return launch_quantise<FATHOM_DT_BF16>(K, lead, n, D, scale_dtype, nblk, cover, sub, nsb, code, scales_blk,
-                                             planes_log, planes_sb, scales_sb, st);
-    default:
-      return launch_quantise<FATHOM_DT_F32>(K, lead, n, D, scale_dtype, nblk, cover, sub, nsb, code, scales_blk,
-                                            planes_log, planes_sb, scales_sb, st);
-  }
+  return quantise_dispatch<false>(K, k_dtype, lead, n, D, scale_dtype, nblk, cover, sub, nsb, code, scales_blk,
+                                  planes_log, planes_sb, scales_sb, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int fathom_quantise_chan4(const void *K, int k_dtype, int64_t lead, int64_t n, int64_t D, int scale_dtype,
+                                     int64_t sub, uint8_t *code, void *scales_blk, uint32_t *chan_sb,
+                                     uint16_t *scales_sb, void *stream) {
+  if (!K || !chan_sb || !scales_sb) return fail(FATHOM_ERR_INVALID, "quantise_chan4: null pointer");
+  if (!valid_dtype(k_dtype) || !valid_dtype(scale_dtype)) return fail(FATHOM_ERR_INVALID, "quantise_chan4: bad dtype");
+  if (n < 1 || sub < 1) return fail(FATHOM_ERR_INVALID, "quantise_chan4: n=%lld sub=%lld", (long long)n, (long long)sub);
+  if (reinterpret_cast<uintptr_t>(chan_sb) & 15) return fail(FATHOM_ERR_INVALID, "quantise_chan4: chan_sb not 16-byte aligned");
+  const int64_t nblk = cdiv(n, kBlk);
+  const int64_t nsb = cdiv(nblk, sub);
+  int rc = check_grid(lead, D, nsb * sub, "quantise_chan4");
+  if (rc) return rc;
+  return quantise_dispatch<true>(K, k_dtype, lead, n, D, scale_dtype, nblk, nsb * sub, sub, nsb, code, scales_blk,
+                                 nullptr, nullptr, scales_sb, chan_sb, (hipStream_t)stream);
+}
+
+extern "C" int fathom_pack_chan4(const uint8_t *code, int64_t lead, int64_t n, int64_t D, int64_t sub, uint32_t *chan_sb,
+                                 void *stream) {
+  if (!code || !chan_sb) return fail(FATHOM_ERR_INVALID, "pack_chan4: null pointer");
+  if (n < 1 || sub < 1) return fail(FATHOM_ERR_INVALID, "pack_chan4: n=%lld sub=%lld", (long long)n, (long long)sub);
+  if (reinterpret_cast<uintptr_t>(chan_sb) & 15) return fail(FATHOM_ERR_INVALID, "pack_chan4: chan_sb not 16-byte aligned");
+  const int64_t nsb = cdiv(cdiv(n, kBlk), sub);
+  int rc = check_grid(lead, D, nsb * sub, "pack_chan4");
+  if (rc) return rc;
+  dim3 grid((unsigned)cdiv(nsb * sub, kBlocksPerWG), (unsigned)cdiv(D, 64), (unsigned)lead);
+  pack_chan4_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(code, n, D, nsb * sub, sub, nsb, chan_sb);
+  return launch_status("pack_chan4_kernel");
 }
 
 extern "C" int fathom_pack_planes(const uint8_t *code, int64_t lead, int64_t n, int64_t D, uint64_t *planes,

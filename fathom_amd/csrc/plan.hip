@@ -118,6 +118,32 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
   }
 }
 
+// channel_list (kernels/bitplane.py:128-132): the listed channels of a row
+// first, ascending, then the others, ascending (a stable sort of ~active); one
+// wave per row, 64 channels per step with ballot prefix counts.
+__global__ __launch_bounds__(64) void channel_list_kernel(const uint8_t *__restrict__ active, int64_t D,
+                                                          int32_t *__restrict__ act, int32_t *__restrict__ nact) {
+  const int lane = threadIdx.x;
+  const int64_t bh = blockIdx.x;
+  const uint8_t *a = active + bh * D;
+  int total = 0;
+  for (int64_t j0 = 0; j0 < D; j0 += kWave) {
+    const bool on = j0 + lane < D && a[j0 + lane] != 0;
+    total += __popcll(__ballot(on));
+  }
+  int on_base = 0, off_base = total;
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int64_t j0 = 0; j0 < D; j0 += kWave) {
+    const bool in = j0 + lane < D;
+    const bool on = in && a[j0 + lane] != 0;
+    const uint64_t mon = __ballot(on), moff = __ballot(in && !on);
+    if (in) act[bh * D + (on ? on_base + __popcll(mon & below) : off_base + __popcll(moff & below))] = (int32_t)(j0 + lane);
+    on_base += __popcll(mon);
+    off_base += __popcll(moff);
+  }
+  if (lane == 0) nact[bh] = total;
+}
+
 }  // namespace
 }  // namespace fathom
 
@@ -141,4 +167,12 @@ extern "C" int fathom_make_plan(const float *g, const float *budget, int64_t BH,
   else
     plan_kernel<4><<<(unsigned)BH, 64, 0, st>>>(g, budget, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
   return launch_status("plan_kernel");
+}
+
+extern "C" int fathom_channel_list(const uint8_t *active, int64_t BH, int64_t D, int32_t *act, int32_t *nact,
+                                   void *stream) {
+  if (!active || !act || !nact) return fail(FATHOM_ERR_INVALID, "channel_list: null pointer");
+  if (BH < 1 || BH > 0x7FFFFFFF || D < 1) return fail(FATHOM_ERR_INVALID, "channel_list: BH=%lld D=%lld", (long long)BH, (long long)D);
+  channel_list_kernel<<<(unsigned)BH, kWave, 0, (hipStream_t)stream>>>(active, D, act, nact);
+  return launch_status("channel_list_kernel");
 }

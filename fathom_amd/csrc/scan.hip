@@ -489,6 +489,156 @@ __global__ __launch_bounds__(kThreads) void scan_tile_kernel(ScanArgs a, Emit em
   emit_group<G, MODE>(em, es, acc, bh, tb0 + wave * kGB, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
 }
 
+// --------------------------------------------------------------------- chan4 baseline scan
+// The channel-major 4-bit store (kernels/bitplane.py:67-74 pack_chan4,
+// :175-198 scan_chan4_kernel): word m of (channel j, block b) holds the codes of
+// tokens 8m..8m+7 of the block, nibble k = token 8m + k.  Every listed channel
+// is read at full depth, 32 + 2 bytes per (channel, block).  Same tile and
+// head contraction as the plane scan: y = 2a (c - 7.5) = c * 2a - 15a (one
+// FMA of exact operands), w = q / 16, acc += w * y on the matrix cores, in
+// list order, so a chan4 scan equals the plane scan of a plan with t = 4 on
+// the same channels bit for bit.
+constexpr int kC4Chan = 8;                 // channels per staged chunk
+constexpr int kC4Row = kTB + 4;            // padded LDS row of one word index over the tile's blocks
+
+struct Chan4Args {
+  const float *q;            // [BH, G, D]
+  const int32_t *act;        // [BH, D] listed channels first
+  const int32_t *nact;       // [BH]
+  const uint4 *chan;         // [BH, nsb, D, sub, 8] uint32 words as 16-byte halves
+  const uint16_t *scales;    // [BH, nsb, D, sub] fp16 bits
+  int64_t n, nsb, sub, blk0, blk_end, tile0;
+  int D;
+};
+
+template <int G>
+struct C4Buf {
+  alignas(16) uint32_t w[kC4Chan][8][kC4Row];  // [channel slot][word m][block]
+  alignas(16) float P[kC4Chan][kTB];           // 2a
+  alignas(16) float Q[kC4Chan][kTB];           // -15a
+  alignas(16) float wq[kC4Chan][QShared<G>::QS];
+};
+
+template <int G>
+struct C4Shared {
+  QShared<G> qs;
+  uint8_t lst[kMaxD];
+  C4Buf<G> buf[2];
+};
+
+// A thread stages two 16-byte halves (item e = tid + 256 h: channel slot e / 64,
+// block (e / 2) % 32, half e % 2) and the scale of (slot tid / 32, block tid % 32).
+struct C4Staged {
+  uint4 v[2];
+  uint16_t s;
+};
+
+__device__ __forceinline__ void c4_load(C4Staged &r, const Chan4Args &a, const uint8_t *lst, int i0, int m, int64_t bh,
+                                        int64_t tb0, int tid) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = tid + kThreads * h, ci = e >> 6, b = (e >> 1) & (kTB - 1), half = e & 1;
+    const int64_t blk = tb0 + b;
+    r.v[h] = make_uint4(0u, 0u, 0u, 0u);
+    if (ci < m && blk < a.nsb * a.sub) {
+      const int64_t sb = blk / a.sub, off = blk - sb * a.sub;
+      r.v[h] = a.chan[(((bh * a.nsb + sb) * a.D + lst[i0 + ci]) * a.sub + off) * 2 + half];
+    }
+  }
+  const int ci = tid >> 5, b = tid & (kTB - 1);
+  const int64_t blk = tb0 + b;
+  r.s = 0;
+  if (ci < m && blk < a.nsb * a.sub) {
+    const int64_t sb = blk / a.sub, off = blk - sb * a.sub;
+    r.s = a.scales[((bh * a.nsb + sb) * a.D + lst[i0 + ci]) * a.sub + off];
+  }
+}
+
+template <int G>
+__device__ __forceinline__ void c4_store(C4Buf<G> &bf, const C4Staged &r, const QShared<G> &qs, const uint8_t *lst,
+                                         int i0, int m, int tid) {
+  constexpr int QS = QShared<G>::QS;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = tid + kThreads * h, ci = e >> 6, b = (e >> 1) & (kTB - 1), half = e & 1;
+    bf.w[ci][4 * half + 0][b] = r.v[h].x;
+    bf.w[ci][4 * half + 1][b] = r.v[h].y;
+    bf.w[ci][4 * half + 2][b] = r.v[h].z;
+    bf.w[ci][4 * half + 3][b] = r.v[h].w;
+  }
+  const int ci = tid >> 5, b = tid & (kTB - 1);
+  const float a = __half2float(__ushort_as_half(r.s));
+  bf.P[ci][b] = 2.0f * a;
+  bf.Q[ci][b] = -15.0f * a;
+  if (b < QS && ci < m) bf.wq[ci][b] = qs.w[lst[i0 + ci] * QS + b];
+}
+
+template <int G>
+__device__ __forceinline__ void c4_compute(const C4Buf<G> &bf, int m, int wave, int lane, Acc<G> &acc) {
+  const int wm = lane >> 3, sh = 4 * (lane & 7);
+  for (int ci = 0; ci < m; ++ci) {
+    QOp<G> q;
+#pragma unroll
+    for (int h = 0; h < QOp<G>::NQ; ++h) q.a[h] = bf.wq[ci][4 * h + (lane & 3)];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint4 w4 = *reinterpret_cast<const uint4 *>(&bf.w[ci][wm][wave * kGB + 4 * hf]);
+      const float4 P4 = *reinterpret_cast<const float4 *>(&bf.P[ci][wave * kGB + 4 * hf]);
+      const float4 Q4 = *reinterpret_cast<const float4 *>(&bf.Q[ci][wave * kGB + 4 * hf]);
+      const uint32_t wd[4] = {w4.x, w4.y, w4.z, w4.w};
+      const float P[4] = {P4.x, P4.y, P4.z, P4.w}, Q[4] = {Q4.x, Q4.y, Q4.z, Q4.w};
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = fmaf((float)__builtin_amdgcn_ubfe(wd[r], sh, 4), P[r], Q[r]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) accum<G>(acc, 4 * hf + r, q, y[r]);
+    }
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void scan_chan4_kernel(Chan4Args a, Emit em) {
+  constexpr int QS = QShared<G>::QS;
+  __shared__ C4Shared<G> sh;
+  __shared__ EmitShared<G> es;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t bh = blockIdx.y;
+  const int64_t tb0 = (a.tile0 + (int64_t)blockIdx.x) * kTB;
+  const int na = min(max(ld_uniform(a.nact + bh), 0), a.D);
+  for (int i = tid; i < na; i += kThreads) {
+    const int j = min(max(a.act[bh * a.D + i], 0), a.D - 1);  // memory-safe
+    sh.lst[i] = (uint8_t)j;
+#pragma unroll
+    for (int g = 0; g < QS; ++g) sh.qs.w[j * QS + g] = g < G ? ldexpf(a.q[(bh * G + g) * a.D + j], -4) : 0.0f;
+  }
+  Acc<G> acc;
+  acc.zero();
+  if (tb0 < a.blk_end && tb0 + kTB > a.blk0 && na > 0) {
+    __syncthreads();
+    C4Staged r;
+    const int nk = (na + kC4Chan - 1) / kC4Chan;
+    c4_load(r, a, sh.lst, 0, min(kC4Chan, na), bh, tb0, tid);
+    c4_store<G>(sh.buf[0], r, sh.qs, sh.lst, 0, min(kC4Chan, na), tid);
+    __syncthreads();
+    for (int k = 0; k < nk; ++k) {
+      const int i0 = k * kC4Chan, m = min(kC4Chan, na - i0);
+      const bool more = k + 1 < nk;
+      const int i1 = i0 + kC4Chan, m1 = min(kC4Chan, na - i1);
+      if (more) c4_load(r, a, sh.lst, i1, m1, bh, tb0, tid);
+      c4_compute<G>(sh.buf[k & 1], m, wave, lane, acc);
+      if (more) c4_store<G>(sh.buf[(k + 1) & 1], r, sh.qs, sh.lst, i1, m1, tid);
+      __syncthreads();
+    }
+  }
+  emit_group<G, kEmitScores>(em, es, acc, bh, tb0 + wave * kGB, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
+}
+
+template <int G>
+void launch_chan4_g(const Chan4Args &a, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
+  scan_chan4_kernel<G><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
+}
+
 // --------------------------------------------------------------------- launch
 template <int G, int MODE>
 void launch_g(const ScanArgs &a, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
@@ -620,4 +770,51 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
     if (rc) return rc;
   }
   return launch_finalize(rows, m, k, sink, local, em.sel, idx, st);
+}
+
+extern "C" int fathom_scan_chan4(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *act,
+                                 const int32_t *nact, const void *chan_sb, const void *scales_sb, int64_t n,
+                                 int64_t nsb, int64_t sub, int64_t blk0, int64_t blk1, float *out, void *stream) {
+  if (!q || !act || !nact || !chan_sb || !scales_sb || !out) return fail(FATHOM_ERR_INVALID, "scan_chan4: null pointer");
+  if (BH < 1 || BH > 65535) return fail(FATHOM_ERR_INVALID, "scan_chan4: BH=%lld outside [1, 65535]", (long long)BH);
+  if (G < 1 || G > 8) return fail(FATHOM_ERR_INVALID, "scan_chan4: G=%lld outside [1, 8]", (long long)G);
+  if (D < 1 || D > kMaxD) return fail(FATHOM_ERR_INVALID, "scan_chan4: D=%lld outside [1, %d]", (long long)D, kMaxD);
+  if (n < 1 || sub < 1 || nsb < 1 || nsb * sub < cdiv(n, kBlk))
+    return fail(FATHOM_ERR_INVALID, "scan_chan4: store of nsb=%lld x sub=%lld blocks does not cover n=%lld",
+                (long long)nsb, (long long)sub, (long long)n);
+  if ((reinterpret_cast<uintptr_t>(chan_sb) & 15) != 0)
+    return fail(FATHOM_ERR_INVALID, "scan_chan4: the nibble store must be 16-byte aligned");
+  if (blk0 < 0 || blk1 < blk0)
+    return fail(FATHOM_ERR_INVALID, "scan_chan4: bad block range [%lld, %lld)", (long long)blk0, (long long)blk1);
+  const int64_t nblk = cdiv(n, kBlk);
+  const int64_t blk_end = blk1 < nblk ? blk1 : nblk;
+  if (blk_end <= blk0) return FATHOM_OK;
+  Chan4Args a{};
+  a.q = q;
+  a.act = act;
+  a.nact = nact;
+  a.chan = static_cast<const uint4 *>(chan_sb);
+  a.scales = static_cast<const uint16_t *>(scales_sb);
+  a.n = n;
+  a.nsb = nsb;
+  a.sub = sub;
+  a.blk0 = blk0;
+  a.blk_end = blk_end;
+  a.tile0 = blk0 / kTB;
+  a.D = (int)D;
+  const int64_t tiles = cdiv(blk_end, kTB) - a.tile0;
+  Emit em{};
+  em.out = out;
+  hipStream_t st = (hipStream_t)stream;
+  switch (G) {
+    case 1: launch_chan4_g<1>(a, tiles, BH, em, st); break;
+    case 2: launch_chan4_g<2>(a, tiles, BH, em, st); break;
+    case 3: launch_chan4_g<3>(a, tiles, BH, em, st); break;
+    case 4: launch_chan4_g<4>(a, tiles, BH, em, st); break;
+    case 5: launch_chan4_g<5>(a, tiles, BH, em, st); break;
+    case 6: launch_chan4_g<6>(a, tiles, BH, em, st); break;
+    case 7: launch_chan4_g<7>(a, tiles, BH, em, st); break;
+    default: launch_chan4_g<8>(a, tiles, BH, em, st); break;
+  }
+  return launch_status("scan_chan4_kernel");
 }

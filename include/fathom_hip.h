@@ -113,6 +113,32 @@ int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const i
                        int64_t blk0, int64_t blk1, float *out, void *stream);
 
 /*
+ * The chan4 baseline store: channel-major 4-bit codes, word m of (channel j,
+ * block b) holding tokens 8m..8m+7 of the block, nibble k = token 8m + k.
+ *   pack_chan4 (kernels/bitplane.py:67-74): code [lead, n, D] uint8 ->
+ *     chan_sb [lead, nsb, D, sub, 8] uint32 (16-byte aligned), zero padded,
+ *     nsb = ceil(ceil(n / 64) / sub).
+ *   quantise_chan4 (Chan4Store.__init__, kernels/bitplane.py:342-347): keys ->
+ *     codes and block scales (optional outputs, as fathom_quantise_pack),
+ *     chan_sb and the fp16 superblock scales scales_sb [lead, nsb, D, sub].
+ *   channel_list (kernels/bitplane.py:128-132): active [BH, D] (bytes, 0 or 1)
+ *     -> act [BH, D] int32 (listed channels first, then the others, both
+ *     ascending) and nact [BH] int32.
+ *   scan_chan4 (Chan4Store.scan, kernels/bitplane.py:348-353, kernel :175-198):
+ *     scores [BH, G, n] over the first nact[bh] channels of act at full depth,
+ *     blocks [blk0, blk1) only.
+ */
+int fathom_pack_chan4(const uint8_t *code, int64_t lead, int64_t n, int64_t D, int64_t sub, uint32_t *chan_sb,
+                      void *stream);
+int fathom_quantise_chan4(const void *K, int k_dtype, int64_t lead, int64_t n, int64_t D, int scale_dtype,
+                          int64_t sub, uint8_t *code, void *scales_blk, uint32_t *chan_sb, uint16_t *scales_sb,
+                          void *stream);
+int fathom_channel_list(const uint8_t *active, int64_t BH, int64_t D, int32_t *act, int32_t *nact, void *stream);
+int fathom_scan_chan4(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *act, const int32_t *nact,
+                      const void *chan_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t blk0,
+                      int64_t blk1, float *out, void *stream);
+
+/*
  * Fused scan + sink/local top-k: the selection of fathom_scan_planes followed by
  * fathom_sink_local_topk on its scores (kernels/bitplane.py:319-338 then
  * :372-378, as chained by scripts/B_kernel_bench.py:74 and

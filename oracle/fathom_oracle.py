@@ -40,6 +40,13 @@ Parity status per function (how each is pinned; the tests hold the checks):
   The reference (torch.topk) leaves tie order unspecified: parity unpinned
   for ties, the build defines lowest index first.
 * gather_rows / gather_union: pure-Python loops; dedup changes traffic only.
+* pack_chan4: pure-Python nibble brute force, round trip through the words.
+* channel_list: a stable argsort of ~active (numpy, the reference's own formula).
+* scan_chan4: equals scan_planes with t = 4 on the listed channels and 0 elsewhere
+  (the chan4 store reads every listed channel at full depth); the worked
+  example's full-depth scores.
+* gather_attention: closed forms (weights fixed by construction, duplicates,
+  zero rows, recent-buffer rows), shift invariance, the one-hot limit.
 * gather_runs / copy_index_runs: pure-Python word loops; the copy-index run
   list equals, slot by slot, the reference's offp/lenp/offs/lens formulas
   (hand-computed example in the tests), and scanning the staged copy equals
@@ -181,6 +188,55 @@ def bytes_planes(t, n):
     t = np.asarray(t, np.float64)
     nb = -(-n // BLK)
     return float(((t.sum(-1) * 8 + (t > 0).sum(-1) * 2) * nb).sum())
+
+
+# ----------------------------------------------------------------------------- chan4 baseline store
+def pack_chan4(code, sub):
+    """codes uint8 [..., n, D] -> channel-major 4-bit store uint32 [..., nsb, D, sub, 8]
+    (kernels/bitplane.py:67-74): word m of (channel j, block b) holds the codes of
+    tokens 8m..8m+7 of the block, nibble k (bits 4k..4k+3) = token 8m + k; tokens
+    past n and blocks past nblk are code 0."""
+    code = np.asarray(code, np.uint8)
+    *lead, n, d = code.shape
+    nb = -(-n // BLK)
+    nsb = -(-nb // sub)
+    pad = nsb * sub * BLK - n
+    cb = np.concatenate([code, np.zeros((*lead, pad, d), np.uint8)], -2)
+    cb = cb.reshape(*lead, nsb, sub, 8, 8, d).astype(np.uint64)       # [.., nsb, sub, m, k, d]
+    shift = (4 * np.arange(8, dtype=np.uint64)).reshape(8, 1)
+    words = np.bitwise_or.reduce(cb << shift, axis=-2).astype(np.uint32)   # [.., nsb, sub, m, d]
+    nl = len(lead)
+    return np.ascontiguousarray(np.moveaxis(words, -1, nl + 1))       # [.., nsb, d, sub, m]
+
+
+def channel_list(active):
+    """active bool [BH, D] -> (act [BH, D] int32: listed channels first, ascending,
+    then the others, ascending; nact [BH]) (kernels/bitplane.py:128-132)."""
+    active = np.asarray(active, bool)
+    act = np.stack([np.concatenate([np.flatnonzero(r), np.flatnonzero(~r)]) for r in active]).astype(np.int32)
+    return act, active.sum(-1).astype(np.int32)
+
+
+def scan_chan4(q, code, scales, act, nact):
+    """Scores of the chan4 scan (kernels/bitplane.py:175-198, 348-353; reference
+    semantics scan_chan4_reference :365-370): sum over the first nact listed channels
+    of q_j * a_bj * (c - 7.5) / 8, i.e. the full-depth dequantised code.  float64,
+    [BH, G, n]."""
+    q = np.asarray(q, np.float64)
+    BH, G, D = q.shape
+    out = []
+    for b in range(BH):
+        mask = np.zeros(D)
+        mask[np.asarray(act[b][: int(nact[b])], np.int64)] = 1.0
+        val = dequant_planes(code[b], scales[b], 4).astype(np.float64) * mask[None]
+        out.append(q[b] @ val.T)
+    return np.stack(out)
+
+
+def bytes_chan4(nact, n):
+    """(32 + 2) bytes per listed channel and 64-token block (kernels/bitplane.py:79-80)."""
+    nb = -(-n // BLK)
+    return float(np.sum(np.asarray(nact, np.float64) * 34 * nb))
 
 
 # ----------------------------------------------------------------------------- log2

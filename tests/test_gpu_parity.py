@@ -626,3 +626,97 @@ def test_decode_layer_graph_replays_equal_eager():
         e_idx, e_out = layer()  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(e_idx, ref_idx) and torch.equal(e_out, ref_out)
+
+
+# ----------------------------------------------------------------------------- chan4 baseline store
+@pytest.mark.parametrize("n,sub", [(1000, 16), (4097, 3), (700, 11)])
+def test_chan4_store_bitexact(n, sub):
+    print(f"[chan4-store] n={n} sub={sub}", flush=True)
+    K = _keys(2, n, dtype=torch.bfloat16)
+    code_r, sc_r = O.quantise_u4(K.float().numpy())
+    old = bp.SUB
+    bp.SUB = sub
+    try:
+        st = bp.Chan4Store(K.to(DEV))
+        words = bp.pack_chan4(torch.from_numpy(code_r).to(DEV))
+    finally:
+        bp.SUB = old
+    torch.cuda.synchronize()
+    ref = O.pack_chan4(code_r, sub).view(np.int32)
+    np.testing.assert_array_equal(st.code.cpu().numpy(), code_r)
+    np.testing.assert_array_equal(st.chan_k.cpu().numpy(), ref)
+    np.testing.assert_array_equal(words.cpu().numpy(), ref)
+    _, sc_sb = O.to_superblocks(O.pack_planes(code_r), sc_r, sub)
+    np.testing.assert_array_equal(st.scales_k.cpu().float().numpy(), sc_sb.astype(np.float16).astype(np.float32))
+
+
+def test_channel_list_matches_oracle():
+    rng = np.random.default_rng(2)
+    active = rng.random((37, 128)) < 0.3
+    active[0] = False
+    active[1] = True
+    act, nact = bp.channel_list(torch.from_numpy(active).to(DEV))
+    ra, rn = O.channel_list(active)
+    np.testing.assert_array_equal(act.cpu().numpy(), ra)
+    np.testing.assert_array_equal(nact.cpu().numpy(), rn)
+
+
+def _full_depth_plan(act, nact, D=128):
+    """A plan dict whose only class is depth 4 over the listed channels (in list order)."""
+    BH = act.shape[0]
+    cls = torch.zeros(BH, 4, D, dtype=torch.int32, device=act.device)
+    cls[:, 3] = act
+    clsn = torch.zeros(BH, 4, dtype=torch.int32, device=act.device)
+    clsn[:, 3] = nact
+    return {"cls": cls, "clsn": clsn}
+
+
+@pytest.mark.parametrize("G,n,r", [(4, 5000, 32), (7, 3000, 16), (1, 700, 128), (3, 2100, 0)])
+def test_scan_chan4_matches_oracle_and_plane_scan(G, n, r):
+    """Chan4 scores against the float64 oracle, and bit-identical to the plane scan of a
+    plan with t = 4 on the same channels (same y = 2a(c - 7.5), weights q/16, order)."""
+    print(f"[scan-chan4] G={G} n={n} r={r}", flush=True)
+    BH = 3
+    K = _keys(BH, n, dtype=torch.bfloat16, edge=False)
+    q = torch.randn(BH, G, 128, generator=torch.Generator().manual_seed(G))
+    Kd, qd = K.to(DEV), q.to(DEV)
+    # SparQ-style lists: top-r channels of sum_g |q_g| (scripts/B_kernel_bench.py:54-56)
+    active = torch.zeros(BH, 128, dtype=torch.bool)
+    if r:
+        active.scatter_(1, q.abs().sum(1).topk(r, -1).indices, True)
+    act, nact = bp.channel_list(active.to(DEV))
+    cs = bp.Chan4Store(Kd)
+    got = cs.scan(qd, act, nact)
+    ps = bp.PlaneStore(Kd)
+    plane = ps.scan(qd, _full_depth_plan(act, nact))
+    torch.cuda.synchronize()
+    assert torch.equal(got, plane), "chan4 scan differs from the depth-4 plane scan"
+    code, sc = O.quantise_u4(K.float().numpy())
+    ref = O.scan_chan4(q.numpy(), code, sc, act.cpu().numpy(), nact.cpu().numpy())
+    _scores_close(got.cpu().numpy(), ref)
+    # a block sub-range leaves the rest of `out` untouched
+    out = torch.full_like(got, 7.0)
+    cs.scan(qd, act, nact, out=out, blocks=(3, 9))
+    torch.cuda.synchronize()
+    assert torch.equal(out[..., 3 * 64:min(9 * 64, n)], got[..., 3 * 64:min(9 * 64, n)])
+    assert (out[..., :3 * 64] == 7.0).all() and (out[..., 9 * 64:] == 7.0).all()
+
+
+def test_scan_chan4_host_resident():
+    K = _keys(2, 9000, dtype=torch.bfloat16, edge=False)
+    q = torch.randn(2, 4, 128).to(DEV)
+    cs = bp.Chan4Store(K.to(DEV), keep_code=False)
+    active = torch.zeros(2, 128, dtype=torch.bool, device=DEV)
+    active[:, :32] = True                                   # a contiguous 32-channel (Loki / DS) store
+    act, nact = bp.channel_list(active)
+    ref = cs.scan(q, act, nact)
+    _, ch_dev, h1 = off.host_mapped(cs.chan_k)
+    _, sc_dev, h2 = off.host_mapped(cs.scales_k)
+    try:
+        cs.chan_k, cs.scales_k = ch_dev, sc_dev
+        got = cs.scan(q, act, nact)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+    finally:
+        off.free_host(h1)
+        off.free_host(h2)

@@ -414,3 +414,49 @@ def test_gather_attention_shift_and_scale():
         for g in range(G):
             s = K[bb, idx[bb, g]] @ q[bb, g]
             np.testing.assert_allclose(c[bb, g], V[bb, idx[bb, g, int(np.argmax(s))]], rtol=1e-9, atol=1e-9)
+
+
+# ----------------------------------------------------------------------------- chan4 baseline store
+def test_pack_chan4_bruteforce():
+    rng = np.random.default_rng(8)
+    code = rng.integers(0, 16, size=(2, 150, 5)).astype(np.uint8)
+    sub = 2
+    w = O.pack_chan4(code, sub)
+    assert w.shape == (2, 2, 5, 2, 8) and w.dtype == np.uint32
+    for b in range(2):
+        for i in range(4 * 64):
+            blk, sb, bs = i // 64, (i // 64) // sub, (i // 64) % sub
+            m, k = (i % 64) // 8, i % 8
+            for j in range(5):
+                want = int(code[b, i, j]) if i < 150 else 0
+                assert (int(w[b, sb, j, bs, m]) >> (4 * k)) & 15 == want, (b, i, j)
+
+
+def test_channel_list_and_bytes():
+    active = np.array([[0, 1, 0, 1, 1, 0], [1, 1, 1, 1, 1, 1], [0, 0, 0, 0, 0, 0]], bool)
+    act, nact = O.channel_list(active)
+    np.testing.assert_array_equal(act, [[1, 3, 4, 0, 2, 5], [0, 1, 2, 3, 4, 5], [0, 1, 2, 3, 4, 5]])
+    np.testing.assert_array_equal(nact, [3, 6, 0])
+    assert O.bytes_chan4(nact, 130) == (3 + 6 + 0) * 34 * 3
+
+
+def test_scan_chan4_is_full_depth_scan():
+    """The chan4 score of a token is sum over listed channels of q_j * a * (c - 7.5) / 8:
+    checked by scalar loops, and equal to the plane scan with t = 4 on the listed
+    channels and t = 0 elsewhere."""
+    rng = np.random.default_rng(9)
+    BH, G, n, d = 2, 3, 130, 8
+    K = rng.standard_normal((BH, n, d)).astype(np.float32)
+    code, sc = O.quantise_u4(K)
+    q = rng.standard_normal((BH, G, d))
+    active = rng.random((BH, d)) < 0.5
+    act, nact = O.channel_list(active)
+    s = O.scan_chan4(q, code, sc, act, nact)
+    for b in range(BH):
+        for g in range(G):
+            for i in (0, 63, 64, 129):
+                want = sum(q[b, g, j] * float(sc[b, i // 64, j]) * (int(code[b, i, j]) - 7.5) / 8
+                           for j in range(d) if active[b, j])
+                assert abs(s[b, g, i] - want) <= 1e-12 * (1 + abs(want))
+    t = np.where(active, 4, 0)
+    np.testing.assert_allclose(s, O.scan_planes(q, code, sc, t), rtol=0, atol=1e-12)
