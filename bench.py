@@ -258,6 +258,59 @@ def run_decode_step(torch, bp, off, W, dev, steps, warmup):
             "scan_topk_GBps": scan_bytes / (ms["scan_topk"] * 1e-3) / 1e9}
 
 
+def _graph_ms(torch, fn, reps=20):
+    """GPU time of one fn() call: reps calls captured in one HIP graph, replayed
+    3 times after a warm-up, events around the replays."""
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        for _ in range(reps):
+            fn()
+    gph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        gph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (3 * reps)
+
+
+def run_kernel_table(torch, bp, W, dev):
+    """The reference's scan-kernel comparison (paper/tables/tab_kernel.tex:6-10, measured
+    by scripts/B_kernel_bench.py at n = 131072, batch 4 x 8 KV heads, G = 4): the
+    bit-plane scan at B = 48 and the chan4 nibble scans over 16 (SparQ r = 16), 32
+    and all 128 channels, each a single scan kernel, GB/s = algorithmic bytes / time."""
+    x = W.config_inputs(2, device=dev, BH=32)
+    q, n = x["q"], x["n"]
+    ps = bp.PlaneStore(x["K"], keep_code=False)
+    cs = bp.Chan4Store(x["K"], keep_code=False)
+    plan = bp.make_plan(x["g"], x["budget"])
+    out = torch.empty(32, x["G"], n, device=dev, dtype=torch.float32)
+    rows = {}
+    ms = _graph_ms(torch, lambda: ps.scan(q, plan, out=out))
+    by = bp.bytes_planes(plan["t"], n)
+    rows["planes_B48"] = {"ms": ms, "bytes": by, "GBps": by / (ms * 1e-3) / 1e9,
+                          "bits_per_token": by * 8 / (n * 32)}
+    abs_sum = q.abs().sum(1)
+    for r in (16, 32, 128):
+        active = torch.zeros(32, 128, dtype=torch.bool, device=dev)
+        active.scatter_(1, abs_sum.topk(r, -1).indices, True)
+        act, nact = bp.channel_list(active)
+        ms = _graph_ms(torch, lambda: cs.scan(q, act, nact, out=out))
+        by = bp.bytes_chan4(nact, n)
+        rows[f"chan4_r{r}"] = {"ms": ms, "bytes": by, "GBps": by / (ms * 1e-3) / 1e9}
+    del ps, cs, x
+    torch.cuda.empty_cache()
+    return {"shape": "n=131072, BH=32 (batch 4 x 8 KV heads), G=4, synthetic config-2 keys",
+            "timing": "HIP graph of 20 launches, 3 replays", "scans": rows,
+            "reference_A100": "paper/tables/tab_kernel.tex:6-10 at 128k: Fathom 48 0.415 ms (102 GB/s); "
+                              "16-ch / 32-ch / full 4-bit nibble scans 218 / 245 / 282 GB/s"}
+
+
 def cpu_baseline(x_cpu, reps=3):
     """The oracle's port of the reference CPU scorer (scripts/sketch.py:110-131 planes
     branch + exact top-k) on one KV head of the same distribution, 1 thread."""
@@ -391,6 +444,11 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] calibration copy: 3 x {a.calib_copy_mib} MiB read + written")
 
+    ktab = None
+    if not a.no_decode and not a.stages_only and a.n is None:
+        ktab = run_kernel_table(torch, bp, W, dev)
+        log(f"[bench] kernel table: {json.dumps(ktab)}")
+
     decode = None
     if not a.no_decode and not a.stages_only and a.n is None:
         del store
@@ -421,6 +479,7 @@ def main():
                      "algorithmic_bytes_per_launch": hbm["scan_bytes"]},
         "host_resident": host,
         "decode_step": decode,
+        "kernel_table": ktab,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
