@@ -31,6 +31,7 @@ PROTOTYPES = {
     "fathom_quantise_chan4": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _vp]),
     "fathom_channel_list": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "fathom_scan_chan4": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "fathom_klt_query": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "fathom_scan_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "fathom_scan_topk": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _vp, _vp, _sz, _vp]),

@@ -47,6 +47,11 @@ Parity status per function (how each is pinned; the tests hold the checks):
   example's full-depth scores.
 * gather_attention: closed forms (weights fixed by construction, duplicates,
   zero rows, recent-buffer rows), shift invariance, the one-hot limit.
+* klt_params: orthonormal basis, lam = variance of the rotated calibration keys,
+  score invariance q.(k - mu) = (q Vt).((k - mu) Vt), ordering by w.
+* klt_query: the invariance above; GPU gains against it within fp32 tolerance.
+* allocate: hand-worked example; brute-force optimum on convex equal-step tables
+  (where greedy marginal allocation is optimal).
 * gather_runs / copy_index_runs: pure-Python word loops; the copy-index run
   list equals, slot by slot, the reference's offp/lenp/offs/lens formulas
   (hand-computed example in the tests), and scanning the staged copy equals
@@ -237,6 +242,53 @@ def bytes_chan4(nact, n):
     """(32 + 2) bytes per listed channel and 64-token block (kernels/bitplane.py:79-80)."""
     nb = -(-n // BLK)
     return float(np.sum(np.asarray(nact, np.float64) * 34 * nb))
+
+
+# ----------------------------------------------------------------------------- KLT store, budget allocation
+def klt_params(Kcal, Qcal, sink=4):
+    """Per-row KLT basis (scripts/sketch.py:44-50): mu = mean of Kcal[:, sink*4:],
+    SVD of the centred keys, lam = S^2 / N, Vt = V (columns = components), ordered by
+    descending w = mean((Qcal @ Vt)^2) * lam.  float64.  Returns dict(mu, Vt, lam, w)."""
+    K = np.asarray(Kcal, np.float64)[:, sink * 4:]
+    Q = np.asarray(Qcal, np.float64)
+    out = {"mu": [], "Vt": [], "lam": [], "w": []}
+    for b in range(K.shape[0]):
+        mu = K[b].mean(0)
+        _, S, Vh = np.linalg.svd(K[b] - mu, full_matrices=False)
+        lam = S ** 2 / K.shape[1]
+        Vt = Vh.T
+        w = ((Q[b] @ Vt) ** 2).mean(0) * lam
+        order = np.argsort(-w, kind="stable")
+        out["mu"].append(mu)
+        out["Vt"].append(Vt[:, order])
+        out["lam"].append(lam[order])
+        out["w"].append(w[order])
+    return {k: np.stack(v) for k, v in out.items()}
+
+
+def klt_query(q, Vt, lam):
+    """qr = q @ Vt and plan gains sum_g qr^2 * lam (scripts/R_ruler.py:83), float64."""
+    qr = np.einsum("bgd,bde->bge", np.asarray(q, np.float64), np.asarray(Vt, np.float64))
+    return qr, ((qr ** 2) * np.asarray(lam, np.float64)[:, None, :]).sum(1)
+
+
+def allocate(err, budgets, mean_target):
+    """Greedy per-layer allocation (scripts/l4_final_alloc.py:143-154): from budgets[0]
+    everywhere, repeatedly move up the layer with the largest (e_i - e_{i+1}) /
+    (B_{i+1} - B_i) (first on ties) until the mean budget reaches mean_target or no
+    layer can move.  err: {budget: [error per layer]}.  Returns [budget per layer]."""
+    budgets = list(budgets)
+    nl = len(err[budgets[0]])
+    idx = [0] * nl
+    while sum(budgets[i] for i in idx) / nl < mean_target:
+        slopes = [((err[budgets[idx[L]]][L] - err[budgets[idx[L] + 1]][L]) / (budgets[idx[L] + 1] - budgets[idx[L]]), L)
+                  for L in range(nl) if idx[L] + 1 < len(budgets)]
+        slopes = [(d, L) for d, L in slopes if d > -1.0]
+        if not slopes:
+            break
+        best = max(d for d, _ in slopes)
+        idx[min(L for d, L in slopes if d == best)] += 1
+    return [budgets[i] for i in idx]
 
 
 # ----------------------------------------------------------------------------- log2

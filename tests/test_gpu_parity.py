@@ -720,3 +720,56 @@ def test_scan_chan4_host_resident():
     finally:
         off.free_host(h1)
         off.free_host(h2)
+
+
+# ----------------------------------------------------------------------------- KLT-rotated store
+def _klt_case(n=6000, BH=2, G=7, seed=0):
+    x = W.config_inputs(4, device="cpu", n=n, BH=BH, seed=seed)       # RoPE-rotated keys (config 4)
+    gen = torch.Generator().manual_seed(seed + 1)
+    Qcal = torch.randn(BH, 16 * G, 128, generator=gen)
+    return x, Qcal
+
+
+def test_klt_params_and_query_match_oracle():
+    from fathom_amd import klt
+    x, Qcal = _klt_case()
+    K = x["K"].float()
+    p = klt.klt_params(K.to(DEV), Qcal.to(DEV))
+    r = O.klt_params(K.numpy(), Qcal.numpy())
+    for b in range(K.shape[0]):
+        # same components up to sign (distinct eigenvalues on this data)
+        M = p["Vt"][b].cpu().double().numpy().T @ r["Vt"][b]
+        np.testing.assert_allclose(np.abs(M), np.eye(128), atol=2e-4)
+    np.testing.assert_allclose(p["lam"].cpu().numpy(), r["lam"], rtol=1e-5)
+    np.testing.assert_allclose(p["mu"].cpu().numpy(), r["mu"], rtol=1e-5, atol=1e-6)
+    q = x["q"]
+    qr, gain = klt.klt_query(q.to(DEV), p["Vt"], p["lam"])
+    rq, rg = O.klt_query(q.numpy(), p["Vt"].cpu().numpy(), p["lam"].cpu().numpy())
+    np.testing.assert_allclose(qr.cpu().numpy(), rq, rtol=1e-5, atol=1e-5 * np.abs(rq).max())
+    np.testing.assert_allclose(gain.cpu().numpy(), rg, rtol=1e-5, atol=1e-6 * np.abs(rg).max())
+
+
+@pytest.mark.parametrize("budget", [40.0, 48.0, 80.0])
+def test_klt_store_scan_and_topk(budget):
+    """The rotated store: codes of the rotated keys bit-exact, scores within tolerance of
+    the oracle scan over them with the rotated query, plan bit-exact from the kernel's
+    gains, fused top-k equal to the unfused one."""
+    print(f"[klt] budget={budget}", flush=True)
+    from fathom_amd import klt
+    x, Qcal = _klt_case()
+    Kd = x["K"].to(DEV)
+    p = klt.klt_params(Kd, Qcal.to(DEV))
+    st = klt.KLTPlaneStore(Kd, p)
+    Kr = torch.matmul(Kd.float() - p["mu"][:, None, :], p["Vt"]).cpu()    # the store's own rotation
+    code_r, sc_r = O.quantise_u4(Kr.numpy())
+    np.testing.assert_array_equal(st.code.cpu().numpy(), code_r)
+    q = x["q"].to(DEV)
+    qr, gain = st.query(q)
+    plan = st.plan(q, budget)
+    rp = O.make_plan(gain.cpu().numpy(), budget)
+    np.testing.assert_array_equal(plan["t"].cpu().numpy(), rp["t"])
+    s = st.scan(q, plan)
+    ref = O.scan_planes(qr.cpu().numpy(), code_r, sc_r, rp["t"])
+    _scores_close(s.cpu().numpy(), ref)
+    idx = st.scan_topk(q, plan, 2048, 4, 32)
+    torch.testing.assert_close(idx, bp.sink_local_topk(s, 2048, 4, 32), rtol=0, atol=0)

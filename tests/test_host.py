@@ -1,0 +1,40 @@
+"""Host-side logic of the package (no GPU): per-layer budget allocation and the
+lazy safetensors reader."""
+import numpy as np
+import pytest
+import torch
+
+from fathom_amd import capsio
+from fathom_amd.klt import allocate
+from oracle import fathom_oracle as O
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_allocate_matches_oracle(seed):
+    rng = np.random.default_rng(seed)
+    budgets = (24, 32, 40, 48, 64, 80, 96, 128)            # scripts/l4_final_alloc.py:18
+    nl = 36
+    err = {B: list(rng.random(nl) / (1 + i) ** rng.uniform(0.5, 2)) for i, B in enumerate(budgets)}
+    for target in (32, 40, 48, 64, 80):
+        got = allocate({B: dict(enumerate(v)) for B, v in err.items()}, budgets, target)
+        assert [got[L] for L in range(nl)] == O.allocate(err, budgets, target)
+        assert sum(got.values()) / nl >= target or all(b == budgets[-1] for b in got.values())
+
+
+def test_capsio_reads_slices(tmp_path):
+    from safetensors.torch import save_file
+    g = torch.Generator().manual_seed(0)
+    t = {"k0": torch.randn(8, 300, 128, generator=g).to(torch.bfloat16),
+         "q0": torch.randn(32, 300, 128, generator=g).to(torch.float16),
+         "v3": torch.randn(5, 7, generator=g), "ids": torch.arange(11, dtype=torch.int64)}
+    path = str(tmp_path / "caps_test.safetensors")
+    save_file(t, path, metadata={"model": "synthetic"})
+    f = capsio.safe_open(path, "pt")
+    assert sorted(f.keys()) == sorted(t) and "k0" in f and len(f) == 4
+    assert f.get_slice("q0").get_shape() == [32, 300, 128]
+    assert torch.equal(f.get_slice("k0")[2], t["k0"][2])
+    assert torch.equal(f.get_slice("q0")[4:12, 290:], t["q0"][4:12, 290:])
+    assert torch.equal(f.get_slice("k0")[-1], t["k0"][-1])
+    assert torch.equal(f["v3"], t["v3"]) and torch.equal(f.get_tensor("ids"), t["ids"])
+    assert f.get_slice("k0")[3:3].shape == (0, 300, 128)
+    f.close()

@@ -460,3 +460,58 @@ def test_scan_chan4_is_full_depth_scan():
                 assert abs(s[b, g, i] - want) <= 1e-12 * (1 + abs(want))
     t = np.where(active, 4, 0)
     np.testing.assert_allclose(s, O.scan_planes(q, code, sc, t), rtol=0, atol=1e-12)
+
+
+# ----------------------------------------------------------------------------- KLT store, budget allocation
+def test_klt_basis_identities():
+    """Orthonormal components; lam is the variance of the rotated calibration keys
+    (v' C v = lam); scores are invariant under the rotation; components ordered by w."""
+    rng = np.random.default_rng(12)
+    BH, n, d, m = 2, 400, 16, 24
+    A = rng.standard_normal((BH, d, d))
+    K = rng.standard_normal((BH, n, d)) @ A + rng.standard_normal((BH, 1, d)) * 3
+    Q = rng.standard_normal((BH, m, d))
+    p = O.klt_params(K, Q)
+    for b in range(BH):
+        V = p["Vt"][b]
+        np.testing.assert_allclose(V.T @ V, np.eye(d), atol=1e-10)
+        Kc = K[b, 16:] - p["mu"][b]
+        np.testing.assert_allclose((Kc @ V).var(0), p["lam"][b], rtol=1e-9, atol=1e-12)
+        np.testing.assert_allclose(p["w"][b], ((Q[b] @ V) ** 2).mean(0) * p["lam"][b], rtol=1e-12)
+        assert (np.diff(p["w"][b]) <= 0).all()
+        q = rng.standard_normal((3, d))
+        np.testing.assert_allclose((q @ V) @ (Kc @ V).T, q @ Kc.T, rtol=1e-9, atol=1e-9)
+    qr, g = O.klt_query(Q[:, :4], p["Vt"], p["lam"])
+    np.testing.assert_allclose(g, (qr ** 2 * p["lam"][:, None]).sum(1))
+
+
+def test_allocate_worked_example():
+    """Three layers, budgets 24/32/48: slopes per bit at each step decide by hand.
+    Step 1: slopes (24->32) = 0.8/8, 0.4/8, 1.6/8 -> layer 2 to 32 (mean 26.67).
+    Step 2: layer 2 (32->48) 0.8/16 = 0.05; layer 0 0.1; layer 1 0.05 -> layer 0 (mean 29.33).
+    Step 3: layer 0 (32->48) 0.32/16 = 0.02; layer 1 0.05; layer 2 0.05 -> layer 1 (first of
+    the tie) to 32 (mean 32) -> stop at target 32."""
+    err = {24: [1.0, 0.9, 2.0], 32: [0.2, 0.5, 0.4], 48: [-0.12, 0.0, -0.4]}
+    assert O.allocate(err, (24, 32, 48), 32) == [32, 32, 32]
+    assert O.allocate(err, (24, 32, 48), 26) == [24, 24, 32]
+    assert O.allocate(err, (24, 32, 48), 100) == [48, 48, 48]        # every layer at the top budget
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_allocate_greedy_optimal_on_convex_equal_steps(seed):
+    """Equal budget steps and convex decreasing errors: greedy marginal allocation
+    reaches the minimum total error among all allocations of the same total budget."""
+    import itertools
+    rng = np.random.default_rng(seed)
+    budgets = (16, 24, 32, 40, 48)
+    nl = 4
+    drops = np.sort(rng.random((nl, len(budgets) - 1)), axis=1)[:, ::-1]   # decreasing drops -> convex
+    base = rng.random(nl) + 5
+    errs = np.concatenate([base[:, None], base[:, None] - np.cumsum(drops, 1)], 1)
+    err = {B: list(errs[:, i]) for i, B in enumerate(budgets)}
+    for target in (20, 28, 36):
+        got = O.allocate(err, budgets, target)
+        total = sum(got)
+        best = min(sum(errs[L, budgets.index(B)] for L, B in enumerate(c))
+                   for c in itertools.product(budgets, repeat=nl) if sum(c) == total)
+        assert abs(sum(errs[L, budgets.index(B)] for L, B in enumerate(got)) - best) < 1e-12
