@@ -311,6 +311,39 @@ def run_kernel_table(torch, bp, W, dev):
                               "16-ch / 32-ch / full 4-bit nibble scans 218 / 245 / 282 GB/s"}
 
 
+def run_config4(torch, bp, W, dev):
+    """Config 4 (Qwen2.5-7B layer: batch 2 x 4 KV heads, G = 7, n = 131072, RoPE keys
+    with 8 outlier channels, k = 2048): plan + fused scan/top-k at budgets B = 40,
+    48, 80 code bits (47 / 56 / 92 bits per token with scales) over the raw-channel
+    store and the KLT-rotated store (calibrated on the layer's first 16384 keys and
+    16 synthetic queries per head), each stage timed as a HIP graph."""
+    from fathom_amd import klt
+    x = W.config_inputs(4, device=dev)
+    q, n, k = x["q"], x["n"], x["k"]
+    gen = torch.Generator(device=dev).manual_seed(44)
+    Qcal = torch.randn(x["BH"], 16 * x["G"], 128, generator=gen, device=dev)
+    p = klt.klt_params(x["K"][:, :16384], Qcal)
+    stores = {"raw": bp.PlaneStore(x["K"], keep_code=False), "klt": klt.KLTPlaneStore(x["K"], p, keep_code=False)}
+    res = {}
+    for name, st in stores.items():
+        for B in x["budgets"]:
+            if name == "raw":
+                plan_fn = lambda: bp.make_plan(x["g"], B)
+            else:
+                plan_fn = lambda: st.plan(q, B)
+            plan = plan_fn()
+            ms_plan = _graph_ms(torch, plan_fn, reps=10)
+            ms_st = _graph_ms(torch, lambda: st.scan_topk(q, plan, k, x["sink"], x["local"]), reps=10)
+            by = bp.bytes_planes(plan["t"], n)
+            res[f"{name}_B{int(B)}"] = {"plan_ms": ms_plan, "scan_topk_ms": ms_st,
+                                        "bits_per_token": by * 8 / (n * x["BH"]),
+                                        "scanned_tokens_per_s": n * x["BH"] / (ms_st * 1e-3)}
+    del stores, x
+    torch.cuda.empty_cache()
+    return {"workload": W.CONFIGS[4]["name"], "k": 2048, "timing": "HIP graph of 10 launches, 3 replays",
+            "runs": res}
+
+
 def cpu_baseline(x_cpu, reps=3):
     """The oracle's port of the reference CPU scorer (scripts/sketch.py:110-131 planes
     branch + exact top-k) on one KV head of the same distribution, 1 thread."""
@@ -449,6 +482,11 @@ def main():
         ktab = run_kernel_table(torch, bp, W, dev)
         log(f"[bench] kernel table: {json.dumps(ktab)}")
 
+    cfg4 = None
+    if not a.no_decode and not a.stages_only and a.n is None:
+        cfg4 = run_config4(torch, bp, W, dev)
+        log(f"[bench] config 4: {json.dumps(cfg4)}")
+
     decode = None
     if not a.no_decode and not a.stages_only and a.n is None:
         del store
@@ -480,6 +518,7 @@ def main():
         "host_resident": host,
         "decode_step": decode,
         "kernel_table": ktab,
+        "config4": cfg4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -3,10 +3,10 @@
 // so each decode step rotates the query the same way, qr = q @ Vt, and plans
 // from the gains g_e = sum_g qr_ge^2 * lam_e of the rotated coordinates.
 //
-// One workgroup per (batch, KV head) row: the G query heads are staged in LDS;
-// thread e owns output coordinate e and walks Vt's column e (row-major Vt, so
-// the threads of a wave read consecutive floats of each row d) with one fp32
-// FMA per (head, d) in ascending d, then forms the gain in head order.
+// A workgroup owns 16 output coordinates of one (batch, KV head) row, with the
+// G query heads staged in LDS: thread (c, p) sums q_g[d] * Vt[d, e0 + c] over
+// the p-th of 16 d ranges (fp32 FMAs, ascending d, every load in flight at
+// once), and the range sums are added in order; the gain follows in head order.
 #include "common.hpp"
 
 namespace fathom {
@@ -15,36 +15,51 @@ namespace {
 constexpr int kKltThreads = 256;
 constexpr int kKltMaxG = 8;
 constexpr int kKltMaxD = 256;
+constexpr int kKltCols = 16;                     // output coordinates per workgroup
+constexpr int kKltParts = kKltThreads / kKltCols;  // d ranges per coordinate
 
 __global__ __launch_bounds__(kKltThreads) void klt_query_kernel(const float *__restrict__ q,
                                                                  const float *__restrict__ Vt,
                                                                  const float *__restrict__ lam, int G, int D,
                                                                  float *__restrict__ qr, float *__restrict__ gain) {
   __shared__ float qs[kKltMaxG][kKltMaxD];
-  const int64_t bh = blockIdx.x;
-  for (int e = threadIdx.x; e < G * D; e += kKltThreads) qs[e / D][e % D] = q[bh * G * D + e];
+  __shared__ float part[kKltParts][kKltMaxG][kKltCols];
+  const int tid = threadIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int e0 = blockIdx.x * kKltCols;
+  for (int e = tid; e < G * D; e += kKltThreads) qs[e / D][e % D] = q[bh * G * D + e];
   __syncthreads();
   const float *V = Vt + bh * (int64_t)D * D;
-  for (int e = threadIdx.x; e < D; e += kKltThreads) {
-    float acc[kKltMaxG];
+  const int c = tid % kKltCols, pt = tid / kKltCols, e = e0 + c;
+  const int per = (D + kKltParts - 1) / kKltParts;
+  float acc[kKltMaxG];
 #pragma unroll
-    for (int g = 0; g < kKltMaxG; ++g) acc[g] = 0.0f;
-    for (int d = 0; d < D; ++d) {
-      const float v = V[(int64_t)d * D + e];
+  for (int g = 0; g < kKltMaxG; ++g) acc[g] = 0.0f;
+  if (e < D) {
+    for (int i = 0; i < per; ++i) {
+      const int d = pt * per + i;
+      if (d < D) {
+        const float v = V[(int64_t)d * D + e];
 #pragma unroll
-      for (int g = 0; g < kKltMaxG; ++g)
-        if (g < G) acc[g] = fmaf(qs[g][d], v, acc[g]);
-    }
-    const float l = lam[bh * D + e];
-    float s = 0.0f;
-#pragma unroll
-    for (int g = 0; g < kKltMaxG; ++g) {
-      if (g < G) {
-        qr[(bh * G + g) * D + e] = acc[g];
-        s += (acc[g] * acc[g]) * l;  // ((qr ** 2) * lam).sum over heads, in head order
+        for (int g = 0; g < kKltMaxG; ++g)
+          if (g < G) acc[g] = fmaf(qs[g][d], v, acc[g]);
       }
     }
-    gain[bh * D + e] = s;
+  }
+#pragma unroll
+  for (int g = 0; g < kKltMaxG; ++g) part[pt][g][c] = acc[g];
+  __syncthreads();
+  if (tid < kKltCols && e0 + tid < D) {
+    const int eo = e0 + tid;
+    const float l = lam[bh * D + eo];
+    float s = 0.0f;
+    for (int g = 0; g < G; ++g) {
+      float r = 0.0f;
+      for (int p = 0; p < kKltParts; ++p) r += part[p][g][tid];  // the d ranges in order
+      qr[(bh * G + g) * D + eo] = r;
+      s += (r * r) * l;  // ((qr ** 2) * lam).sum over heads, in head order
+    }
+    gain[bh * D + eo] = s;
   }
 }
 
@@ -59,6 +74,8 @@ extern "C" int fathom_klt_query(const float *q, const float *Vt, const float *la
   if (BH < 1 || BH > 0x7FFFFFFF) return fail(FATHOM_ERR_INVALID, "klt_query: BH=%lld", (long long)BH);
   if (G < 1 || G > kKltMaxG) return fail(FATHOM_ERR_INVALID, "klt_query: G=%lld outside [1, %d]", (long long)G, kKltMaxG);
   if (D < 1 || D > kKltMaxD) return fail(FATHOM_ERR_INVALID, "klt_query: D=%lld outside [1, %d]", (long long)D, kKltMaxD);
-  klt_query_kernel<<<(unsigned)BH, kKltThreads, 0, (hipStream_t)stream>>>(q, Vt, lam, (int)G, (int)D, qr, gain);
+  const dim3 grid((unsigned)cdiv(D, kKltCols), (unsigned)BH);
+  if (BH > 65535) return fail(FATHOM_ERR_INVALID, "klt_query: BH=%lld above 65535", (long long)BH);
+  klt_query_kernel<<<grid, kKltThreads, 0, (hipStream_t)stream>>>(q, Vt, lam, (int)G, (int)D, qr, gain);
   return launch_status("klt_query_kernel");
 }

@@ -59,44 +59,46 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
   return v;
 }
 
-// Number of values > x in a run of 64 sorted descending (binary search).
-__device__ __forceinline__ int count_greater64(const uint64_t *run, uint64_t x) {
-  int lo = 0, hi = 64;
-#pragma unroll
-  for (int it = 0; it < 7; ++it) {
-    if (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (run[mid] > x) lo = mid + 1; else hi = mid;
-    }
-  }
-  return lo;
-}
-
-// Ranks (0 = largest) of up to E * 1024 distinct nonzero values: thread t holds
-// elements t + 1024 e (zero = padding).  Each wave sorts its 64-value runs in
-// registers; a value's rank is its position in its own run plus the number of
-// larger values in every other run.  runs: LDS scratch of E * 1024 values.
-// Returns the sorted value held at the same slot and its rank.
+// Descending sort of E * 1024 values, thread t holding slots t + 1024 e (the
+// whole workgroup calls it): each wave sorts its 64-value runs in registers,
+// then log2(E * 1024 / 64) merge levels double the sorted runs in LDS.  At a
+// level an element's new place is its index in its own run plus the number of
+// elements of the partner run ahead of it (found by a binary search in the
+// partner run: strictly greater values for the left run, greater or equal for
+// the right one, so equal values keep run order and every place is distinct).
+// Only the first nlim slots (a power of two, 64 <= nlim <= E * 1024) are
+// merged: callers put every value that matters there.  a and b: LDS buffers of
+// E * 1024 values; returns the one holding the sorted first nlim slots.
 template <int E>
-__device__ void run_ranks(uint64_t (&v)[E], int (&rank)[E], uint64_t *runs, int nvals) {
+__device__ uint64_t *block_sort_desc(uint64_t (&v)[E], uint64_t *a, uint64_t *b, int nlim) {
   const int t = threadIdx.x, lane = t & 63;
-  const int nruns = (nvals + 63) >> 6;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    v[e] = wave_sort_desc(v[e], lane);
-    runs[t + 1024 * e] = v[e];
-  }
+  for (int e = 0; e < E; ++e) a[t + 1024 * e] = wave_sort_desc(v[e], lane);
   __syncthreads();
+  for (int w = kWave; w < nlim; w <<= 1) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int own = (t + 1024 * e) >> 6;
-    int r = lane;
-    if (v[e] != 0ull) {
-      for (int q = 0; q < nruns; ++q)
-        if (q != own) r += count_greater64(runs + 64 * q, v[e]);
+    for (int e = 0; e < E; ++e) {
+      const int i = t + 1024 * e;
+      if (i >= nlim) continue;
+      const uint64_t x = a[i];
+      const int r = i / w, p = i - r * w;
+      const bool left = (r & 1) == 0;
+      const uint64_t *part = a + (r ^ 1) * w;
+      int c = 0;  // elements of the partner run placed ahead of x (a prefix of it)
+      for (int step = w; step > 0; step >>= 1) {
+        if (c + step <= w) {
+          const uint64_t y = part[c + step - 1];
+          if (left ? (y > x) : (y >= x)) c += step;
+        }
+      }
+      b[(r >> 1) * 2 * w + p + c] = x;
     }
-    rank[e] = v[e] != 0ull ? r : 0x7FFFFFFF;
+    __syncthreads();
+    uint64_t *tmp = a;
+    a = b;
+    b = tmp;
   }
+  return a;
 }
 
 // Smallest value >= lo of the need-th largest element among cnt values read
@@ -205,7 +207,7 @@ __device__ __forceinline__ uint32_t masked_key(const float *row, int64_t i, int6
 // T_hi is the r_hi-th largest of the same values (r_hi <= kk, so T_hi >= T_lo).
 template <int M>
 __device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t r_hi, uint64_t *vals,
-                             uint32_t *s_thr, uint32_t &t_lo, uint32_t &t_hi) {
+                             RangeShared &sh, uint32_t &t_lo, uint32_t &t_hi) {
   uint32_t top[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) top[i] = 0u;
@@ -219,28 +221,32 @@ __device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t
       top[i] = hi;
     }
   }
-  // ranks of the M * 1024 candidates (key << 32 | slot: distinct, nonzero);
-  // the keys of ranks kk - 1 and r_hi - 1 are the thresholds
+  // the M * 1024 candidates as distinct nonzero values key << 32 | slot; the
+  // keys of the kk-th and r_hi-th largest are the thresholds
   uint64_t w[M];
-  int rk[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) w[i] = ((uint64_t)top[i] << 32) | (uint32_t)(threadIdx.x + 1024 * i + 1);
-  run_ranks<M>(w, rk, vals, M * kSelThreads);
+  if constexpr (M > 1) {  // 2048+ values: histogram range selection
 #pragma unroll
-  for (int i = 0; i < M; ++i) {
-    if (rk[i] == (int)kk - 1) s_thr[0] = (uint32_t)(w[i] >> 32);
-    if (rk[i] == (int)r_hi - 1) s_thr[1] = (uint32_t)(w[i] >> 32);
+    for (int i = 0; i < M; ++i) vals[threadIdx.x + kSelThreads * i] = w[i];
+    __syncthreads();
+    auto get = [&](int64_t i) { return vals[i]; };
+    const uint64_t lo = range_select(get, (int64_t)M * kSelThreads, kk, sh);
+    const uint64_t hi = r_hi < kk ? range_select(get, (int64_t)M * kSelThreads, r_hi, sh) : lo;
+    t_lo = (uint32_t)(lo >> 32);
+    t_hi = (uint32_t)(hi >> 32);
+  } else {  // 1024 values: sort them and read the two ranks
+    const uint64_t *srt = block_sort_desc<M>(w, vals, vals + M * kSelThreads, M * kSelThreads);
+    t_lo = (uint32_t)(srt[kk - 1] >> 32);
+    t_hi = r_hi < kk ? (uint32_t)(srt[r_hi - 1] >> 32) : t_lo;
   }
-  __syncthreads();
-  t_lo = s_thr[0];
-  t_hi = r_hi < kk ? s_thr[1] : t_lo;
 }
 
 __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t *__restrict__ samp,
                                                                   int64_t samp_cap, uint32_t kk, uint32_t r_hi,
                                                                   TopkSel s) {
   __shared__ uint64_t vals[4 * kSelThreads];
-  __shared__ uint32_t s_thr[2];
+  __shared__ RangeShared sh;
   const int64_t row = blockIdx.x;
   const uint32_t *src = samp + row * samp_cap;
   uint32_t v[kSelPer];
@@ -252,11 +258,11 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
   uint32_t t_lo = 0u, t_hi = 0u;  // fewer samples than kk: every element is a candidate
   if (samp_cap >= (int64_t)kk) {
     if (2 * kk <= kSelThreads)
-      sample_bound<1>(v, kk, r_hi, vals, s_thr, t_lo, t_hi);
+      sample_bound<1>(v, kk, r_hi, vals, sh, t_lo, t_hi);
     else if (kk <= kSelThreads)
-      sample_bound<2>(v, kk, r_hi, vals, s_thr, t_lo, t_hi);
+      sample_bound<2>(v, kk, r_hi, vals, sh, t_lo, t_hi);
     else
-      sample_bound<4>(v, kk, r_hi, vals, s_thr, t_lo, t_hi);
+      sample_bound<4>(v, kk, r_hi, vals, sh, t_lo, t_hi);
   }
   if (threadIdx.x == 0) {
     s.thr[row] = t_hi;
@@ -358,7 +364,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   }
   if (tid == 0) s_cnt = 0u;
   __syncthreads();
-  // the exact kk largest first (range selection), then their ranks
+  // the exact kk largest first (range selection), then sorted
   const uint64_t thr = in_lds ? range_select([&](int64_t i) { return cl[i]; }, cnt, (uint32_t)kk, sh)
                               : range_select([&](int64_t i) { return gc[i]; }, cnt, (uint32_t)kk, sh);
   for (int64_t i = tid; i < cnt; i += kFinThreads) {
@@ -373,13 +379,16 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   uint64_t v2[2];  // zero: padding (below every K64)
   v2[0] = tid < nv ? ss[tid] : 0ull;
   v2[1] = tid + kFinThreads < nv ? ss[tid + kFinThreads] : 0ull;
-  __syncthreads();  // cl is the rank scratch from here
-  int rk[2];
-  run_ranks<2>(v2, rk, cl, nv);
+  __syncthreads();  // cl is the sort scratch from here
+  int nlim = kWave;
+  while (nlim < nv) nlim <<= 1;  // the survivors fill the first nv <= 2048 slots
+  const uint64_t *srt = block_sort_desc<2>(v2, cl, cl + 2 * kFinThreads, nlim);
   const int got = nv < (int)kk ? nv : (int)kk;
 #pragma unroll
-  for (int e = 0; e < 2; ++e)
-    if (rk[e] < got) out[rk[e]] = (int64_t)(0xFFFFFFFFu - (uint32_t)v2[e]);
+  for (int e = 0; e < 2; ++e) {
+    const int i = tid + e * kFinThreads;
+    if (i < got) out[i] = (int64_t)(0xFFFFFFFFu - (uint32_t)srt[i]);
+  }
   for (int i = got + tid; i < (int)kk; i += kFinThreads) out[i] = 0;
   for (int i = tid; i < (int)(sink + local); i += kFinThreads)
     out[kk + i] = (i < sink) ? (int64_t)i : (int64_t)(m - local + (i - sink));
