@@ -46,6 +46,7 @@ PROTOTYPES = {
                                        ctypes.c_float, _vp, _vp, _vp, _sz, _vp]),
     "fathom_gather_runs": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fathom_copy_index": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "fathom_copy_index_range": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
     "fathom_host_alloc_mapped": (_i32, [_sz, _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
     "fathom_host_free": (_i32, [_vp]),
     "fathom_memcpy": (_i32, [_vp, _vp, _sz, _vp]),

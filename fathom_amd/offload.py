@@ -10,6 +10,9 @@
   recent tokens (index >= n) come from a device buffer.
 * select_and_gather: plan -> scan -> sink/local top-k -> union gather, the
   selection half of offload_attn (scripts/B_e2e_offload_v2.py:163-242).
+* chunk_bounds / stream_planes / stream_chan4: the chunked two-stream pipeline
+  (scripts/B_e2e_offload_v2.py:103-144): chunk c + 1's runs cross PCIe on a copy
+  stream while chunk c is scanned on a scan stream.
 * gather_runs / host_store / copy_index: the copy-index path
   (scripts/B_e2e_offload_v2.py:62-71, 190-197, 267): a store in the
   whole-sequence layout (SUB = nblk) in mapped host memory, whose plan-selected
@@ -71,40 +74,50 @@ def gather_runs(src, dst, off, ln, nrun, max_len, CH=4096):
 
 
 def host_store(store):
-    """A copy of a whole-sequence-layout PlaneStore (built with bitplane.SUB = nblk)
-    whose planes and scales live in mapped pinned host memory: the returned store's
-    planes32 / scales_k are DevPtr objects, as the reference's offload does
-    (scripts/B_e2e_offload_v2.py:267, 296-309).  Returns (store, host pointers to
-    free with free_host)."""
+    """A copy of a whole-sequence-layout PlaneStore or Chan4Store (built with
+    bitplane.SUB = nblk) whose store words and scales live in mapped pinned host
+    memory: the returned store's planes32 (chan_k) / scales_k are DevPtr objects, as
+    the reference's offload does (scripts/B_e2e_offload_v2.py:267, 296-309).
+    Returns (store, host pointers to free with free_host)."""
+    from .bitplane import Chan4Store, PlaneStore
     if store.nsb != 1:
         raise ValueError("copy-index stores use the whole-sequence layout: build them with bitplane.SUB = nblk")
-    from .bitplane import PlaneStore
-    _, pl, h1 = host_mapped(store.planes_k)
+    c4 = isinstance(store, Chan4Store)
+    _, pl, h1 = host_mapped(store.chan_k if c4 else store.planes_k)
     try:
         _, sc, h2 = host_mapped(store.scales_k)
     except Exception:
         free_host(h1)
         raise
-    hs = PlaneStore.__new__(PlaneStore)
+    hs = (Chan4Store if c4 else PlaneStore).__new__(Chan4Store if c4 else PlaneStore)
     hs.BH, hs.n, hs.nsb, hs.sub = store.BH, store.n, store.nsb, store.sub
     hs.code, hs.scales_blk = None, None
-    hs.planes32, hs.scales_k = pl, sc
+    if c4:
+        hs.chan_k = pl
+    else:
+        hs.planes32 = pl
+    hs.scales_k = sc
     return hs, (h1, h2)
 
 
 def staging_store(store, device=None):
-    """An HBM PlaneStore with store's shape and whole-sequence layout, planes and
-    scales zeroed: the target of copy_index."""
+    """An HBM store (PlaneStore or Chan4Store, as `store`) with store's shape and
+    whole-sequence layout, words and scales zeroed: the target of copy_index and of
+    the chunked pipeline."""
+    from .bitplane import Chan4Store, PlaneStore
     if store.nsb != 1:
         raise ValueError("copy-index stores use the whole-sequence layout: build them with bitplane.SUB = nblk")
-    from .bitplane import PlaneStore
     dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
-    st = PlaneStore.__new__(PlaneStore)
+    c4 = isinstance(store, Chan4Store)
+    st = (Chan4Store if c4 else PlaneStore).__new__(Chan4Store if c4 else PlaneStore)
     st.BH, st.n, st.nsb, st.sub = store.BH, store.n, 1, store.sub
     st.code, st.scales_blk = None, None
-    st.planes_k = torch.zeros(store.BH, 1, D, 4, store.sub, dtype=torch.int64, device=dev)
+    if c4:
+        st.chan_k = torch.zeros(store.BH, 1, D, store.sub, 8, dtype=torch.int32, device=dev)
+    else:
+        st.planes_k = torch.zeros(store.BH, 1, D, 4, store.sub, dtype=torch.int64, device=dev)
+        st.planes32 = st.planes_k.view(torch.int32)
     st.scales_k = torch.zeros(store.BH, 1, D, store.sub, dtype=torch.float16, device=dev)
-    st.planes32 = st.planes_k.view(torch.int32)
     return st
 
 
@@ -123,6 +136,85 @@ def copy_index(src, staging, plan):
     _lib.call("fathom_copy_index", _ptr(tt), BH, d, int(staging.sub), ctypes.c_void_p(src.planes32.data_ptr()),
               ctypes.c_void_p(src.scales_k.data_ptr()), ctypes.c_void_p(staging.planes32.data_ptr()),
               ctypes.c_void_p(staging.scales_k.data_ptr()), _stream(tt.device))
+
+
+def chunk_bounds(nblk, parts, align=64):
+    """Block ranges [(b0, b1)] splitting nblk blocks into `parts` chunks whose interior
+    boundaries are multiples of align (scripts/B_e2e_offload_v2.py:105-108)."""
+    cuts = {0, nblk} | {min(nblk, (nblk * i // parts) // align * align) for i in range(1, parts)}
+    edges = sorted(cuts)
+    return list(zip(edges[:-1], edges[1:]))
+
+
+_PIPE_STREAMS = {}
+
+
+def _pipe_streams(dev):
+    """The copy and scan streams of the pipeline on device dev (default priority)."""
+    key = torch.device(dev).index
+    if key not in _PIPE_STREAMS:
+        _PIPE_STREAMS[key] = (torch.cuda.Stream(dev), torch.cuda.Stream(dev))
+    return _PIPE_STREAMS[key]
+
+
+def _stream_chunks(src, staging, t8, planes, block_bytes, data_attr, scan_chunk, n_out, q, parts):
+    """Shared body of stream_planes / stream_chan4: per chunk of blocks, its runs are
+    copied on the copy stream and the chunk is scanned on the scan stream after the
+    copy's event, so chunk c + 1 crosses PCIe while chunk c is scanned."""
+    dev = q.device
+    BH, d = t8.shape
+    nblk = int(staging.sub)
+    s_copy, s_scan = _pipe_streams(dev)
+    cur = torch.cuda.current_stream(dev)
+    scores = torch.empty(BH, q.shape[1], n_out, device=dev, dtype=torch.float32)
+    ev0 = torch.cuda.Event()
+    ev0.record(cur)
+    s_copy.wait_event(ev0)
+    s_scan.wait_event(ev0)
+    t8.record_stream(s_copy)
+    scores.record_stream(s_scan)
+    for b0, b1 in chunk_bounds(nblk, parts):
+        with torch.cuda.stream(s_copy):
+            _lib.call("fathom_copy_index_range", _ptr(t8), BH, d, nblk, b0, b1, block_bytes, planes,
+                      ctypes.c_void_p(getattr(src, data_attr).data_ptr()), ctypes.c_void_p(src.scales_k.data_ptr()),
+                      ctypes.c_void_p(getattr(staging, data_attr).data_ptr()),
+                      ctypes.c_void_p(staging.scales_k.data_ptr()), _stream(dev))
+            ev = torch.cuda.Event()
+            ev.record(s_copy)
+        with torch.cuda.stream(s_scan):
+            s_scan.wait_event(ev)
+            scan_chunk(scores, b0, b1)
+    ev1 = torch.cuda.Event()
+    ev1.record(s_scan)
+    cur.wait_event(ev1)
+    return scores
+
+
+def stream_planes(src, staging, q, plan, parts=4):
+    """Chunked copy-index scan (scripts/B_e2e_offload_v2.py:116-130 stream_planes):
+    blocks are split by chunk_bounds; each chunk's plan-selected plane runs and
+    scales go from src (host_store) into staging (staging_store) on a copy stream
+    while the previous chunk is scanned on a scan stream.  Returns scores
+    [BH, G, n], bit-identical to staging.scan after a whole copy_index."""
+    t8 = plan["t"].contiguous().to(torch.int8)
+    _need_gpu(q, t8)
+    if src.nsb != 1 or staging.nsb != 1 or (src.BH, src.n, src.sub) != (staging.BH, staging.n, staging.sub):
+        raise ValueError("stream_planes needs two whole-sequence-layout stores of the same shape")
+    return _stream_chunks(src, staging, t8, 4, 8, "planes32",
+                          lambda out, b0, b1: staging.scan(q, plan, out=out, blocks=(b0, b1)), staging.n, q, parts)
+
+
+def stream_chan4(src, staging, q, active, act, nact, parts=4):
+    """The chan4 store's chunked copy-index scan (scripts/B_e2e_offload_v2.py:132-144
+    stream_chan4): the active channels' nibble runs and scales of each chunk are
+    copied while the previous chunk is scanned.  Returns scores [BH, G, n]."""
+    a8 = active.contiguous().to(torch.int8)
+    _need_gpu(q, a8)
+    if src.nsb != 1 or staging.nsb != 1 or (src.BH, src.n, src.sub) != (staging.BH, staging.n, staging.sub):
+        raise ValueError("stream_chan4 needs two whole-sequence-layout stores of the same shape")
+    return _stream_chunks(src, staging, a8, 1, 32, "chan_k",
+                          lambda out, b0, b1: staging.scan(q, act, nact, out=out, blocks=(b0, b1)), staging.n, q,
+                          parts)
 
 
 def gather_rows(src, cap, idx, BH, dtype=torch.bfloat16, d=D):

@@ -222,6 +222,22 @@ int fathom_gather_attention(const float *q, const int64_t *idx, int64_t BH, int6
                             size_t workspace_bytes, void *stream);
 
 /*
+ * One chunk of the chunked copy/scan pipeline (scripts/B_e2e_offload_v2.py:
+ * 105-133, stream_planes / stream_chan4 with chunk_bounds): copies blocks
+ * [b0, b1) of every plan-selected run of a whole-sequence store (sub = nblk,
+ * nsb = 1) from data_src/scales_src to the same places of data_dst/scales_dst.
+ *   planes = 4: bit-plane store, data [BH, 1, D, 4, nblk] uint64
+ *               (block_bytes = 8), plane p of channel j copied when p < min(t, 4);
+ *   planes = 1: chan4 store, data [BH, 1, D, nblk, 8] uint32 (block_bytes = 32),
+ *               channel j copied when t > 0 (t = the active mask as int8);
+ *   scales [BH, 1, D, nblk] fp16, copied for channels with t > 0.
+ * t [BH, D] int8 (device).  BH * D * planes <= 65535.
+ */
+int fathom_copy_index_range(const int8_t *t, int64_t BH, int64_t D, int64_t nblk, int64_t b0, int64_t b1,
+                            int64_t block_bytes, int planes, const void *data_src, const void *scales_src,
+                            void *data_dst, void *scales_dst, void *stream);
+
+/*
  * gather_runs (scripts/B_e2e_offload_v2.py:62-71, gather_runs_kernel): copy run r,
  * the 4-byte words [off[r], off[r] + len[r]) of src, to the same words of dst,
  * for r < *nrun (off, len [R] int64 and nrun [1] int32 in device memory, so the

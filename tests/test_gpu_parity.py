@@ -773,3 +773,62 @@ def test_klt_store_scan_and_topk(budget):
     _scores_close(s.cpu().numpy(), ref)
     idx = st.scan_topk(q, plan, 2048, 4, 32)
     torch.testing.assert_close(idx, bp.sink_local_topk(s, 2048, 4, 32), rtol=0, atol=0)
+
+
+# ----------------------------------------------------------------------------- chunked copy/scan pipeline
+@pytest.mark.parametrize("n,parts", [(300000, 4), (50001, 3), (9000, 1), (130000, 8)])
+def test_stream_planes_equals_full_scan(n, parts):
+    """Chunks copied on one stream and scanned on another give the scores of the full
+    store bit for bit (the reference's PLANES_CHECK, with a zeroed staging store)."""
+    print(f"[stream_planes] n={n} parts={parts}", flush=True)
+    x = W.config_inputs(2, device="cpu", n=n, BH=2)
+    nb = math.ceil(n / 64)
+    old = bp.SUB
+    bp.SUB = nb
+    try:
+        full = bp.PlaneStore(x["K"].to(DEV), keep_code=False)
+    finally:
+        bp.SUB = old
+    q = x["q"].to(DEV)
+    plan = bp.make_plan(x["g"].to(DEV), x["budget"])
+    ref = full.scan(q, plan)
+    hs, hps = off.host_store(full)
+    try:
+        stg = off.staging_store(full)
+        got = off.stream_planes(hs, stg, q, plan, parts=parts)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+        # unselected runs stay zero in the staging store
+        t = plan["t"].cpu()
+        for b in range(2):
+            off_ch = (t[b] == 0).nonzero().flatten()[:3]
+            for j in off_ch.tolist():
+                assert int(stg.planes_k[b, 0, j].abs().sum().item()) == 0
+    finally:
+        for h in hps:
+            off.free_host(h)
+
+
+def test_stream_chan4_equals_full_scan():
+    n = 70000
+    K = _keys(2, n, dtype=torch.bfloat16, edge=False)
+    q = torch.randn(2, 4, 128).to(DEV)
+    old = bp.SUB
+    bp.SUB = math.ceil(n / 64)
+    try:
+        full = bp.Chan4Store(K.to(DEV), keep_code=False)
+    finally:
+        bp.SUB = old
+    active = torch.zeros(2, 128, dtype=torch.bool, device=DEV)
+    active.scatter_(1, q.abs().sum(1).topk(32, -1).indices, True)
+    act, nact = bp.channel_list(active)
+    ref = full.scan(q, act, nact)
+    hs, hps = off.host_store(full)
+    try:
+        stg = off.staging_store(full)
+        got = off.stream_chan4(hs, stg, q, active, act, nact, parts=4)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+    finally:
+        for h in hps:
+            off.free_host(h)

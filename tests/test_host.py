@@ -38,3 +38,17 @@ def test_capsio_reads_slices(tmp_path):
     assert torch.equal(f["v3"], t["v3"]) and torch.equal(f.get_tensor("ids"), t["ids"])
     assert f.get_slice("k0")[3:3].shape == (0, 300, 128)
     f.close()
+
+
+def test_chunk_bounds():
+    from fathom_amd.offload import chunk_bounds
+    assert chunk_bounds(1000, 4) == [(0, 192), (192, 448), (448, 704), (704, 1000)]
+    assert chunk_bounds(16384, 4) == [(0, 4096), (4096, 8192), (8192, 12288), (12288, 16384)]
+    assert chunk_bounds(100, 4) == [(0, 64), (64, 100)]          # empty chunks dropped
+    assert chunk_bounds(50, 3) == [(0, 50)]
+    for nblk in (1, 63, 64, 65, 777, 4097):
+        for parts in (1, 2, 3, 8):
+            ch = chunk_bounds(nblk, parts)
+            assert ch[0][0] == 0 and ch[-1][1] == nblk and len(ch) <= parts
+            assert all(a < b for a, b in ch) and all(ch[i][1] == ch[i + 1][0] for i in range(len(ch) - 1))
+            assert all(b % 64 == 0 for _, b in ch[:-1])
