@@ -168,8 +168,24 @@ def run_copy_index(torch, bp, off, x, K_dev, V_dev, steps, warmup):
         st = timer.collect()
         scan_bytes = bp.bytes_planes(out["plan"]["t"], n)
         uniq = int(out["rows"][1].sum().item())
+        # the reference's pipelined form (B_e2e_offload_v2.py:116-130): the copy of chunk
+        # c + 1 overlaps the scan of chunk c, then top-k over the scores
+        pnames = ["plan", "stream_scan", "topk", "attn"]
+        pfns = {"plan": fns["plan"],
+                "stream_scan": lambda o: o.__setitem__("scores", off.stream_planes(hs, stg, q, o["plan"], parts=4)),
+                "topk": lambda o: o.__setitem__("idx", bp.sink_local_topk(o["scores"], k, x["sink"], x["local"])),
+                "attn": fns["attn"]}
+        ptimer = StageTimer(torch, pnames)
+        for _ in range(warmup):
+            ptimer.step(pfns)
+        torch.cuda.synchronize()
+        ptimer.evs = []
+        for _ in range(steps):
+            pout = ptimer.step(pfns)
+        torch.cuda.synchronize()
+        pst = ptimer.collect()
         return {"stage_ms": st, "scan_bytes": scan_bytes, "row_bytes": 2 * uniq * 128 * 2, "unique_rows": uniq,
-                "idx": out["idx"]}
+                "idx": out["idx"], "pipelined_stage_ms": pst, "pipelined_idx": pout["idx"]}
     finally:
         for h in hps:
             off.free_host(h)
@@ -454,6 +470,13 @@ def main():
                           "roofline_pcie": {"peak": PCIE_PEAK_GBPS,
                                             "frac_step": ci_bytes / (ci_tot * 1e-3) / 1e9 / PCIE_PEAK_GBPS},
                           "index_sets_equal_hbm": bool(torch.equal(ci["idx"], hbm["idx"]))}
+            ps = ci["pipelined_stage_ms"]
+            p_tot = sum(ps.values())
+            copy_index["pipelined_4_chunks"] = {
+                "stage_ms": {k: round(v, 4) for k, v in ps.items()}, "step_ms": p_tot,
+                "pcie_GBps_step": ci_bytes / (p_tot * 1e-3) / 1e9,
+                "roofline_pcie": {"peak": PCIE_PEAK_GBPS, "frac_step": ci_bytes / (p_tot * 1e-3) / 1e9 / PCIE_PEAK_GBPS},
+                "index_sets_equal_hbm": bool(torch.equal(ci["pipelined_idx"], hbm["idx"]))}
             host = {"stage_ms": {k: round(v, 4) for k, v in hs.items()},
                     "scanned_tokens_per_s": n * BH / (hs["scan_topk"] * 1e-3),
                     "step_ms": tot, "pcie_bytes_per_step": pcie_bytes,
