@@ -46,10 +46,11 @@ constexpr int kGB = 8;             // blocks per wave
 constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kTB = kGB * kWaves;  // blocks per tile
 constexpr int kMaxD = 256;
-constexpr int kUnits = 16;         // (channel, plane) units per chunk
+constexpr int kWUnits = 32;        // (channel, plane) units per wave chunk
 static_assert(kTB * kBlk == kTileTok, "scan tile and top-k sample tile must agree");
 constexpr int kThreads = 64 * kWaves;
-static_assert(kUnits == 2 * (kThreads / kTB), "each thread stages two units of one block");
+static_assert(2 * kWUnits == kWave, "two staging lanes per unit");
+static_assert(kGB == 8, "a wave stages two groups of four blocks");
 
 enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2 };
 
@@ -73,6 +74,7 @@ struct ScanArgs {
   int64_t tile0;           // tile of blockIdx.x == 0 (tile T = blocks [32T, 32T + 32))
   int64_t tile_stride;     // tiles between consecutive workgroups
   int D, bmax, ncls;       // classes 1..ncls are scanned (ncls = min(bmax, 4))
+  int fast;                // sub % 4 == 0 and 16-byte (planes) / 8-byte (scales) aligned: vector staging loads
 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -130,20 +132,13 @@ __device__ __forceinline__ void accum(Acc<G> &acc, int b, const QOp<G> &q, float
 }
 
 // ----------------------------------------------------------------- value of a lane
-// y = a * x' of the lane's token from the C dwords holding its plane bits (bit
-// l31 of each) and the block's staged scale pair (P, Q):
+// y = a * x' of a lane's token from its plane bits and the block's staged
+// scale pair (P, Q):
 //  * depth 1: y = -a * x = (bit ? -a/2 : +a/2), the bit put into the sign of
 //    P = a/2 (a >= 0);
 //  * deeper: y = 2a * x = c * P + Q with P = 2a, Q = -(2^C - 1) a and c the
 //    C-bit code: one fused multiply-add of exact operands (c < 16, a fp16).
-template <int C>
-__device__ __forceinline__ float lane_value(const uint32_t (&dw)[C], int l31, uint32_t sign, float P, float Q) {
-  if (C == 1) return __uint_as_float(((dw[0] << (31 - l31)) & sign) | __float_as_uint(P));
-  uint32_t c = __builtin_amdgcn_ubfe(dw[0], l31, 1);
-#pragma unroll
-  for (int p = 1; p < C; ++p) c = (c << 1) + __builtin_amdgcn_ubfe(dw[p], l31, 1);
-  return fmaf((float)c, P, Q);
-}
+// (compute_chunk below forms both from the octet-layout dwords.)
 
 // --------------------------------------------------------------------- emission
 template <int G>
@@ -272,154 +267,290 @@ __device__ __forceinline__ void emit_group(const Emit &em, EmitShared<G> &es, co
 }
 
 // --------------------------------------------------------------------- tile kernel
-// One chunk of the plan: channels [i0, i0 + m) of depth class c + 1, staged as
-// m * (c + 1) (channel, plane) units (unit u = channel slot * (c + 1) + plane).
-struct Chunk {
-  int c, i0, m;
+// The plan as two streams, built once per workgroup: channel slots in class
+// order (class 1 list, then 2, 3, 4; SF[c] = end of class c's slots) and their
+// (channel, plane) units (slot s of class c owns units UE[c-1] + (s -
+// SF[c-1]) * (c + 1) + p, p < c + 1; UE[c] = end of class c's units).
+struct PlanStreams {
+  int SF[4], UE[4];
 };
 
-// Channels per chunk of class index c (depth c + 1): 16, 8, 5, 4.
-__host__ __device__ constexpr int chunk_channels(int c) { return kUnits / (c + 1); }
-
-__device__ __forceinline__ Chunk chunk_at(const int (&nc)[4], int k) {
+__device__ __forceinline__ PlanStreams plan_streams(const int (&nc)[4]) {
+  PlanStreams ps;
+  int s = 0, u = 0;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const int cpc = chunk_channels(c);
-    const int nk = (nc[c] + cpc - 1) / cpc;
-    if (k < nk) return Chunk{c, k * cpc, min(cpc, nc[c] - k * cpc)};
-    k -= nk;
+    s += nc[c];
+    u += nc[c] * (c + 1);
+    ps.SF[c] = s;
+    ps.UE[c] = u;
   }
-  return Chunk{0, 0, 0};
+  return ps;
 }
 
-// u / (c + 1) for u < 16 without a division
-__device__ __forceinline__ int unit_channel(int u, int c) {
-  return c == 0 ? u : c == 1 ? (u >> 1) : c == 2 ? ((u * 11) >> 5) : (u >> 2);
+// A wave chunk: plan slots [s0, s1) (whole channels), their units [u0, u1),
+// at most kWUnits units.
+struct Chunk {
+  int s0, s1, u0, u1;
+};
+
+// The chunk starting at slot s (s < SF[3]).
+__device__ __forceinline__ Chunk chunk_from(const PlanStreams &ps, int s) {
+  Chunk ck;
+  ck.s0 = s;
+  int used = 0, u0 = -1;
+  bool open = true;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int lo = c ? ps.SF[c - 1] : 0;
+    if (open && s < ps.SF[c]) {
+      if (u0 < 0) u0 = (c ? ps.UE[c - 1] : 0) + (s - lo) * (c + 1);
+      const int take = min(ps.SF[c] - s, (kWUnits - used) / (c + 1));
+      used += take * (c + 1);
+      s += take;
+      if (s < ps.SF[c]) open = false;
+    }
+  }
+  ck.s1 = s;
+  ck.u0 = u0;
+  ck.u1 = u0 + used;
+  return ck;
 }
 
-// A staged chunk: low and high dword of each unit's 32 block words, the scale
-// pair (P, Q) of each channel slot's 32 blocks, and each slot's head weights.
-template <int G>
-struct ChunkBuf {
-  alignas(16) uint32_t lo[kUnits][kTB];
-  alignas(16) uint32_t hi[kUnits][kTB];
-  alignas(16) float P[kUnits][kTB];
-  alignas(16) float Q[kUnits][kTB];
-  alignas(16) float w[kUnits][QShared<G>::QS];
+// A wave's staged chunk in the octet layout.  For unit u, block group g
+// (blocks 4g..4g+3 of the wave) and token octet o (tokens 8o..8o+7 of a
+// block), dword oct[u][g][o] holds byte o of the four blocks' plane words,
+// block k in byte k: bit 8k + t is token 8o + t of block 4g + k.  A lane
+// (token 8o + t) reads one dword per (unit, group) and finds its bit of the
+// four blocks at bits t, 8 + t, 16 + t, 24 + t.  A channel of depth C > 1
+// stores plane p rotated left by C - 1 - p: masking the C dwords at the lane's
+// positions, OR-ing them and one rotation right by t leave the lane's C-bit
+// code of block k in byte k.  P, Q: the scale pair of each channel slot and
+// block (see lane_value).
+struct WaveBuf {
+  alignas(16) uint32_t oct[kWUnits][2][8];
+  alignas(16) float P[kWUnits][kGB];
+  alignas(16) float Q[kWUnits][kGB];
 };
 
 template <int G>
 struct TileShared {
-  QShared<G> qs;
-  uint8_t lst[4][kMaxD];  // the plan's class lists, clamped to [0, D)
-  ChunkBuf<G> buf[2];
+  alignas(16) float w[kMaxD][QShared<G>::QS];  // head weights by plan slot
+  uint16_t unit[4 * kMaxD];                    // plan unit -> (j * 4 + p) << 2 | (C - 1 - p)
+  uint16_t slot[kMaxD];                        // plan slot -> j | class << 8
+  WaveBuf wb[kWaves];
 };
 
-// The words and scales one thread stages: block bi = tid % 32 of units and
-// channel slots tid / 32 and tid / 32 + 8.
+// What a lane loads for one chunk: the four plane words of its (unit, group)
+// with the rotation its plane needs, and the four scales of its (channel
+// slot, group) with the slot's class.
 struct Staged {
-  uint64_t w[2];
-  uint16_t s[2];
+  uint64_t w[4];
+  uint32_t s[2];
+  uint32_t rot;
+  int scls;
 };
 
-// pbase / sbase: element offsets of the thread's block in planes / scales with
-// the channel term left out (channel j adds j * 4 * sub / j * sub).
-__device__ __forceinline__ void load_chunk(Staged &r, const ScanArgs &a, const uint8_t (*lst)[kMaxD], const Chunk &ck,
-                                           int slot, bool inb, int64_t pbase, int64_t sbase) {
-  const int C = ck.c + 1;
+// A lane's staging addresses: element offsets of the first block of its plane
+// group (lane & 1) and of its scale group (lane >> 5), with the channel term
+// left out; all four blocks of a group share them when the store qualifies
+// for vector loads (sub % 4 == 0).
+struct LaneAddr {
+  int64_t pbase, sbase;
+  bool pin, sin;  // the group lies inside the store's nsb * sub blocks
+};
+
+__device__ __forceinline__ void group_base(const ScanArgs &a, int64_t bh, int64_t blk, int64_t &pb, int64_t &sb_off) {
+  const uint32_t s = (uint32_t)a.sub;
+  const uint32_t sb = (uint32_t)blk / s, off = (uint32_t)blk - sb * s;
+  pb = ((bh * a.nsb + sb) * a.D * 4) * a.sub + off;
+  sb_off = ((bh * a.nsb + sb) * a.D) * a.sub + off;
+}
+
+// Issues the global loads of chunk ck: lane l stages unit l >> 1 for block
+// group l & 1 and the scales of channel slot l & 31 for group l >> 5.
+template <int G, bool FAST>
+__device__ __forceinline__ void stage_load(Staged &r, const ScanArgs &a, const TileShared<G> &sh, const Chunk &ck,
+                                           const LaneAddr &la, int64_t gb0, int64_t bh, int lane) {
+  const int u = ck.u0 + (lane >> 1), g = lane & 1;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int u = slot + 8 * h;
-    r.w[h] = 0ull;
-    r.s[h] = 0;
-    if (inb && u < ck.m * C) {
-      const int ci = unit_channel(u, ck.c), p = u - ci * C;
-      const int j = lst[ck.c][ck.i0 + ci];
-      r.w[h] = a.planes[pbase + ((int64_t)j * 4 + p) * a.sub];
+  for (int k = 0; k < 4; ++k) r.w[k] = 0ull;
+  r.rot = 0u;
+  if (u < ck.u1) {
+    const uint32_t d = sh.unit[u];
+    const int64_t jp = d >> 2;
+    r.rot = (32u - (d & 3u)) & 31u;  // alignbit amount of the left rotation by C - 1 - p
+    if (FAST) {
+      if (la.pin) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.planes + la.pbase + jp * a.sub);
+        const uint4 v0 = src[0], v1 = src[1];
+        r.w[0] = ((uint64_t)v0.y << 32) | v0.x;
+        r.w[1] = ((uint64_t)v0.w << 32) | v0.z;
+        r.w[2] = ((uint64_t)v1.y << 32) | v1.x;
+        r.w[3] = ((uint64_t)v1.w << 32) | v1.z;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t blk = gb0 + 4 * g + k;
+        if (blk < a.nsb * a.sub) {
+          int64_t pb, sbo;
+          group_base(a, bh, blk, pb, sbo);
+          r.w[k] = a.planes[pb + jp * a.sub];
+        }
+      }
     }
-    if (inb && u < ck.m) {
-      const int j = lst[ck.c][ck.i0 + u];
-      r.s[h] = a.scales[sbase + (int64_t)j * a.sub];
+  }
+  const int cs = ck.s0 + (lane & 31), gs = lane >> 5;
+  r.s[0] = r.s[1] = 0u;
+  r.scls = 0;
+  if (cs < ck.s1) {
+    const uint32_t sd = sh.slot[cs];
+    const int64_t j = sd & 0xFFu;
+    r.scls = (int)(sd >> 8);
+    if (FAST) {
+      if (la.sin) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(a.scales + la.sbase + j * a.sub);
+        r.s[0] = v.x;
+        r.s[1] = v.y;
+      }
+    } else {
+      uint32_t h[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t blk = gb0 + 4 * gs + k;
+        if (blk < a.nsb * a.sub) {
+          int64_t pb, sbo;
+          group_base(a, bh, blk, pb, sbo);
+          h[k] = a.scales[sbo + j * a.sub];
+        }
+      }
+      r.s[0] = h[0] | (h[1] << 16);
+      r.s[1] = h[2] | (h[3] << 16);
     }
   }
 }
 
-// Writes a loaded chunk to LDS; the head weights of its channel slots come from
-// the workgroup's weight table (thread (slot, bi < QS) copies slot's weight bi).
-template <int G>
-__device__ __forceinline__ void store_chunk(ChunkBuf<G> &b, const Staged &r, const QShared<G> &qs,
-                                            const uint8_t (*lst)[kMaxD], const Chunk &ck, int slot, int bi) {
-  constexpr int QS = QShared<G>::QS;
+// Writes a loaded chunk to the wave's buffer: plane words as octet dwords
+// (two 4 x 4 byte transposes per lane, rotated for the unit's plane) and the
+// scale pairs.
+__device__ __forceinline__ void stage_store(WaveBuf &wb, const Staged &r, const Chunk &ck, int lane) {
+  const int u = lane >> 1, g = lane & 1;
+  if (ck.u0 + u < ck.u1) {
+    uint32_t out[8];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int u = slot + 8 * h;
-    b.lo[u][bi] = (uint32_t)r.w[h];
-    b.hi[u][bi] = (uint32_t)(r.w[h] >> 32);
-    const float a = __half2float(__ushort_as_half(r.s[h]));
-    b.P[u][bi] = ck.c == 0 ? 0.5f * a : 2.0f * a;
-    b.Q[u][bi] = ck.c == 0 ? 0.0f : -(float)((2 << ck.c) - 1) * a;
-    if (bi < QS && u < ck.m) b.w[u][bi] = qs.w[lst[ck.c][ck.i0 + u] * QS + bi];
+    for (int h = 0; h < 2; ++h) {  // h = 0: tokens 0-31 (octets 0-3), h = 1: tokens 32-63
+      const uint32_t x0 = (uint32_t)(r.w[0] >> (32 * h)), x1 = (uint32_t)(r.w[1] >> (32 * h));
+      const uint32_t x2 = (uint32_t)(r.w[2] >> (32 * h)), x3 = (uint32_t)(r.w[3] >> (32 * h));
+      const uint32_t e0 = __builtin_amdgcn_perm(x1, x0, 0x06020400u);  // x0.b0 x1.b0 x0.b2 x1.b2
+      const uint32_t e1 = __builtin_amdgcn_perm(x1, x0, 0x07030501u);  // x0.b1 x1.b1 x0.b3 x1.b3
+      const uint32_t e2 = __builtin_amdgcn_perm(x3, x2, 0x06020400u);
+      const uint32_t e3 = __builtin_amdgcn_perm(x3, x2, 0x07030501u);
+      out[4 * h + 0] = __builtin_amdgcn_perm(e2, e0, 0x05040100u);  // byte 0 of x0..x3
+      out[4 * h + 1] = __builtin_amdgcn_perm(e3, e1, 0x05040100u);  // byte 1
+      out[4 * h + 2] = __builtin_amdgcn_perm(e2, e0, 0x07060302u);  // byte 2
+      out[4 * h + 3] = __builtin_amdgcn_perm(e3, e1, 0x07060302u);  // byte 3
+    }
+#pragma unroll
+    for (int o = 0; o < 8; ++o) out[o] = __builtin_amdgcn_alignbit(out[o], out[o], r.rot);
+    uint4 *dst = reinterpret_cast<uint4 *>(&wb.oct[u][g][0]);
+    dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+    dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+  }
+  const int cs = lane & 31, gs = lane >> 5;
+  if (ck.s0 + cs < ck.s1) {
+    float P[4], Q[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = __half2float(__ushort_as_half((uint16_t)(r.s[k >> 1] >> (16 * (k & 1)))));
+      P[k] = r.scls == 0 ? 0.5f * a : 2.0f * a;
+      Q[k] = r.scls == 0 ? 0.0f : -(float)((2 << r.scls) - 1) * a;
+    }
+    *reinterpret_cast<float4 *>(&wb.P[cs][4 * gs]) = make_float4(P[0], P[1], P[2], P[3]);
+    *reinterpret_cast<float4 *>(&wb.Q[cs][4 * gs]) = make_float4(Q[0], Q[1], Q[2], Q[3]);
   }
 }
 
-// The wave's 8 blocks of every channel of a staged chunk of depth C, in list
-// order, four blocks per half: one 16-byte LDS read per (plane, half) brings the
-// lane's four dwords, two more the four scale pairs.
+// Orders the wave's LDS accesses around a staging store: every lane's writes
+// complete before any lane reads the chunk, and the reads of the previous chunk
+// before the writes.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The wave's 8 blocks of chunk slots [s0, s1), all of depth C, whose units
+// start at chunk unit u0; w: the head weights of those slots.  In slot order,
+// four blocks per group: one dword read per (plane, group) brings the lane's
+// bits of the group's four blocks, two 16-byte reads the scale pairs.
 template <int C, int G>
-__device__ __forceinline__ void compute_chunk(const ChunkBuf<G> &b, int m, int wave, int lane, uint32_t sign,
-                                              Acc<G> &acc) {
-  constexpr int QS = QShared<G>::QS;
-  const int l31 = lane & 31;
-  const uint32_t *wl = (lane < 32 ? &b.lo[0][0] : &b.hi[0][0]) + wave * kGB;
-  for (int ci = 0; ci < m; ++ci) {
+__device__ __forceinline__ void compute_slots(const WaveBuf &wb, const float (*w)[QShared<G>::QS], int s0, int s1,
+                                              int u0, int lane, uint32_t sign, Acc<G> &acc) {
+  const int o = lane >> 3, t = lane & 7;
+  // depth 1: the shift bringing block k's bit to bit 31; deeper: plane p's mask
+  uint32_t sh[4], mk[C];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sh[k] = (uint32_t)(31 - 8 * k - t);
+#pragma unroll
+  for (int p = 0; p < C; ++p) mk[p] = 0x01010101u << ((t + C - 1 - p) & 7);
+  const uint32_t *ob = &wb.oct[u0][0][o];
+  for (int ci = s0; ci < s1; ++ci, ob += C * 16) {
     QOp<G> q;
 #pragma unroll
-    for (int h = 0; h < QOp<G>::NQ; ++h) q.a[h] = b.w[ci][4 * h + (lane & 3)];
+    for (int h = 0; h < QOp<G>::NQ; ++h) q.a[h] = w[ci][4 * h + (lane & 3)];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const float4 P4 = *reinterpret_cast<const float4 *>(&b.P[ci][wave * kGB + 4 * hf]);
+    for (int g = 0; g < 2; ++g) {
+      const float4 P4 = *reinterpret_cast<const float4 *>(&wb.P[ci][4 * g]);
       float4 Q4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (C > 1) Q4 = *reinterpret_cast<const float4 *>(&b.Q[ci][wave * kGB + 4 * hf]);
+      if (C > 1) Q4 = *reinterpret_cast<const float4 *>(&wb.Q[ci][4 * g]);
       const float P[4] = {P4.x, P4.y, P4.z, P4.w}, Q[4] = {Q4.x, Q4.y, Q4.z, Q4.w};
-      uint4 dq[C];
+      uint32_t d[C];
 #pragma unroll
-      for (int p = 0; p < C; ++p) dq[p] = *reinterpret_cast<const uint4 *>(wl + (ci * C + p) * kTB + 4 * hf);
+      for (int p = 0; p < C; ++p) d[p] = ob[p * 16 + g * 8];
       float y[4];
+      if (C == 1) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint32_t dw[C];
+        for (int k = 0; k < 4; ++k) y[k] = __uint_as_float(((d[0] << sh[k]) & sign) | __float_as_uint(P[k]));
+      } else {
+        uint32_t x = d[0] & mk[0];
 #pragma unroll
-        for (int p = 0; p < C; ++p) dw[p] = r == 0 ? dq[p].x : r == 1 ? dq[p].y : r == 2 ? dq[p].z : dq[p].w;
-        y[r] = lane_value<C>(dw, l31, sign, P[r], Q[r]);
+        for (int p = 1; p < C; ++p) x |= d[p] & mk[p];
+        x = __builtin_amdgcn_alignbit(x, x, (uint32_t)t);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) y[k] = fmaf((float)((x >> (8 * k)) & 0xFFu), P[k], Q[k]);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) accum<G>(acc, 4 * hf + r, q, y[r]);
+      for (int k = 0; k < 4; ++k) accum<G>(acc, 4 * g + k, q, y[k]);
     }
   }
 }
 
-// Workgroup prologue: the plan's class lists and the head weights in LDS
-// (w = -q at depth 1, q * 2^-t deeper: see lane_value).
+// Workgroup prologue: the plan streams in LDS -- per slot its channel and
+// class and the head weights (w = -q at depth 1, q * 2^-C deeper: exact
+// power-of-two scalings), per unit its plane word index and rotation.
 template <int G>
-__device__ __forceinline__ void tile_prologue(TileShared<G> &sh, const ScanArgs &a, const int (&nc)[4], int64_t bh) {
+__device__ __forceinline__ void tile_prologue(TileShared<G> &sh, const ScanArgs &a, const int (&nc)[4],
+                                              const PlanStreams &ps, int64_t bh) {
   constexpr int QS = QShared<G>::QS;
-  const int pre1 = nc[0], pre2 = pre1 + nc[1], pre3 = pre2 + nc[2], tot = pre3 + nc[3];
-  for (int e = threadIdx.x; e < tot; e += kThreads) {
-    const int c = (e >= pre1) + (e >= pre2) + (e >= pre3);
-    const int i = e - (c == 0 ? 0 : c == 1 ? pre1 : c == 2 ? pre2 : pre3);
-    const int jr = a.cls[(bh * a.bmax + c) * a.D + i];
+  for (int e = threadIdx.x; e < ps.SF[3]; e += kThreads) {
+    const int c = (e >= ps.SF[0]) + (e >= ps.SF[1]) + (e >= ps.SF[2]);
+    const int lo = c == 0 ? 0 : c == 1 ? ps.SF[0] : c == 2 ? ps.SF[1] : ps.SF[2];
+    const int ub = (c == 0 ? 0 : c == 1 ? ps.UE[0] : c == 2 ? ps.UE[1] : ps.UE[2]) + (e - lo) * (c + 1);
+    const int jr = a.cls[(bh * a.bmax + c) * a.D + (e - lo)];
     const int j = min(max(jr, 0), a.D - 1);  // memory-safe; make_plan lists only valid channels
-    sh.lst[c][i] = (uint8_t)j;
+    sh.slot[e] = (uint16_t)(j | (c << 8));
+    for (int p = 0; p <= c; ++p) sh.unit[ub + p] = (uint16_t)(((j * 4 + p) << 2) | (c - p));
 #pragma unroll
     for (int g = 0; g < QS; ++g) {
       const float qv = g < G ? a.q[(bh * G + g) * a.D + j] : 0.0f;
-      sh.qs.w[j * QS + g] = c == 0 ? -qv : ldexpf(qv, -(c + 1));
+      sh.w[e][g] = c == 0 ? -qv : ldexpf(qv, -(c + 1));
     }
   }
 }
 
-template <int G, int MODE>
-__global__ __launch_bounds__(kThreads) void scan_tile_kernel(ScanArgs a, Emit em) {
+template <int G, int MODE, bool FAST>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 5 : 4))) void scan_tile_kernel(ScanArgs a, Emit em) {
   __shared__ TileShared<G> sh;
   __shared__ EmitShared<G> es;
   const int tid = threadIdx.x;
@@ -437,56 +568,58 @@ __global__ __launch_bounds__(kThreads) void scan_tile_kernel(ScanArgs a, Emit em
   int nc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) nc[c] = c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
-  tile_prologue<G>(sh, a, nc, bh);
-  // the thread's staging block
-  const int bi = tid & (kTB - 1), slot = tid / kTB;
-  const int64_t b = tb0 + bi;
-  const bool inb = b < a.nsb * a.sub;
-  const int64_t sb = inb ? b / a.sub : 0;
-  const int64_t off = b - sb * a.sub;
-  const int64_t pbase = (bh * a.nsb + sb) * a.D * 4 * a.sub + off;
-  const int64_t sbase = (bh * a.nsb + sb) * a.D * a.sub + off;
+  const PlanStreams ps = plan_streams(nc);
+  tile_prologue<G>(sh, a, nc, ps, bh);
+  const int64_t gb0 = tb0 + wave * kGB;  // the wave's first block
+  LaneAddr la{0, 0, false, false};
+  {
+    const int64_t pblk = gb0 + 4 * (lane & 1), sblk = gb0 + 4 * (lane >> 5);
+    int64_t unused;
+    la.pin = pblk < a.nsb * a.sub;
+    la.sin = sblk < a.nsb * a.sub;
+    if (la.pin) group_base(a, bh, pblk, la.pbase, unused);
+    if (la.sin) group_base(a, bh, sblk, unused, la.sbase);
+  }
   Acc<G> acc;
   acc.zero();
-  int nk = 0;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) nk += (nc[c] + chunk_channels(c) - 1) / chunk_channels(c);
-  if (tb0 < a.blk_end && tb0 + kTB > a.blk0 && nk > 0) {  // uniform over the workgroup
+  WaveBuf &wb = sh.wb[wave];
+  __syncthreads();  // plan streams ready
+  if (tb0 < a.blk_end && tb0 + kTB > a.blk0 && ps.SF[3] > 0) {  // uniform over the workgroup
     Staged r;
     // the sign-bit mask as an opaque VGPR value (VOP3 encodings take no literal)
     uint32_t sign;
     asm("v_mov_b32 %0, 0x80000000" : "=v"(sign));
-    __syncthreads();  // class lists and weights ready
-    Chunk nxt = chunk_at(nc, 0);
-    load_chunk(r, a, sh.lst, nxt, slot, inb, pbase, sbase);
-    store_chunk<G>(sh.buf[0], r, sh.qs, sh.lst, nxt, slot, bi);
-    __syncthreads();
-    int k = 0;
-    // classes in order, each a loop over its chunks with the depth known at
-    // compile time; the next chunk (possibly of the next class) is loaded
-    // while the current one is computed
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      constexpr int kC[4] = {1, 2, 3, 4};
-      const int cpc = chunk_channels(c);
-      for (int i0 = 0; i0 < nc[c]; i0 += cpc, ++k) {
-        const bool more = k + 1 < nk;
-        if (more) {
-          nxt = chunk_at(nc, k + 1);
-          load_chunk(r, a, sh.lst, nxt, slot, inb, pbase, sbase);
-        }
-        const ChunkBuf<G> &cb = sh.buf[k & 1];
-        const int m = min(cpc, nc[c] - i0);
-        if (c == 0) compute_chunk<kC[0], G>(cb, m, wave, lane, sign, acc);
-        if (c == 1) compute_chunk<kC[1], G>(cb, m, wave, lane, sign, acc);
-        if (c == 2) compute_chunk<kC[2], G>(cb, m, wave, lane, sign, acc);
-        if (c == 3) compute_chunk<kC[3], G>(cb, m, wave, lane, sign, acc);
-        if (more) store_chunk<G>(sh.buf[(k + 1) & 1], r, sh.qs, sh.lst, nxt, slot, bi);
-        __syncthreads();
+    Chunk cur = chunk_from(ps, 0);
+    stage_load<G, FAST>(r, a, sh, cur, la, gb0, bh, lane);
+    // chunks in plan order; the next chunk is loaded while the current one is
+    // computed.  Waves run independently: each stages and computes its own blocks.
+    while (true) {
+      wave_lds_sync();  // the previous chunk's reads are done
+      stage_store(wb, r, cur, lane);
+      wave_lds_sync();
+      const bool more = cur.s1 < ps.SF[3];
+      Chunk nxt = cur;
+      if (more) {
+        nxt = chunk_from(ps, cur.s1);
+        stage_load<G, FAST>(r, a, sh, nxt, la, gb0, bh, lane);
       }
+      const float (*w)[QShared<G>::QS] = sh.w + cur.s0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int lo = max(cur.s0, c ? ps.SF[c - 1] : 0), hi = min(cur.s1, ps.SF[c]);
+        if (lo < hi) {
+          const int ul = (c ? ps.UE[c - 1] : 0) + (lo - (c ? ps.SF[c - 1] : 0)) * (c + 1) - cur.u0;
+          if (c == 0) compute_slots<1, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+          if (c == 1) compute_slots<2, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+          if (c == 2) compute_slots<3, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+          if (c == 3) compute_slots<4, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+        }
+      }
+      if (!more) break;
+      cur = nxt;
     }
   }
-  emit_group<G, MODE>(em, es, acc, bh, tb0 + wave * kGB, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
+  emit_group<G, MODE>(em, es, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
 }
 
 // --------------------------------------------------------------------- chan4 baseline scan
@@ -642,7 +775,10 @@ void launch_chan4_g(const Chan4Args &a, int64_t tiles, int64_t BH, const Emit &e
 // --------------------------------------------------------------------- launch
 template <int G, int MODE>
 void launch_g(const ScanArgs &a, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
-  scan_tile_kernel<G, MODE><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
+  if (a.fast)
+    scan_tile_kernel<G, MODE, true><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
+  else
+    scan_tile_kernel<G, MODE, false><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
 }
 
 template <int MODE>
@@ -691,6 +827,8 @@ ScanArgs make_args(const float *q, int64_t D, const int32_t *cls, const int32_t 
   a.bmax = bmax;
   a.ncls = bmax < 4 ? bmax : 4;
   a.tile_stride = 1;
+  a.fast = sub % 4 == 0 && (reinterpret_cast<uintptr_t>(planes_sb) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(scales_sb) & 7) == 0;
   return a;
 }
 
