@@ -52,7 +52,7 @@ constexpr int kThreads = 64 * kWaves;
 static_assert(2 * kWUnits == kWave, "two staging lanes per unit");
 static_assert(kGB == 8, "a wave stages two groups of four blocks");
 
-enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2 };
+enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2, kEmitFallback = 3 };
 
 struct Emit {
   float *out;        // scores [BH, G, n]
@@ -72,7 +72,8 @@ struct ScanArgs {
   int64_t n, nsb, sub;
   int64_t blk0, blk_end;   // blocks [blk0, blk_end) are emitted
   int64_t tile0;           // tile of blockIdx.x == 0 (tile T = blocks [32T, 32T + 32))
-  int64_t tile_stride;     // tiles between consecutive workgroups
+  int64_t tile_stride;     // tiles between consecutive list entries
+  int64_t ntiles;          // list entries (tile0 + L * tile_stride, L < ntiles)
   int D, bmax, ncls;       // classes 1..ncls are scanned (ncls = min(bmax, 4))
   int fast;                // sub % 4 == 0 and 16-byte (planes) / 8-byte (scales) aligned: vector staging loads
 };
@@ -549,27 +550,13 @@ __device__ __forceinline__ void tile_prologue(TileShared<G> &sh, const ScanArgs 
   }
 }
 
+// One tile (list entry L of the launch) of a workgroup: the plan streams are in
+// LDS; each wave stages and computes its own 8 blocks, then emits them.
 template <int G, int MODE, bool FAST>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 5 : 4))) void scan_tile_kernel(ScanArgs a, Emit em) {
-  __shared__ TileShared<G> sh;
-  __shared__ EmitShared<G> es;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+__device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, TileShared<G> &sh, EmitShared<G> &es,
+                                         const PlanStreams &ps, int64_t L, int wave, int lane) {
   const int64_t bh = blockIdx.y;
-  const int64_t tile = a.tile0 + (int64_t)blockIdx.x * a.tile_stride;
-  const int64_t tb0 = tile * kTB;
-  if (MODE == kEmitFilter && em.fallback) {  // uniform: skip the tile unless one of its rows needs the pass
-    bool need = false;
-#pragma unroll
-    for (int g = 0; g < G; ++g) need |= ld_uniform(em.sel.cand_cnt + bh * G + g) < em.sel.kk;
-    if (!need) return;
-  }
-  int nc[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) nc[c] = c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
-  const PlanStreams ps = plan_streams(nc);
-  tile_prologue<G>(sh, a, nc, ps, bh);
+  const int64_t tb0 = (a.tile0 + L * a.tile_stride) * kTB;
   const int64_t gb0 = tb0 + wave * kGB;  // the wave's first block
   LaneAddr la{0, 0, false, false};
   {
@@ -583,7 +570,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4
   Acc<G> acc;
   acc.zero();
   WaveBuf &wb = sh.wb[wave];
-  __syncthreads();  // plan streams ready
   if (tb0 < a.blk_end && tb0 + kTB > a.blk0 && ps.SF[3] > 0) {  // uniform over the workgroup
     Staged r;
     // the sign-bit mask as an opaque VGPR value (VOP3 encodings take no literal)
@@ -619,7 +605,37 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4
       cur = nxt;
     }
   }
-  emit_group<G, MODE>(em, es, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
+  emit_group<G, MODE>(em, es, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, L);
+}
+
+// One tile per workgroup (grid.x = list entries), except the fallback pass:
+// a grid-stride loop of few workgroups over the list, so that rows which need
+// no fallback (every row, normally) cost only those workgroups' launches.
+template <int G, int MODE, bool FAST>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4 && MODE != kEmitFallback ? 5 : 4))) void scan_tile_kernel(ScanArgs a, Emit em) {
+  __shared__ TileShared<G> sh;
+  __shared__ EmitShared<G> es;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t bh = blockIdx.y;
+  if (MODE == kEmitFallback) {  // uniform: skip the row unless one of its heads needs the pass
+    bool need = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) need |= ld_uniform(em.sel.cand_cnt + bh * G + g) < em.sel.kk;
+    if (!need) return;
+  }
+  int nc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) nc[c] = c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
+  const PlanStreams ps = plan_streams(nc);
+  tile_prologue<G>(sh, a, nc, ps, bh);
+  __syncthreads();  // plan streams ready
+  if (MODE == kEmitFallback) {
+    for (int64_t L = blockIdx.x; L < a.ntiles; L += gridDim.x) scan_one<G, kEmitFilter, FAST>(a, em, sh, es, ps, L, wave, lane);
+  } else {
+    scan_one<G, MODE, FAST>(a, em, sh, es, ps, blockIdx.x, wave, lane);
+  }
 }
 
 // --------------------------------------------------------------------- chan4 baseline scan
@@ -781,9 +797,14 @@ void launch_g(const ScanArgs &a, int64_t tiles, int64_t BH, const Emit &em, hipS
     scan_tile_kernel<G, MODE, false><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
 }
 
+constexpr int64_t kFallbackWGs = 64;  // workgroups per row of the fallback pass
+
 template <int MODE>
-int launch_scan(const ScanArgs &a, int64_t G, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
+int launch_scan(const ScanArgs &a0, int64_t G, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
   if (tiles <= 0) return FATHOM_OK;
+  ScanArgs a = a0;
+  a.ntiles = tiles;
+  if (MODE == kEmitFallback && tiles > kFallbackWGs) tiles = kFallbackWGs;
   switch (G) {
     case 1: launch_g<1, MODE>(a, tiles, BH, em, st); break;
     case 2: launch_g<2, MODE>(a, tiles, BH, em, st); break;
@@ -904,7 +925,7 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   if (rc) return rc;
   if (r_hi < kk) {  // T_hi may exceed a row's kk-th largest key: rows with < kk candidates scan again with T_lo
     em.fallback = 1;
-    rc = launch_scan<kEmitFilter>(a, G, cdiv(nblk, kTB), BH, em, st);
+    rc = launch_scan<kEmitFallback>(a, G, cdiv(nblk, kTB), BH, em, st);
     if (rc) return rc;
   }
   return launch_finalize(rows, m, k, sink, local, em.sel, idx, st);

@@ -37,17 +37,21 @@ struct TopkSel {
   uint32_t kk;
 };
 
-// Sample stride in tiles: about 8192 / kk expected candidates per row while
-// keeping at least 4 kk sampled tokens and at most kMaxSample of them.
+// Sample stride in tiles: about 8 sampled tiles per row, more where the sample
+// must hold 2 kk keys or where about 16 sampled keys must reach the first-pass
+// threshold (kAlpha * kk * sample / n >= 16), at most kMaxSample keys.
 inline int64_t topk_tile_stride(int64_t n, int64_t kk) {
   const int64_t ntiles = cdiv(n, kTileTok);
-  int64_t S = kk > 0 ? 8192 / kk : 64;
-  const int64_t keep = kk > 0 ? (ntiles * kTileTok) / (4 * kk) : 64;
-  if (keep < S) S = keep;
-  const int64_t fit = cdiv(ntiles, kMaxSample / kTileTok);
-  if (S < fit) S = fit;
-  if (S < 1) S = 1;
-  return S;
+  int64_t want = 8;
+  if (kk > 0) {
+    const int64_t a = cdiv(2 * kk, kTileTok), b = cdiv(16 * n, kAlpha * kk * kTileTok);
+    want = a > want ? a : want;
+    want = b > want ? b : want;
+  }
+  const int64_t cap = kMaxSample / kTileTok;
+  if (want > cap) want = cap;
+  const int64_t S = ntiles / want;
+  return S < 1 ? 1 : S;
 }
 
 inline int64_t topk_sample_tiles(int64_t n, int64_t S) { return cdiv(cdiv(n, kTileTok), S); }
