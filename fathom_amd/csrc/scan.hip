@@ -907,14 +907,14 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   int64_t S = 1;
   topk_layout(rows, n, k, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
   em.sel.kk = (uint32_t)kk;
-  const int64_t r_hi = topk_hi_rank(n, S, kk);
-  em.sink = sink;
-  em.lstart = (m - local) > 0 ? (m - local) : 0;
   const int64_t nblk = cdiv(n, kBlk);
   ScanArgs a = make_args(q, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub);
   a.blk0 = 0;
   a.blk_end = nblk;
   a.tile0 = 0;
+  const int64_t r_hi = topk_hi_rank(n, S, kk);
+  em.sink = sink;
+  em.lstart = (m - local) > 0 ? (m - local) : 0;
   a.tile_stride = S;
   rc = launch_scan<kEmitSample>(a, G, topk_sample_tiles(n, S), BH, em, st);
   if (rc) return rc;

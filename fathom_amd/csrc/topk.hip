@@ -334,27 +334,24 @@ __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const flo
 
 // Exact top kk of a row's candidates, sorted by K64 descending (score
 // descending, index ascending), then the sink and local positions.
-__global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_t k, int64_t sink, int64_t local,
-                                                               TopkSel s, int64_t *__restrict__ idx) {
+// Exact top kk of cnt distinct K64 values read through get(i), sorted
+// descending, written to out, followed by the sink and local positions (the
+// whole workgroup calls it).  cl: LDS scratch of kCandLds values, which also
+// holds the values when cnt <= kCandLds and stage is set (get may read cl
+// only when stage is clear).
+template <typename Get>
+__device__ void select_sorted(Get get, int64_t cnt, int64_t kk, int64_t m, int64_t sink, int64_t local,
+                              int64_t *out, uint64_t *cl, uint64_t *ss, RangeShared &sh, uint32_t &s_cnt,
+                              bool stage = true) {
   constexpr int kPer = kCandLds / kFinThreads;
-  __shared__ uint64_t cl[kCandLds];
-  __shared__ uint64_t ss[kMaxK];
-  __shared__ RangeShared sh;
-  __shared__ uint32_t s_cnt;
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const int64_t kk = k - sink - local;
-  const uint32_t c1 = s.cand_cnt[row];  // the fallback pass ran for rows whose first pass found < kk
-  const int64_t cnt = min((int64_t)(c1 >= s.kk ? c1 : s.cand2_cnt[row]), s.cand_cap);
-  const uint64_t *gc = s.cand + row * s.cand_cap;
-  int64_t *out = idx + row * k;
-  const bool in_lds = cnt <= kCandLds;
+  const bool in_lds = stage && cnt <= kCandLds;
   if (in_lds) {
     uint64_t v[kPer];  // all loads in flight before the first store
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int64_t i = tid + (int64_t)u * kFinThreads;
-      v[u] = i < cnt ? gc[i] : 0ull;
+      v[u] = i < cnt ? get(i) : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
@@ -366,9 +363,9 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   __syncthreads();
   // the exact kk largest first (range selection), then sorted
   const uint64_t thr = in_lds ? range_select([&](int64_t i) { return cl[i]; }, cnt, (uint32_t)kk, sh)
-                              : range_select([&](int64_t i) { return gc[i]; }, cnt, (uint32_t)kk, sh);
+                              : range_select(get, cnt, (uint32_t)kk, sh);
   for (int64_t i = tid; i < cnt; i += kFinThreads) {
-    const uint64_t v = in_lds ? cl[i] : gc[i];
+    const uint64_t v = in_lds ? cl[i] : get(i);
     if (v >= thr) {
       const uint32_t p = atomicAdd(&s_cnt, 1u);
       if (p < (uint32_t)kMaxK) ss[p] = v;
@@ -392,6 +389,48 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   for (int i = got + tid; i < (int)kk; i += kFinThreads) out[i] = 0;
   for (int i = tid; i < (int)(sink + local); i += kFinThreads)
     out[kk + i] = (i < sink) ? (int64_t)i : (int64_t)(m - local + (i - sink));
+}
+
+// Exact top kk of a row's candidates (the list of the pass in effect).
+__global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_t k, int64_t sink, int64_t local,
+                                                               TopkSel s, int64_t *__restrict__ idx) {
+  __shared__ uint64_t cl[kCandLds];
+  __shared__ uint64_t ss[kMaxK];
+  __shared__ RangeShared sh;
+  __shared__ uint32_t s_cnt;
+  const int64_t row = blockIdx.x;
+  const uint32_t c1 = s.cand_cnt[row];  // the fallback pass ran for rows whose first pass found < kk
+  const int64_t cnt = min((int64_t)(c1 >= s.kk ? c1 : s.cand2_cnt[row]), s.cand_cap);
+  const uint64_t *gc = s.cand + row * s.cand_cap;
+  select_sorted([&](int64_t i) { return gc[i]; }, cnt, k - sink - local, m, sink, local, idx + row * k, cl, ss, sh,
+                s_cnt);
+}
+
+// Exact top kk of a whole score row (rows up to kRowSelectMax): every element
+// is a candidate.  Rows up to 2 * kCandLds keep their 32-bit keys in LDS (the
+// K64 of element i is rebuilt from its key and index); longer rows would be
+// read from global memory.
+__global__ __launch_bounds__(kFinThreads) void rowselect_kernel(const float *__restrict__ scores, int64_t n, int64_t m,
+                                                                int64_t k, int64_t sink, int64_t local,
+                                                                int64_t *__restrict__ idx) {
+  __shared__ uint64_t cl[kCandLds];
+  __shared__ uint64_t ss[kMaxK];
+  __shared__ RangeShared sh;
+  __shared__ uint32_t s_cnt;
+  const int64_t row = blockIdx.x;
+  const float *rs = scores + row * n;
+  const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
+  const int64_t kk = k - sink - local;
+  if (n <= 2 * kCandLds) {
+    uint32_t *kl = reinterpret_cast<uint32_t *>(cl);
+    for (int64_t i = threadIdx.x; i < n; i += kFinThreads) kl[i] = masked_key(rs, i, sink, lstart);
+    __syncthreads();
+    select_sorted([&](int64_t i) { return ((uint64_t)kl[i] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i); }, n, kk,
+                  m, sink, local, idx + row * k, cl, ss, sh, s_cnt, false);
+  } else {
+    select_sorted([&](int64_t i) { return k64_of(masked_key(rs, i, sink, lstart), i); }, n, kk, m, sink, local,
+                  idx + row * k, cl, ss, sh, s_cnt);
+  }
 }
 
 __global__ __launch_bounds__(256) void fixed_only_kernel(int64_t rows, int64_t m, int64_t k, int64_t sink,
@@ -462,6 +501,12 @@ int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t lo
   return launch_status("finalize_kernel");
 }
 
+int launch_rowselect(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+                     int64_t *idx, hipStream_t st) {
+  rowselect_kernel<<<(unsigned)rows, kFinThreads, 0, st>>>(scores, n, m, k, sink, local, idx);
+  return launch_status("rowselect_kernel");
+}
+
 int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st) {
   if (k == 0) return FATHOM_OK;
   fixed_only_kernel<<<(unsigned)min(cdiv(rows * k, 256), (int64_t)65535), 256, 0, st>>>(rows, m, k, sink, local, idx);
@@ -508,6 +553,7 @@ extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t
   int64_t samp_cap = 0, S = 1;
   topk_layout(rows, n, k, static_cast<char *>(workspace), &samp, &samp_cap, &s, &S);
   s.kk = (uint32_t)kk;
+  if (n <= kRowSelectMax) return launch_rowselect(scores, rows, n, m, k, sink, local, idx, st);
   const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
   const int64_t r_hi = topk_hi_rank(n, S, kk);
   rc = launch_sample_scores(scores, rows, n, S, sink, lstart, samp, samp_cap, st);

@@ -27,6 +27,12 @@ constexpr int64_t kMaxSample = 65536; // sampled keys per row (held in registers
 
 constexpr int64_t kAlpha = 4;  // expected first-pass candidates per row, in units of kk
 
+// Score rows up to this length (their 32-bit keys fit in one workgroup's LDS)
+// select their top kk in one kernel, one workgroup per row, instead of
+// sample -> select -> filter -> finalize: fewer launches for short rows.  The
+// fused scan + top-k keeps the chain (its first pass writes no scores).
+constexpr int64_t kRowSelectMax = 32768;
+
 struct TopkSel {
   uint32_t *thr;        // [rows] first-pass threshold key T_hi
   uint32_t *thr_lo;     // [rows] safe threshold key T_lo
@@ -90,6 +96,9 @@ int launch_filter_scores(const float *scores, int64_t rows, int64_t n, int64_t s
                          bool fallback, hipStream_t st);
 int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, TopkSel s, int64_t *idx,
                     hipStream_t st);
+// Exact top kk of whole score rows [rows, n] (n <= kRowSelectMax).
+int launch_rowselect(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+                     int64_t *idx, hipStream_t st);
 // kk == 0: only the sink and local positions are written.
 int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st);
 // Shape checks shared by the top-k entry points (FATHOM_OK or an error status).

@@ -204,8 +204,11 @@ def _topk_case(rows, k, sink, local, m=None):
 
 
 @pytest.mark.parametrize("n,k,sink,local", [(1000, 128, 4, 64), (16384, 128, 4, 64), (131072, 512, 4, 32),
-                                            (100000, 2048, 4, 32), (3000, 2048, 4, 32), (600, 40, 0, 0)])
+                                            (100000, 2048, 4, 32), (3000, 2048, 4, 32), (600, 40, 0, 0),
+                                            (32768, 512, 4, 32), (32769, 512, 4, 32), (32768, 2048, 0, 0)])
 def test_topk_random_bitexact(n, k, sink, local):
+    """Rows up to 32768 take the one-kernel row selection, longer rows the
+    sample / select / filter / finalize chain; both must equal the oracle."""
     print(f"[topk] n={n} k={k}", flush=True)
     rng = np.random.default_rng(n + k)
     rows = rng.standard_normal((2, 3, n)).astype(np.float32)
@@ -232,6 +235,7 @@ def test_topk_huge_tie_bucket_slow_path():
     rows = (1.0 + rng.integers(0, 50, size=(2, n)) * 1e-7).astype(np.float32)
     _topk_case(rows, 512, 4, 32)
     _topk_case(np.ones((1, 70000), np.float32), 300, 4, 32)
+    _topk_case(np.ones((2, 32768), np.float32), 300, 4, 32)  # one tie group, row-selection path
 
 
 @pytest.mark.parametrize("order", ["falling", "rising", "front_block"])
