@@ -44,6 +44,24 @@ __device__ float flog2(float x) {
   return (float)r;
 }
 
+// Exact wave sum / exclusive prefix sum of small non-negative integers (below
+// 2^BITS): bit-sliced with one ballot per bit, so no lane shuffles.
+template <int BITS>
+__device__ __forceinline__ int wave_sum_small(int v) {
+  int s = 0;
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) s += __popcll(__ballot((v >> b) & 1)) << b;
+  return s;
+}
+template <int BITS>
+__device__ __forceinline__ int wave_excl_scan_small(int v, int lane) {
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int s = 0;
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) s += __popcll(__ballot((v >> b) & 1) & lt) << b;
+  return s;
+}
+
 template <int CPL>
 __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, const float *__restrict__ budget, int D,
                                                   int bmax, int iters, int8_t *__restrict__ t_out,
@@ -61,14 +79,17 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
     // kernels/bitplane.py:89: lg = log2(max(g, 1e-30)); NaN g takes the 1e-30 floor.
     lg[k] = (j < D) ? flog2(fmaxf(g[bh * D + j], 1e-30f)) : -INFINITY;
   }
+  // depths are integers in [0, bmax]: a lane's sum is below 2^6, the row's
+  // (an exact integer) equals the float sum in any order
+  constexpr int kSumBits = CPL <= 1 ? 4 : CPL <= 2 ? 5 : 6;
   const float Br = budget[bh];
   float lo = -60.0f, hi = 60.0f;
   for (int it = 0; it < iters; ++it) {
     const float mid = (lo + hi) * 0.5f;
-    float s = 0.0f;
+    int s = 0;
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) s += fminf(fmaxf(rintf((lg[k] - mid) * 0.5f), 0.0f), bm);
-    const float tot = wave_sum_f(s);
+    for (int k = 0; k < CPL; ++k) s += (int)fminf(fmaxf(rintf((lg[k] - mid) * 0.5f), 0.0f), bm);
+    const float tot = (float)wave_sum_small<kSumBits>(s);
     if (tot > Br) lo = mid; else hi = mid;
   }
   int t[CPL];
@@ -81,10 +102,11 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
     cnt_act += t[k] > 0;
     cnt_pairs += t[k];
   }
+  constexpr int kCntBits = CPL <= 1 ? 1 : CPL <= 2 ? 2 : 3;  // per-lane channel counts <= CPL
   // active channels, ascending
   {
-    int pos = wave_excl_scan_i(cnt_act, lane);
-    const int total = wave_sum_i(cnt_act);
+    int pos = wave_excl_scan_small<kCntBits>(cnt_act, lane);
+    const int total = wave_sum_small<kCntBits>(cnt_act);
 #pragma unroll
     for (int k = 0; k < CPL; ++k)
       if (t[k] > 0) act[bh * D + pos++] = lane * CPL + k;
@@ -93,8 +115,8 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
   }
   // (channel, plane) pairs: channel-major, plane ascending
   {
-    int pos = wave_excl_scan_i(cnt_pairs, lane);
-    const int total = wave_sum_i(cnt_pairs);
+    int pos = wave_excl_scan_small<kSumBits>(cnt_pairs, lane);
+    const int total = wave_sum_small<kSumBits>(cnt_pairs);
     const int64_t base = bh * (int64_t)D * bmax;
 #pragma unroll
     for (int k = 0; k < CPL; ++k)
@@ -107,8 +129,8 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
     int cnt = 0;
 #pragma unroll
     for (int k = 0; k < CPL; ++k) cnt += t[k] == c;
-    int pos = wave_excl_scan_i(cnt, lane);
-    const int total = wave_sum_i(cnt);
+    int pos = wave_excl_scan_small<kCntBits>(cnt, lane);
+    const int total = wave_sum_small<kCntBits>(cnt);
     const int64_t base = (bh * bmax + (c - 1)) * (int64_t)D;
 #pragma unroll
     for (int k = 0; k < CPL; ++k)
