@@ -92,4 +92,22 @@ __device__ __forceinline__ int wave_excl_scan_i(int v, int lane) {
   return incl - v;
 }
 
+// Exact wave sum / exclusive prefix sum of small non-negative integers (below
+// 2^BITS): bit-sliced with one ballot per bit, so no lane shuffles.
+template <int BITS>
+__device__ __forceinline__ int wave_sum_small(int v) {
+  int s = 0;
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) s += __popcll(__ballot((v >> b) & 1)) << b;
+  return s;
+}
+template <int BITS>
+__device__ __forceinline__ int wave_excl_scan_small(int v, int lane) {
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int s = 0;
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) s += __popcll(__ballot((v >> b) & 1) & lt) << b;
+  return s;
+}
+
 }  // namespace fathom

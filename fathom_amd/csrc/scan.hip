@@ -51,6 +51,7 @@ static_assert(kTB * kBlk == kTileTok, "scan tile and top-k sample tile must agre
 constexpr int kThreads = 64 * kWaves;
 static_assert(2 * kWUnits == kWave, "two staging lanes per unit");
 static_assert(kGB == 8, "a wave stages two groups of four blocks");
+static_assert(kGB * kBlk == kRegTok, "a candidate region is one wave's blocks");
 
 enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2, kEmitFallback = 3 };
 
@@ -142,12 +143,6 @@ __device__ __forceinline__ void accum(Acc<G> &acc, int b, const QOp<G> &q, float
 // (compute_chunk below forms both from the octet-layout dwords.)
 
 // --------------------------------------------------------------------- emission
-template <int G>
-struct EmitShared {
-  uint32_t wcnt[G];   // candidates of the workgroup per head
-  uint32_t gbase[G];  // their first slot in the row's global list
-};
-
 // Threshold of a row as a float for "key >= thr": every element whose key is
 // >= thr has !(v < thr_f) (thr at or below -inf's key: everything passes; thr
 // in the NaN range: NaN and +inf pass -- extra candidates never change the
@@ -158,93 +153,53 @@ __device__ __forceinline__ float threshold_value(uint32_t thr) {
   return key_value(thr);
 }
 
-// Candidate emission of a wave's 8 blocks: count the passing tokens per head
-// (one compare + ballot per (block, head)), reserve the wave's slots with one
-// LDS atomic per head and the workgroup's with one global atomic per head,
-// then write each passing token's K64 straight to the row's list.
+// Candidate emission of a wave's 8 blocks into its region of each row's
+// candidate buffer (region gb0 / kGB: tokens [gb0 * kBlk, + kRegTok)): one
+// compare + ballot per (block, head) ranks the passing tokens, each writes its
+// K64 at its rank, and lane 0 writes the region's count.  The wave touches no
+// other wave's memory and no shared counter.  Heads in skipm emit nothing.
 template <int G>
-__device__ __forceinline__ void emit_filter(const Emit &em, EmitShared<G> &es, const Acc<G> &acc, int64_t bh,
-                                            int64_t gb0, int64_t blk0, int64_t blk_end, int64_t n, int lane) {
-  const int tid = threadIdx.x;
-  if (tid < G) es.wcnt[tid] = 0u;
+__device__ __forceinline__ void emit_filter(const Emit &em, const Acc<G> &acc, int64_t bh, int64_t gb0, int64_t blk0,
+                                            int64_t blk_end, int64_t n, int lane, uint32_t skipm) {
   const int64_t t0 = gb0 * kBlk, t1 = t0 + kGB * kBlk;
   // no per-lane validity or sink/local masking anywhere in the wave's blocks
   const bool plain = gb0 >= blk0 && gb0 + kGB <= blk_end && t1 <= n && t0 >= em.sink && t1 <= em.lstart;
-  // the pass's threshold per head; in the fallback pass, heads whose first pass
-  // found kk candidates emit nothing
-  float thr_f[G];
-  bool skip[G];
+  const uint32_t *const thr = em.fallback ? em.sel.thr_lo : em.sel.thr;
+  uint32_t *const rc = em.fallback ? em.sel.rc2 : em.sel.rc1;
+  const int64_t region = gb0 / kGB;
+  const uint64_t lt = (1ull << lane) - 1ull;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    skip[g] = em.fallback && ld_uniform(em.sel.cand_cnt + bh * G + g) >= em.sel.kk;
-    thr_f[g] = threshold_value(ld_uniform((em.fallback ? em.sel.thr_lo : em.sel.thr) + bh * G + g));
-  }
-  uint32_t *const gcnt = em.fallback ? em.sel.cand2_cnt : em.sel.cand_cnt;
-  auto masked_value = [&](int r, int g, bool &valid) -> float {
-    const float v = acc.get(r, g);
-    if (plain) {
-      valid = true;
-      return v;
-    }
-    const int64_t b = gb0 + r, tok = b * kBlk + lane;
-    valid = b >= blk0 && b < blk_end && tok < n;
-    return (tok < em.sink || tok >= em.lstart) ? -INFINITY : v;
-  };
-  uint32_t cnt[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    cnt[g] = 0u;
-    if (skip[g]) continue;
-#pragma unroll
-    for (int r = 0; r < kGB; ++r) {
-      bool valid;
-      const float vm = masked_value(r, g, valid);
-      cnt[g] += (uint32_t)__popcll(__ballot(valid && !(vm < thr_f[g])));
-    }
-  }
-  __syncthreads();  // counters cleared
-  uint32_t wbase[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    uint32_t o = 0u;
-    if (lane == 0 && cnt[g]) o = atomicAdd(&es.wcnt[g], cnt[g]);
-    wbase[g] = __builtin_amdgcn_readfirstlane(o);
-  }
-  __syncthreads();
-  if (tid < G) {
-    const uint32_t c = es.wcnt[tid];
-    es.gbase[tid] = c ? atomicAdd(&gcnt[bh * G + tid], c) : 0u;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (cnt[g] == 0u) continue;
+    if ((skipm >> g) & 1u) continue;
     const int64_t row = bh * G + g;
-    uint64_t *dst = em.sel.cand + row * em.sel.cand_cap;
-    uint64_t off = (uint64_t)es.gbase[g] + wbase[g];
+    const float thr_f = threshold_value(ld_uniform(thr + row));
+    uint64_t *dst = em.sel.cand + row * em.sel.cand_cap + t0;
+    uint32_t off = 0u;
 #pragma unroll
     for (int r = 0; r < kGB; ++r) {
-      bool valid;
-      const float vm = masked_value(r, g, valid);
-      const bool pass = valid && !(vm < thr_f[g]);
-      const uint64_t m = __ballot(pass);
-      if (m == 0ull) continue;
-      const uint64_t slot = off + (uint64_t)__popcll(m & ((1ull << lane) - 1ull));
-      if (pass && slot < (uint64_t)em.sel.cand_cap) {
-        const int64_t tok = (gb0 + r) * kBlk + lane;
-        dst[slot] = k64_of(vm == -INFINITY ? kKeyNegInf : score_key(vm), tok);
+      const float v = acc.get(r, g);
+      const int64_t tok = (gb0 + r) * kBlk + lane;
+      bool valid = true;
+      float vm = v;
+      if (!plain) {
+        valid = gb0 + r >= blk0 && gb0 + r < blk_end && tok < n;
+        vm = (tok < em.sink || tok >= em.lstart) ? -INFINITY : v;
       }
-      off += (uint64_t)__popcll(m);
+      const bool pass = valid && !(vm < thr_f);
+      const uint64_t m = __ballot(pass);
+      if (pass) dst[off + (uint32_t)__popcll(m & lt)] = k64_of(vm == -INFINITY ? kKeyNegInf : score_key(vm), tok);
+      off += (uint32_t)__popcll(m);
     }
+    if (lane == 0) rc[row * em.sel.nreg + region] = off;
   }
 }
 
 template <int G, int MODE>
-__device__ __forceinline__ void emit_group(const Emit &em, EmitShared<G> &es, const Acc<G> &acc, int64_t bh,
-                                           int64_t gb0, int64_t blk0, int64_t blk_end, int64_t n, int wave, int lane,
-                                           int64_t samp_tile) {
+__device__ __forceinline__ void emit_group(const Emit &em, const Acc<G> &acc, int64_t bh, int64_t gb0, int64_t blk0,
+                                           int64_t blk_end, int64_t n, int wave, int lane, int64_t samp_tile,
+                                           uint32_t skipm) {
   if (MODE == kEmitFilter) {
-    emit_filter<G>(em, es, acc, bh, gb0, blk0, blk_end, n, lane);
+    emit_filter<G>(em, acc, bh, gb0, blk0, blk_end, n, lane, skipm);
     return;
   }
 #pragma unroll
@@ -553,8 +508,8 @@ __device__ __forceinline__ void tile_prologue(TileShared<G> &sh, const ScanArgs 
 // One tile (list entry L of the launch) of a workgroup: the plan streams are in
 // LDS; each wave stages and computes its own 8 blocks, then emits them.
 template <int G, int MODE, bool FAST>
-__device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, TileShared<G> &sh, EmitShared<G> &es,
-                                         const PlanStreams &ps, int64_t L, int wave, int lane) {
+__device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, TileShared<G> &sh, const PlanStreams &ps,
+                                         int64_t L, int wave, int lane, uint32_t skipm) {
   const int64_t bh = blockIdx.y;
   const int64_t tb0 = (a.tile0 + L * a.tile_stride) * kTB;
   const int64_t gb0 = tb0 + wave * kGB;  // the wave's first block
@@ -605,7 +560,7 @@ __device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, Tile
       cur = nxt;
     }
   }
-  emit_group<G, MODE>(em, es, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, L);
+  emit_group<G, MODE>(em, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, L, skipm);
 }
 
 // One tile per workgroup (grid.x = list entries), except the fallback pass:
@@ -614,16 +569,31 @@ __device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, Tile
 template <int G, int MODE, bool FAST>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4 && MODE != kEmitFallback ? 5 : 4))) void scan_tile_kernel(ScanArgs a, Emit em) {
   __shared__ TileShared<G> sh;
-  __shared__ EmitShared<G> es;
+  __shared__ uint32_t s_tot[G];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
-  if (MODE == kEmitFallback) {  // uniform: skip the row unless one of its heads needs the pass
-    bool need = false;
+  uint32_t skipm = 0u;
+  if (MODE == kEmitFallback) {  // heads whose first pass found kk candidates skip the pass
+    if (tid < G) s_tot[tid] = 0u;
+    __syncthreads();
+    const int64_t nq = em.sel.nreg / 4;  // regions per row: a multiple of 4
 #pragma unroll
-    for (int g = 0; g < G; ++g) need |= ld_uniform(em.sel.cand_cnt + bh * G + g) < em.sel.kk;
-    if (!need) return;
+    for (int g = 0; g < G; ++g) {
+      const uint4 *rc = reinterpret_cast<const uint4 *>(em.sel.rc1 + (bh * G + g) * em.sel.nreg);
+      uint32_t part = 0u;
+      for (int64_t i = tid; i < nq; i += kThreads) {
+        const uint4 c = rc[i];
+        part += c.x + c.y + c.z + c.w;
+      }
+      part = (uint32_t)wave_sum_i((int)part);
+      if (lane == 0 && part) atomicAdd(&s_tot[g], part);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) skipm |= (s_tot[g] >= em.sel.kk ? 1u : 0u) << g;
+    if (skipm == (1u << G) - 1u) return;  // uniform
   }
   int nc[4];
 #pragma unroll
@@ -632,9 +602,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4
   tile_prologue<G>(sh, a, nc, ps, bh);
   __syncthreads();  // plan streams ready
   if (MODE == kEmitFallback) {
-    for (int64_t L = blockIdx.x; L < a.ntiles; L += gridDim.x) scan_one<G, kEmitFilter, FAST>(a, em, sh, es, ps, L, wave, lane);
+    for (int64_t L = blockIdx.x; L < a.ntiles; L += gridDim.x) scan_one<G, kEmitFilter, FAST>(a, em, sh, ps, L, wave, lane, skipm);
   } else {
-    scan_one<G, MODE, FAST>(a, em, sh, es, ps, blockIdx.x, wave, lane);
+    scan_one<G, MODE, FAST>(a, em, sh, ps, blockIdx.x, wave, lane, 0u);
   }
 }
 
@@ -749,7 +719,6 @@ template <int G>
 __global__ __launch_bounds__(kThreads) void scan_chan4_kernel(Chan4Args a, Emit em) {
   constexpr int QS = QShared<G>::QS;
   __shared__ C4Shared<G> sh;
-  __shared__ EmitShared<G> es;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
@@ -780,7 +749,7 @@ __global__ __launch_bounds__(kThreads) void scan_chan4_kernel(Chan4Args a, Emit 
       __syncthreads();
     }
   }
-  emit_group<G, kEmitScores>(em, es, acc, bh, tb0 + wave * kGB, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x);
+  emit_group<G, kEmitScores>(em, acc, bh, tb0 + wave * kGB, a.blk0, a.blk_end, a.n, wave, lane, blockIdx.x, 0u);
 }
 
 template <int G>
@@ -884,7 +853,7 @@ extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_
                                                    int64_t local) {
   const int64_t kk = k - sink - local;
   if (BH < 1 || G < 1 || n < 1 || kk < 0) return 0;
-  return topk_layout(BH * G, n, k, nullptr, nullptr, nullptr, nullptr, nullptr);
+  return topk_layout(BH * G, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
 
 extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
@@ -900,12 +869,12 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
   if (kk == 0) return launch_fixed_only(rows, m, k, sink, local, idx, st);
-  const size_t need = topk_layout(rows, n, k, nullptr, nullptr, nullptr, nullptr, nullptr);
+  const size_t need = topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "scan_topk: workspace %zu bytes, need %zu", workspace_bytes, need);
   Emit em{};
   int64_t S = 1;
-  topk_layout(rows, n, k, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
+  topk_layout(rows, n, k, true, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
   em.sel.kk = (uint32_t)kk;
   const int64_t nblk = cdiv(n, kBlk);
   ScanArgs a = make_args(q, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub);

@@ -44,38 +44,89 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Descending bitonic sort of the 64 values of a wave (one per lane), in
-// registers: 21 compare-exchange stages over lane shuffles.
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
-#pragma unroll
-  for (int kb = 2; kb <= 64; kb <<= 1) {
-#pragma unroll
-    for (int j = kb >> 1; j > 0; j >>= 1) {
-      const uint64_t w = shfl_xor_u64(v, j);
-      const bool keep_max = ((lane & j) == 0) == ((lane & kb) == 0);
-      v = keep_max ? (v > w ? v : w) : (v < w ? v : w);
+// The two values of lane pair {i & ~J, i | J} (in some order) for a compare-
+// exchange at distance J, on the VALU: DPP quad permutes (J = 1, 2), a quad
+// reversal then a half-row mirror (J = 4: i ^ 3 ^ 7), a row rotation by 8
+// (J = 8), and the gfx950 row swaps v_permlane16/32_swap (J = 16, 32: the
+// values of lanes i & ~J and i | J).
+template <int J>
+__device__ __forceinline__ void lane_pair(uint64_t v, uint64_t &x, uint64_t &y) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  uint32_t l0, l1, h0, h1;
+  if constexpr (J == 16 || J == 32) {
+    const auto pl = J == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                            : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto ph = J == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                            : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    l0 = pl[0];
+    l1 = pl[1];
+    h0 = ph[0];
+    h1 = ph[1];
+  } else {
+    l0 = lo;
+    h0 = hi;
+    if constexpr (J == 1) {
+      l1 = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+      h1 = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (J == 2) {
+      l1 = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+      h1 = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (J == 4) {  // quad_perm [3,2,1,0], then row_half_mirror
+      l1 = __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(lo, 0x1B, 0xF, 0xF, false), 0x141, 0xF, 0xF, false);
+      h1 = __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(hi, 0x1B, 0xF, 0xF, false), 0x141, 0xF, 0xF, false);
+    } else {
+      static_assert(J == 8, "compare-exchange distance");
+      l1 = __builtin_amdgcn_mov_dpp(lo, 0x128, 0xF, 0xF, false);  // row_ror:8
+      h1 = __builtin_amdgcn_mov_dpp(hi, 0x128, 0xF, 0xF, false);
     }
   }
+  x = ((uint64_t)h0 << 32) | l0;
+  y = ((uint64_t)h1 << 32) | l1;
+}
+
+template <int KB, int J>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t v, int lane) {
+  uint64_t x, y;
+  lane_pair<J>(v, x, y);
+  const bool keep_max = ((lane & J) == 0) == ((lane & KB) == 0);
+  const uint64_t mx = x > y ? x : y, mn = x > y ? y : x;
+  v = keep_max ? mx : mn;
+  if constexpr (J > 1) v = bitonic_merge<KB, J / 2>(v, lane);
   return v;
 }
 
-// Descending sort of E * 1024 values, thread t holding slots t + 1024 e (the
-// whole workgroup calls it): each wave sorts its 64-value runs in registers,
-// then log2(E * 1024 / 64) merge levels double the sorted runs in LDS.  At a
-// level an element's new place is its index in its own run plus the number of
-// elements of the partner run ahead of it (found by a binary search in the
-// partner run: strictly greater values for the left run, greater or equal for
-// the right one, so equal values keep run order and every place is distinct).
-// Only the first nlim slots (a power of two, 64 <= nlim <= E * 1024) are
-// merged: callers put every value that matters there.  a and b: LDS buffers of
-// E * 1024 values; returns the one holding the sorted first nlim slots.
-template <int E>
-__device__ uint64_t *block_sort_desc(uint64_t (&v)[E], uint64_t *a, uint64_t *b, int nlim) {
+// Descending bitonic sort of the 64 values of a wave (one per lane), in
+// registers: 21 compare-exchange stages of a few VALU instructions each.
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
+  v = bitonic_merge<2, 1>(v, lane);
+  v = bitonic_merge<4, 2>(v, lane);
+  v = bitonic_merge<8, 4>(v, lane);
+  v = bitonic_merge<16, 8>(v, lane);
+  v = bitonic_merge<32, 16>(v, lane);
+  v = bitonic_merge<64, 32>(v, lane);
+  return v;
+}
+
+// Descending ranks of the first nlim slots (a power of two, 64 <= nlim <= E *
+// 1024) of E * 1024 values, thread t holding slots t + 1024 e (the whole
+// workgroup calls it; slots from nlim on take no part).  Each wave sorts its
+// 64-value runs in registers; merge levels in LDS double the runs until at
+// most 8 remain; then a value's rank is the number of greater values over all
+// runs (binary searches), and put(rank, value) is called for every slot below
+// nlim.  Distinct values get distinct ranks; equal values share one.  a and b:
+// LDS buffers of nlim values.
+template <int E, typename Put>
+__device__ __forceinline__ void block_rank_desc(const uint64_t (&v)[E], uint64_t *a, uint64_t *b, int nlim, Put put) {
   const int t = threadIdx.x, lane = t & 63;
 #pragma unroll
-  for (int e = 0; e < E; ++e) a[t + 1024 * e] = wave_sort_desc(v[e], lane);
+  for (int e = 0; e < E; ++e)
+    if (t + 1024 * e < nlim) a[t + 1024 * e] = wave_sort_desc(v[e], lane);  // uniform per wave
   __syncthreads();
-  for (int w = kWave; w < nlim; w <<= 1) {
+  int w = kWave;
+  for (; nlim > 8 * w; w <<= 1) {
+    // merge: an element's new place is its index in its own run plus the
+    // partner run's elements ahead of it (strictly greater for the left run,
+    // greater or equal for the right one: equal values keep run order)
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = t + 1024 * e;
@@ -84,7 +135,7 @@ __device__ uint64_t *block_sort_desc(uint64_t (&v)[E], uint64_t *a, uint64_t *b,
       const int r = i / w, p = i - r * w;
       const bool left = (r & 1) == 0;
       const uint64_t *part = a + (r ^ 1) * w;
-      int c = 0;  // elements of the partner run placed ahead of x (a prefix of it)
+      int c = 0;
       for (int step = w; step > 0; step >>= 1) {
         if (c + step <= w) {
           const uint64_t y = part[c + step - 1];
@@ -98,24 +149,214 @@ __device__ uint64_t *block_sort_desc(uint64_t (&v)[E], uint64_t *a, uint64_t *b,
     a = b;
     b = tmp;
   }
-  return a;
+  const int nr = nlim / w;  // at most 8 runs
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = t + 1024 * e;
+    if (i >= nlim) continue;
+    const uint64_t x = a[i];
+    // greater values per run, by binary searches in all runs at once (eight
+    // independent LDS reads per step); x's own run counts the values before it
+    int c[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) c[q] = 0;
+    for (int step = w; step > 0; step >>= 1) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int j = min(c[q] + step, w) - 1;
+        const uint64_t y = a[(q < nr ? q * w : 0) + j];  // in bounds for every q
+        if (q < nr && c[q] + step <= w && y > x) c[q] += step;
+      }
+    }
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) rank += c[q];
+    put(rank, x);
+  }
 }
 
-// Smallest value >= lo of the need-th largest element among cnt values read
-// through get(i) (all threads of the workgroup call it).  Returns thr with
-// #{v >= thr} >= need, equality when the values are distinct; thr = 0 when
-// there are fewer than need values.
+// Value sources of the selections.  for_each(f) calls f(ok, v) for every value
+// v of the set, each thread of the workgroup for its share, in loops that are
+// uniform over the workgroup (all threads call it; f runs with every lane
+// active, v meaningful where ok).  The selections never depend on the order.
+struct ArraySrc {  // values p[0, cnt) (LDS or global memory)
+  const uint64_t *p;
+  int64_t cnt;
+  template <typename F>
+  __device__ __forceinline__ void for_each(F f) const {
+    for (int64_t i0 = 0; i0 < cnt; i0 += blockDim.x) {
+      const int64_t i = i0 + threadIdx.x;
+      const bool ok = i < cnt;
+      f(ok, ok ? p[i] : 0ull);
+    }
+  }
+};
+
 template <typename Get>
-__device__ uint64_t range_select(Get get, int64_t cnt, uint32_t need, RangeShared &sh) {
+struct IndexSrc {  // values get(0), ..., get(cnt - 1)
+  Get get;
+  int64_t cnt;
+  template <typename F>
+  __device__ __forceinline__ void for_each(F f) const {
+    for (int64_t i0 = 0; i0 < cnt; i0 += blockDim.x) {
+      const int64_t i = i0 + threadIdx.x;
+      const bool ok = i < cnt;
+      f(ok, ok ? get(i) : 0ull);
+    }
+  }
+};
+template <typename Get>
+__device__ __forceinline__ IndexSrc<Get> index_src(Get get, int64_t cnt) {
+  return IndexSrc<Get>{get, cnt};
+}
+
+// A row's candidates in the region layout: region r holds rc[r] values at
+// cand[r * kRegTok, ...).  Each wave takes batches of 64 regions (the next
+// batch's counts load while the current one is read); lane e of a step reads
+// the batch's e-th value, found by a binary search over the lanes' exclusive
+// prefix sums of the counts.
+struct RegionSrc {
+  const uint32_t *rc;
+  const uint64_t *cand;
+  int64_t nreg;
+  template <typename F>
+  __device__ __forceinline__ void for_each(F f) const {
+    const int lane = threadIdx.x & 63;
+    const int64_t step = (int64_t)(blockDim.x >> 6) * kWave;
+    int64_t r0 = (int64_t)(threadIdx.x >> 6) * kWave;
+    uint32_t c = r0 + lane < nreg ? min(rc[r0 + lane], (uint32_t)kRegTok) : 0u;
+    while (r0 < nreg) {  // uniform per wave
+      const int64_t r1 = r0 + step;
+      const uint32_t cn = r1 + lane < nreg ? min(rc[r1 + lane], (uint32_t)kRegTok) : 0u;
+      const uint32_t pre = (uint32_t)wave_excl_scan_small<10>((int)c, lane);  // counts <= 512
+      const uint32_t tot = (uint32_t)wave_sum_small<10>((int)c);
+      for (uint32_t e0 = 0; e0 < tot; e0 += kWave) {
+        const uint32_t e = e0 + lane;
+        int j = 0;  // the last lane whose prefix is <= e: its region holds value e
+#pragma unroll
+        for (int sft = 32; sft > 0; sft >>= 1)
+          if (__shfl(pre, j + sft, kWave) <= e) j += sft;
+        const uint32_t pj = __shfl(pre, j, kWave);
+        const bool ok = e < tot;
+        f(ok, ok ? cand[(r0 + j) * kRegTok + (e - pj)] : 0ull);
+      }
+      r0 = r1;
+      c = cn;
+    }
+  }
+};
+
+// Wave-aggregated append of the values whose ok holds to an LDS list (one LDS
+// atomic per wave); the counter keeps counting past cap, values past it are
+// dropped.  Call with every lane of the wave active.
+__device__ __forceinline__ void lds_append(bool ok, uint64_t v, uint32_t *cnt, uint64_t *buf, uint32_t cap, int lane) {
+  const uint64_t m = __ballot(ok);
+  if (m == 0ull) return;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  uint32_t base = 0u;
+  if (lane == leader) base = atomicAdd(cnt, (uint32_t)__popcll(m));
+  base = __shfl(base, leader, kWave);
+  const uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+  if (ok && slot < cap) buf[slot] = v;
+}
+
+// Copies a source's values to LDS (at most cap of them); returns how many the
+// source holds.  All threads call it; s_cnt is free again on return.
+template <typename Src>
+__device__ __forceinline__ uint32_t stage_lds(const Src &src, uint64_t *buf, uint32_t cap, uint32_t &s_cnt) {
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x == 0) s_cnt = 0u;
+  __syncthreads();
+  src.for_each([&](bool ok, uint64_t v) { lds_append(ok, v, &s_cnt, buf, cap, lane); });
+  __syncthreads();
+  const uint32_t tot = s_cnt;
+  __syncthreads();
+  return tot;
+}
+
+// Copies a row's candidates in the region layout to LDS (at most cap of them)
+// and returns how many it holds.  Per chunk of up to 4 * kFinThreads regions:
+// each thread loads 4 counts at once, a workgroup prefix sum turns them into
+// the regions' first slots (in pre: 4 * kFinThreads words of LDS), then value
+// e of the chunk is read by thread e mod kFinThreads after a binary search in
+// pre -- every load of a chunk is in flight at once, however unevenly the
+// candidates spread.  nreg: a multiple of 4.  All threads call it.
+__device__ __forceinline__ uint32_t stage_regions(const uint32_t *rc, const uint64_t *cand, int64_t nreg, uint64_t *buf, uint32_t cap,
+                                  uint32_t *pre, RangeShared &sh) {
+  constexpr int kR = 4 * kFinThreads;  // regions per chunk
+  constexpr int kU = 4;                // values per thread read together
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  uint32_t base = 0u;
+  for (int64_t c0 = 0; c0 < nreg; c0 += kR) {
+    const int nr = (int)min((int64_t)kR, nreg - c0);
+    uint4 c = make_uint4(0u, 0u, 0u, 0u);
+    if (4 * tid < nr) c = *reinterpret_cast<const uint4 *>(rc + c0 + 4 * tid);
+    c.x = min(c.x, (uint32_t)kRegTok);
+    c.y = min(c.y, (uint32_t)kRegTok);
+    c.z = min(c.z, (uint32_t)kRegTok);
+    c.w = min(c.w, (uint32_t)kRegTok);
+    const uint32_t t = c.x + c.y + c.z + c.w;
+    const uint32_t wx = (uint32_t)wave_excl_scan_i((int)t, lane);
+    if (lane == kWave - 1) sh.wsum[wave] = wx + t;
+    __syncthreads();
+    uint32_t off = wx, tot = 0u;
+    for (int w = 0; w < nw; ++w) {
+      const uint32_t ws = sh.wsum[w];
+      off += w < wave ? ws : 0u;
+      tot += ws;
+    }
+    if (4 * tid < nr) {
+      pre[4 * tid] = off;
+      pre[4 * tid + 1] = off + c.x;
+      pre[4 * tid + 2] = off + c.x + c.y;
+      pre[4 * tid + 3] = off + c.x + c.y + c.z;
+    }
+    __syncthreads();
+    for (uint32_t e0 = 0; e0 < tot; e0 += kU * kFinThreads) {
+      uint64_t v[kU];
+      uint32_t slot[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const uint32_t e = e0 + u * kFinThreads + tid;
+        slot[u] = ~0u;
+        v[u] = 0ull;
+        if (e < tot) {
+          int lo = 0, hi = nr - 1;  // the last region whose first slot is <= e
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pre[mid] <= e) lo = mid;
+            else hi = mid - 1;
+          }
+          v[u] = cand[(c0 + lo) * kRegTok + (e - pre[lo])];
+          slot[u] = base + e;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (slot[u] < cap) buf[slot[u]] = v[u];
+    }
+    base += tot;
+    __syncthreads();  // pre and wsum are rewritten by the next chunk
+  }
+  return base;
+}
+
+// Smallest value >= lo of the need-th largest element among the cnt values of
+// src (all threads of the workgroup call it).  Returns thr with #{v >= thr} >=
+// need, equality when the values are distinct; thr = 0 when there are fewer
+// than need values.
+template <typename Src>
+__device__ __forceinline__ uint64_t range_select(const Src &src, int64_t cnt, uint32_t need, RangeShared &sh) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   if (cnt < (int64_t)need || need == 0) return 0ull;
   // value range
   uint64_t mn = ~0ull, mx = 0ull;
-  for (int64_t i = tid; i < cnt; i += blockDim.x) {
-    const uint64_t v = get(i);
-    mn = v < mn ? v : mn;
-    mx = v > mx ? v : mx;
-  }
+  src.for_each([&](bool ok, uint64_t v) {
+    if (ok) {
+      mn = v < mn ? v : mn;
+      mx = v > mx ? v : mx;
+    }
+  });
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const uint64_t a = shfl_xor_u64(mn, o), b = shfl_xor_u64(mx, o);
@@ -149,10 +390,9 @@ __device__ uint64_t range_select(Get get, int64_t cnt, uint32_t need, RangeShare
     const int nb = (int)(R >> s) + 1;
     for (int b = tid; b < nb; b += blockDim.x) sh.hist[b] = 0u;
     __syncthreads();
-    for (int64_t i = tid; i < cnt; i += blockDim.x) {
-      const uint64_t v = get(i);
-      if (v >= lo && v <= hi) atomicAdd(&sh.hist[(v - lo) >> s], 1u);
-    }
+    src.for_each([&](bool ok, uint64_t v) {
+      if (ok && v >= lo && v <= hi) atomicAdd(&sh.hist[(v - lo) >> s], 1u);
+    });
     __syncthreads();
     // inclusive suffix sums over the bins (thread t owns bins 2t, 2t + 1)
     const int b0 = 2 * tid;
@@ -230,15 +470,19 @@ __device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t
 #pragma unroll
     for (int i = 0; i < M; ++i) vals[threadIdx.x + kSelThreads * i] = w[i];
     __syncthreads();
-    auto get = [&](int64_t i) { return vals[i]; };
-    const uint64_t lo = range_select(get, (int64_t)M * kSelThreads, kk, sh);
-    const uint64_t hi = r_hi < kk ? range_select(get, (int64_t)M * kSelThreads, r_hi, sh) : lo;
+    const ArraySrc src{vals, (int64_t)M * kSelThreads};
+    const uint64_t lo = range_select(src, src.cnt, kk, sh);
+    const uint64_t hi = r_hi < kk ? range_select(src, src.cnt, r_hi, sh) : lo;
     t_lo = (uint32_t)(lo >> 32);
     t_hi = (uint32_t)(hi >> 32);
-  } else {  // 1024 values: sort them and read the two ranks
-    const uint64_t *srt = block_sort_desc<M>(w, vals, vals + M * kSelThreads, M * kSelThreads);
-    t_lo = (uint32_t)(srt[kk - 1] >> 32);
-    t_hi = r_hi < kk ? (uint32_t)(srt[r_hi - 1] >> 32) : t_lo;
+  } else {  // 1024 values: rank them and keep the two ranks asked for
+    block_rank_desc<M>(w, vals, vals + M * kSelThreads, M * kSelThreads, [&](int rank, uint64_t x) {
+      if (rank == (int)kk - 1) sh.lo = x;
+      if (rank == (int)r_hi - 1) sh.hi = x;
+    });
+    __syncthreads();
+    t_lo = (uint32_t)(sh.lo >> 32);
+    t_hi = r_hi < kk ? (uint32_t)(sh.hi >> 32) : t_lo;
   }
 }
 
@@ -267,8 +511,8 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
   if (threadIdx.x == 0) {
     s.thr[row] = t_hi;
     s.thr_lo[row] = t_lo;
-    s.cand_cnt[row] = 0u;
-    s.cand2_cnt[row] = 0u;
+    *s.cnt1(row) = 0u;
+    *s.cnt2(row) = 0u;
   }
 }
 
@@ -295,10 +539,10 @@ __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const flo
   __shared__ uint32_t lcnt, lbase;
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t row = blockIdx.y;
-  if (fallback && s.cand_cnt[row] >= s.kk) return;  // the first pass holds the row's top kk
+  if (fallback && *s.cnt1(row) >= s.kk) return;  // the first pass holds the row's top kk
   const float *rs = scores + row * n;
   const uint32_t thr = fallback ? s.thr_lo[row] : s.thr[row];
-  uint32_t *cnt = fallback ? &s.cand2_cnt[row] : &s.cand_cnt[row];
+  uint32_t *cnt = fallback ? s.cnt2(row) : s.cnt1(row);
   uint64_t *cand = s.cand + row * s.cand_cap;
   if (tid == 0) lcnt = 0u;
   __syncthreads();
@@ -332,44 +576,36 @@ __global__ __launch_bounds__(kFilterThreads) void filter_scores_kernel(const flo
   flush_local(&lcnt, lbuf, kFilterLocal, cnt, cand, (uint64_t)s.cand_cap, &lbase);
 }
 
-// Exact top kk of a row's candidates, sorted by K64 descending (score
-// descending, index ascending), then the sink and local positions.
-// Exact top kk of cnt distinct K64 values read through get(i), sorted
-// descending, written to out, followed by the sink and local positions (the
-// whole workgroup calls it).  cl: LDS scratch of kCandLds values, which also
-// holds the values when cnt <= kCandLds and stage is set (get may read cl
-// only when stage is clear).
-template <typename Get>
-__device__ void select_sorted(Get get, int64_t cnt, int64_t kk, int64_t m, int64_t sink, int64_t local,
-                              int64_t *out, uint64_t *cl, uint64_t *ss, RangeShared &sh, uint32_t &s_cnt,
-                              bool stage = true) {
-  constexpr int kPer = kCandLds / kFinThreads;
-  const int tid = threadIdx.x;
-  const bool in_lds = stage && cnt <= kCandLds;
-  if (in_lds) {
-    uint64_t v[kPer];  // all loads in flight before the first store
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int64_t i = tid + (int64_t)u * kFinThreads;
-      v[u] = i < cnt ? get(i) : 0ull;
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int64_t i = tid + (int64_t)u * kFinThreads;
-      if (i < cnt) cl[i] = v[u];
-    }
-  }
-  if (tid == 0) s_cnt = 0u;
-  __syncthreads();
+// Writes the tail of a row's output: zeros after the got selected positions
+// (fewer candidates than kk), then the sink and local positions.
+__device__ __forceinline__ void write_fixed(int64_t *out, int got, int64_t kk, int64_t m, int64_t sink, int64_t local) {
+  for (int i = got + (int)threadIdx.x; i < (int)kk; i += kFinThreads) out[i] = 0;
+  for (int i = threadIdx.x; i < (int)(sink + local); i += kFinThreads)
+    out[kk + i] = (i < sink) ? (int64_t)i : (int64_t)(m - local + (i - sink));
+}
+
+// Exact top kk of the cnt distinct K64 values of src, sorted descending (score
+// descending, index ascending), written to out, followed by the sink and local
+// positions (the whole workgroup calls it).  cl: LDS scratch of kCandLds
+// values; with stage set and cnt <= kCandLds the values are copied there first
+// (src must not read cl then).
+template <typename Src>
+__device__ __forceinline__ void select_sorted(const Src &src, int64_t cnt, int64_t kk, int64_t m, int64_t sink,
+                                              int64_t local, int64_t *out, uint64_t *cl, uint64_t *ss,
+                                              RangeShared &sh, uint32_t &s_cnt, bool stage) {
+  const int tid = threadIdx.x, lane = tid & 63;
   // the exact kk largest first (range selection), then sorted
-  const uint64_t thr = in_lds ? range_select([&](int64_t i) { return cl[i]; }, cnt, (uint32_t)kk, sh)
-                              : range_select(get, cnt, (uint32_t)kk, sh);
-  for (int64_t i = tid; i < cnt; i += kFinThreads) {
-    const uint64_t v = in_lds ? cl[i] : get(i);
-    if (v >= thr) {
-      const uint32_t p = atomicAdd(&s_cnt, 1u);
-      if (p < (uint32_t)kMaxK) ss[p] = v;
-    }
+  auto survivors = [&](const auto &sr) {
+    const uint64_t thr = range_select(sr, cnt, (uint32_t)kk, sh);
+    if (tid == 0) s_cnt = 0u;
+    __syncthreads();
+    sr.for_each([&](bool ok, uint64_t v) { lds_append(ok && v >= thr, v, &s_cnt, ss, (uint32_t)kMaxK, lane); });
+  };
+  if (stage && cnt <= kCandLds) {
+    stage_lds(src, cl, (uint32_t)kCandLds, s_cnt);
+    survivors(ArraySrc{cl, cnt});
+  } else {
+    survivors(src);
   }
   __syncthreads();
   const int nv = (int)min(min(s_cnt, (uint32_t)kMaxK), (uint32_t)kk);
@@ -379,19 +615,19 @@ __device__ void select_sorted(Get get, int64_t cnt, int64_t kk, int64_t m, int64
   __syncthreads();  // cl is the sort scratch from here
   int nlim = kWave;
   while (nlim < nv) nlim <<= 1;  // the survivors fill the first nv <= 2048 slots
-  const uint64_t *srt = block_sort_desc<2>(v2, cl, cl + 2 * kFinThreads, nlim);
   const int got = nv < (int)kk ? nv : (int)kk;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int i = tid + e * kFinThreads;
-    if (i < got) out[i] = (int64_t)(0xFFFFFFFFu - (uint32_t)srt[i]);
-  }
-  for (int i = got + tid; i < (int)kk; i += kFinThreads) out[i] = 0;
-  for (int i = tid; i < (int)(sink + local); i += kFinThreads)
-    out[kk + i] = (i < sink) ? (int64_t)i : (int64_t)(m - local + (i - sink));
+  // the padding ranks at or after nv: only the survivors are written
+  block_rank_desc<2>(v2, cl, cl + 2 * kFinThreads, nlim, [&](int rank, uint64_t x) {
+    if (rank < got) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x);
+  });
+  write_fixed(out, got, kk, m, sink, local);
 }
 
-// Exact top kk of a row's candidates (the list of the pass in effect).
+// Exact top kk of a row's candidates: those of the first pass, or, where it
+// found fewer than kk, those of the fallback pass (which ran for exactly such
+// rows).  List layout: counts in the row counters.  Region layout: the first
+// pass's regions are copied to LDS while they are counted; a row with more
+// than kCandLds candidates is selected from its regions in place.
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_t k, int64_t sink, int64_t local,
                                                                TopkSel s, int64_t *__restrict__ idx) {
   __shared__ uint64_t cl[kCandLds];
@@ -399,11 +635,26 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   __shared__ RangeShared sh;
   __shared__ uint32_t s_cnt;
   const int64_t row = blockIdx.x;
-  const uint32_t c1 = s.cand_cnt[row];  // the fallback pass ran for rows whose first pass found < kk
-  const int64_t cnt = min((int64_t)(c1 >= s.kk ? c1 : s.cand2_cnt[row]), s.cand_cap);
+  const int64_t kk = k - sink - local;
   const uint64_t *gc = s.cand + row * s.cand_cap;
-  select_sorted([&](int64_t i) { return gc[i]; }, cnt, k - sink - local, m, sink, local, idx + row * k, cl, ss, sh,
-                s_cnt);
+  int64_t *out = idx + row * k;
+  if (s.rc1) {
+    uint32_t *pre = reinterpret_cast<uint32_t *>(ss);  // free until the survivors are collected
+    RegionSrc src{s.rc1 + row * s.nreg, gc, s.nreg};
+    uint32_t cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
+    if (cnt < s.kk) {
+      src.rc = s.rc2 + row * s.nreg;
+      cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
+    }
+    if (cnt <= (uint32_t)kCandLds)
+      select_sorted(ArraySrc{cl, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
+    else
+      select_sorted(src, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
+    return;
+  }
+  const uint32_t c1 = *s.cnt1(row);
+  const int64_t cnt = min((int64_t)(c1 >= s.kk ? c1 : *s.cnt2(row)), s.cand_cap);
+  select_sorted(ArraySrc{gc, cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, true);
 }
 
 // Exact top kk of a whole score row (rows up to kRowSelectMax): every element
@@ -425,11 +676,11 @@ __global__ __launch_bounds__(kFinThreads) void rowselect_kernel(const float *__r
     uint32_t *kl = reinterpret_cast<uint32_t *>(cl);
     for (int64_t i = threadIdx.x; i < n; i += kFinThreads) kl[i] = masked_key(rs, i, sink, lstart);
     __syncthreads();
-    select_sorted([&](int64_t i) { return ((uint64_t)kl[i] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i); }, n, kk,
-                  m, sink, local, idx + row * k, cl, ss, sh, s_cnt, false);
+    const auto src = index_src([&](int64_t i) { return ((uint64_t)kl[i] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i); }, n);
+    select_sorted(src, n, kk, m, sink, local, idx + row * k, cl, ss, sh, s_cnt, false);
   } else {
-    select_sorted([&](int64_t i) { return k64_of(masked_key(rs, i, sink, lstart), i); }, n, kk, m, sink, local,
-                  idx + row * k, cl, ss, sh, s_cnt);
+    const auto src = index_src([&](int64_t i) { return k64_of(masked_key(rs, i, sink, lstart), i); }, n);
+    select_sorted(src, n, kk, m, sink, local, idx + row * k, cl, ss, sh, s_cnt, true);
   }
 }
 
@@ -444,23 +695,29 @@ __global__ __launch_bounds__(256) void fixed_only_kernel(int64_t rows, int64_t m
 
 }  // namespace
 
-size_t topk_sel_layout(int64_t rows, int64_t cand_cap, char *base, TopkSel *s) {
-  const size_t row_b = ws_align((size_t)rows * 4);  // thr, thr_lo, cand_cnt, cand2_cnt
+size_t topk_sel_layout(int64_t rows, int64_t cand_cap, int64_t nreg, char *base, TopkSel *s) {
+  const size_t row_b = ws_align((size_t)rows * 4);                // thr, thr_lo
+  const size_t cnt_b = ws_align((size_t)rows * 4 * kCntStride);  // cand_cnt, cand2_cnt
+  const size_t reg_b = nreg > 0 ? ws_align((size_t)rows * (size_t)nreg * 4) : 0;  // rc1, rc2
   const size_t cand_b = ws_align((size_t)rows * (size_t)cand_cap * 8);
   if (s) {
-    s->thr = reinterpret_cast<uint32_t *>(base);
-    s->thr_lo = reinterpret_cast<uint32_t *>(base + row_b);
-    s->cand_cnt = reinterpret_cast<uint32_t *>(base + 2 * row_b);
-    s->cand2_cnt = reinterpret_cast<uint32_t *>(base + 3 * row_b);
-    s->cand = reinterpret_cast<uint64_t *>(base + 4 * row_b);
+    char *p = base;
+    s->thr = reinterpret_cast<uint32_t *>(p);
+    s->thr_lo = reinterpret_cast<uint32_t *>(p += row_b);
+    s->cand_cnt = reinterpret_cast<uint32_t *>(p += row_b);
+    s->cand2_cnt = reinterpret_cast<uint32_t *>(p += cnt_b);
+    s->rc1 = nreg > 0 ? reinterpret_cast<uint32_t *>(p + cnt_b) : nullptr;
+    s->rc2 = nreg > 0 ? reinterpret_cast<uint32_t *>(p + cnt_b + reg_b) : nullptr;
+    s->nreg = nreg > 0 ? nreg : 0;
+    s->cand = reinterpret_cast<uint64_t *>(p + cnt_b + 2 * reg_b);
     s->cand_cap = cand_cap;
     s->kk = 0u;
   }
-  return 4 * row_b + cand_b;
+  return 2 * row_b + 2 * cnt_b + 2 * reg_b + cand_b;
 }
 
-size_t topk_layout(int64_t rows, int64_t n, int64_t k, char *base, uint32_t **samp, int64_t *samp_cap, TopkSel *sel,
-                   int64_t *S_out) {
+size_t topk_layout(int64_t rows, int64_t n, int64_t k, bool regions, char *base, uint32_t **samp, int64_t *samp_cap,
+                   TopkSel *sel, int64_t *S_out) {
   const int64_t kk = k > 0 ? k : 0;
   const int64_t S = topk_tile_stride(n, kk);
   const int64_t cap = topk_sample_tiles(n, S) * kTileTok;
@@ -468,7 +725,8 @@ size_t topk_layout(int64_t rows, int64_t n, int64_t k, char *base, uint32_t **sa
   if (samp) *samp = reinterpret_cast<uint32_t *>(base);
   if (samp_cap) *samp_cap = cap;
   if (S_out) *S_out = S;
-  return samp_b + topk_sel_layout(rows, n, base ? base + samp_b : nullptr, sel);
+  const int64_t cand_cap = regions ? cdiv(n, kTileTok) * kTileTok : n;
+  return samp_b + topk_sel_layout(rows, cand_cap, regions ? cand_cap / kRegTok : 0, base ? base + samp_b : nullptr, sel);
 }
 
 int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, int64_t r_hi, TopkSel s,
@@ -533,7 +791,7 @@ using namespace fathom;
 
 extern "C" size_t fathom_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
   if (rows < 1 || n < 1 || k < 0) return 0;
-  return topk_layout(rows, n, k, nullptr, nullptr, nullptr, nullptr, nullptr);
+  return topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
 
 extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k,
@@ -545,13 +803,13 @@ extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
   if (kk == 0) return launch_fixed_only(rows, m, k, sink, local, idx, st);
-  const size_t need = topk_layout(rows, n, k, nullptr, nullptr, nullptr, nullptr, nullptr);
+  const size_t need = topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "sink_local_topk: workspace %zu bytes, need %zu", workspace_bytes, need);
   TopkSel s;
   uint32_t *samp = nullptr;
   int64_t samp_cap = 0, S = 1;
-  topk_layout(rows, n, k, static_cast<char *>(workspace), &samp, &samp_cap, &s, &S);
+  topk_layout(rows, n, k, false, static_cast<char *>(workspace), &samp, &samp_cap, &s, &S);
   s.kk = (uint32_t)kk;
   if (n <= kRowSelectMax) return launch_rowselect(scores, rows, n, m, k, sink, local, idx, st);
   const int64_t lstart = (m - local) > 0 ? (m - local) : 0;

@@ -7,22 +7,31 @@
 //             kAlpha * kk * (sample size / n).  A sample is a subset of the
 //             row, so T_lo never exceeds the row's kk-th largest key; T_hi is
 //             a guess that about kAlpha * kk elements of the row reach;
-//   filter    elements with key >= T_hi are appended to the row's candidate
-//             list.  If at least kk were appended, T_hi <= the row's kk-th
-//             largest key and the list holds the whole top kk;
+//   filter    elements with key >= T_hi become the row's candidates.  If there
+//             are at least kk, T_hi <= the row's kk-th largest key and they
+//             hold the whole top kk;
 //   fallback  rows with fewer than kk candidates (a sample that was not
-//             representative) are filtered again with T_lo, into the same list
-//             under a second counter; other rows skip the pass;
+//             representative) are filtered again with T_lo, into the same
+//             buffer under a second count; other rows skip the pass;
 //   finalize  one workgroup per row selects the exact kk largest candidates by
 //             K64 = key << 32 | (0xFFFFFFFF - index) and writes them sorted.
 // Exactness never depends on the sample: a poor sample only costs a fallback
-// pass or more candidates (the list holds a whole row, so it cannot overflow).
+// pass or more candidates (the buffer holds a whole row, so it cannot overflow).
+//
+// Candidates are kept in one of two layouts:
+//   list      (score-row filter) appended at a row counter: cand[0, count);
+//   regions   (fused scan) region r of a row holds the candidates of tokens
+//             [r * kRegTok, (r + 1) * kRegTok) -- one wave's blocks -- at
+//             cand[r * kRegTok, r * kRegTok + rc[r]), written with the count
+//             rc[r] by that wave alone: no atomics.  A pass writes every
+//             region of a row it does not skip.
 #pragma once
 #include "common.hpp"
 
 namespace fathom {
 
 constexpr int64_t kTileTok = 2048;  // tokens per scan tile (32 blocks)
+constexpr int64_t kRegTok = 512;    // tokens per candidate region (8 blocks: one wave of a scan tile)
 constexpr int64_t kMaxSample = 65536; // sampled keys per row (held in registers by select)
 
 constexpr int64_t kAlpha = 4;  // expected first-pass candidates per row, in units of kk
@@ -33,14 +42,23 @@ constexpr int64_t kAlpha = 4;  // expected first-pass candidates per row, in uni
 // fused scan + top-k keeps the chain (its first pass writes no scores).
 constexpr int64_t kRowSelectMax = 32768;
 
+// Candidate counters of a row, one per 256 bytes: every workgroup of a pass
+// adds to its row's counter, and atomics to one cache line serialise.
+constexpr int64_t kCntStride = 64;
+
 struct TopkSel {
   uint32_t *thr;        // [rows] first-pass threshold key T_hi
   uint32_t *thr_lo;     // [rows] safe threshold key T_lo
-  uint32_t *cand_cnt;   // [rows] candidates of the first pass
-  uint32_t *cand2_cnt;  // [rows] candidates of the fallback pass
+  uint32_t *cand_cnt;   // [rows * kCntStride] candidates of the first pass
+  uint32_t *cand2_cnt;  // [rows * kCntStride] candidates of the fallback pass
   uint64_t *cand;       // [rows, cand_cap] K64 candidates (of the pass in effect)
   int64_t cand_cap;
+  uint32_t *rc1;        // region layout: [rows, nreg] counts of the first pass (null: list layout)
+  uint32_t *rc2;        // region layout: [rows, nreg] counts of the fallback pass
+  int64_t nreg;         // regions per row (cand_cap / kRegTok)
   uint32_t kk;
+  __host__ __device__ uint32_t *cnt1(int64_t row) const { return cand_cnt + row * kCntStride; }
+  __host__ __device__ uint32_t *cnt2(int64_t row) const { return cand2_cnt + row * kCntStride; }
 };
 
 // Sample stride in tiles: about 8 sampled tiles per row, more where the sample
@@ -78,13 +96,15 @@ inline int64_t topk_hi_rank(int64_t n, int64_t S, int64_t kk) {
 inline size_t ws_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Layout of the selection state inside a workspace; returns bytes used.
-size_t topk_sel_layout(int64_t rows, int64_t cand_cap, char *base, TopkSel *s);
+// nreg > 0: region layout with nreg regions per row (cand_cap = nreg * kRegTok).
+size_t topk_sel_layout(int64_t rows, int64_t cand_cap, int64_t nreg, char *base, TopkSel *s);
 
-// Whole top-k workspace: sampled keys [rows, samp_cap] + selection state with a
-// candidate list of a full row.  S is sized for kk = k (an upper bound on
-// k - sink - local; a larger kk only means a denser sample).
-size_t topk_layout(int64_t rows, int64_t n, int64_t k, char *base, uint32_t **samp, int64_t *samp_cap, TopkSel *sel,
-                   int64_t *S_out);
+// Whole top-k workspace: sampled keys [rows, samp_cap] + selection state with
+// candidate room for a full row (regions: whole scan tiles, the list layout
+// otherwise).  S is sized for kk = k (an upper bound on k - sink - local; a
+// larger kk only means a denser sample).
+size_t topk_layout(int64_t rows, int64_t n, int64_t k, bool regions, char *base, uint32_t **samp, int64_t *samp_cap,
+                   TopkSel *sel, int64_t *S_out);
 
 // T_lo (rank kk) and T_hi (rank r_hi <= kk) of every row's sample; clears the counters.
 int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, int64_t r_hi, TopkSel s,
@@ -94,6 +114,7 @@ int launch_sample_scores(const float *scores, int64_t rows, int64_t n, int64_t S
 // First pass (fallback = false) or fallback pass (rows whose first pass found fewer than kk).
 int launch_filter_scores(const float *scores, int64_t rows, int64_t n, int64_t sink, int64_t lstart, TopkSel s,
                          bool fallback, hipStream_t st);
+// Either layout (s.rc1 set: regions).
 int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, TopkSel s, int64_t *idx,
                     hipStream_t st);
 // Exact top kk of whole score rows [rows, n] (n <= kRowSelectMax).

@@ -487,6 +487,24 @@ def test_scan_topk_fallback_pass(direction):
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("n", [70000, 16000])
+def test_scan_topk_all_ties(n):
+    """Every score equal (all-zero keys): every element reaches the threshold,
+    so a row has n candidates -- more than one workgroup's LDS holds at n =
+    70000, when the selection reads the candidate regions in place.  Ties go
+    to the lowest index."""
+    print(f"[fused-ties] n={n}", flush=True)
+    BH, d = 2, 128
+    st = bp.PlaneStore(torch.zeros(BH, n, d, device=DEV))
+    q = torch.randn(BH, 4, d, generator=torch.Generator().manual_seed(5)).to(DEV)
+    plan = bp.make_plan(torch.ones(BH, d, device=DEV), 12.0)
+    ref = bp.sink_local_topk(st.scan(q, plan), 512)
+    got = st.scan_topk(q, plan, 512)
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    expect = O.sink_local_topk(np.zeros((BH * 4, n), np.float32), 512).reshape(BH, 4, 512)
+    np.testing.assert_array_equal(got.cpu().numpy(), expect)
+
+
 def test_scan_topk_adversarial_order():
     """Scores rising along the sequence: the sampled threshold admits far more
     candidates than usual; the result stays exact."""
