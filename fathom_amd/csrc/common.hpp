@@ -92,6 +92,19 @@ __device__ __forceinline__ int wave_excl_scan_i(int v, int lane) {
   return incl - v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave on DPP: shifts by 1, 2, 4
+// and 8 within each row of 16 lanes, then the last lane of row 0 (2) added to
+// row 1 (3) and that of row 1 to rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 // Exact wave sum / exclusive prefix sum of small non-negative integers (below
 // 2^BITS): bit-sliced with one ballot per bit, so no lane shuffles.
 template <int BITS>

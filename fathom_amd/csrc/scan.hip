@@ -587,7 +587,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4
         const uint4 c = rc[i];
         part += c.x + c.y + c.z + c.w;
       }
-      part = (uint32_t)wave_sum_i((int)part);
+      part = __builtin_amdgcn_readlane(wave_incl_scan_u32(part), kWave - 1);
       if (lane == 0 && part) atomicAdd(&s_tot[g], part);
     }
     __syncthreads();

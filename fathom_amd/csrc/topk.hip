@@ -34,8 +34,9 @@ struct RangeShared {
   uint32_t hist[kBins];
   uint64_t wmin[kMaxWaves], wmax[kMaxWaves];
   uint32_t wsum[kMaxWaves];
+  uint64_t fin[kWave];  // the last few values of a range, selected by one wave
   uint64_t lo, hi, thr;
-  uint32_t need, done;
+  uint32_t need, done, hsel, fcnt;
 };
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
@@ -105,6 +106,25 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
   v = bitonic_merge<32, 16>(v, lane);
   v = bitonic_merge<64, 32>(v, lane);
   return v;
+}
+
+// Wave-wide minimum and maximum of 64-bit values (every lane gets both):
+// butterfly over the same lane pairs as the sort.
+template <int J>
+__device__ __forceinline__ void minmax_step(uint64_t &mn, uint64_t &mx) {
+  uint64_t a, b, c, d;
+  lane_pair<J>(mn, a, b);
+  lane_pair<J>(mx, c, d);
+  mn = a < b ? a : b;
+  mx = c > d ? c : d;
+}
+__device__ __forceinline__ void wave_minmax_u64(uint64_t &mn, uint64_t &mx) {
+  minmax_step<1>(mn, mx);
+  minmax_step<2>(mn, mx);
+  minmax_step<4>(mn, mx);
+  minmax_step<8>(mn, mx);
+  minmax_step<16>(mn, mx);
+  minmax_step<32>(mn, mx);
 }
 
 // Descending ranks of the first nlim slots (a power of two, 64 <= nlim <= E *
@@ -255,7 +275,7 @@ __device__ __forceinline__ void lds_append(bool ok, uint64_t v, uint32_t *cnt, u
   const int leader = __ffsll((unsigned long long)m) - 1;
   uint32_t base = 0u;
   if (lane == leader) base = atomicAdd(cnt, (uint32_t)__popcll(m));
-  base = __shfl(base, leader, kWave);
+  base = __builtin_amdgcn_readlane(base, leader);
   const uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
   if (ok && slot < cap) buf[slot] = v;
 }
@@ -296,8 +316,8 @@ __device__ __forceinline__ uint32_t stage_regions(const uint32_t *rc, const uint
     c.z = min(c.z, (uint32_t)kRegTok);
     c.w = min(c.w, (uint32_t)kRegTok);
     const uint32_t t = c.x + c.y + c.z + c.w;
-    const uint32_t wx = (uint32_t)wave_excl_scan_i((int)t, lane);
-    if (lane == kWave - 1) sh.wsum[wave] = wx + t;
+    const uint32_t wi = wave_incl_scan_u32(t), wx = wi - t;
+    if (lane == kWave - 1) sh.wsum[wave] = wi;
     __syncthreads();
     uint32_t off = wx, tot = 0u;
     for (int w = 0; w < nw; ++w) {
@@ -357,12 +377,7 @@ __device__ __forceinline__ uint64_t range_select(const Src &src, int64_t cnt, ui
       mx = v > mx ? v : mx;
     }
   });
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t a = shfl_xor_u64(mn, o), b = shfl_xor_u64(mx, o);
-    mn = a < mn ? a : mn;
-    mx = b > mx ? b : mx;
-  }
+  wave_minmax_u64(mn, mx);
   if (lane == 0) {
     sh.wmin[wave] = mn;
     sh.wmax[wave] = mx;
@@ -378,6 +393,7 @@ __device__ __forceinline__ uint64_t range_select(const Src &src, int64_t cnt, ui
     sh.hi = b;
     sh.need = need;
     sh.done = 0u;
+    sh.hsel = ~0u;
     sh.thr = a;
   }
   __syncthreads();
@@ -394,21 +410,17 @@ __device__ __forceinline__ uint64_t range_select(const Src &src, int64_t cnt, ui
       if (ok && v >= lo && v <= hi) atomicAdd(&sh.hist[(v - lo) >> s], 1u);
     });
     __syncthreads();
-    // inclusive suffix sums over the bins (thread t owns bins 2t, 2t + 1)
+    // values in the bins above each thread's pair (thread t owns bins 2t, 2t + 1)
     const int b0 = 2 * tid;
     const uint32_t h0 = b0 < nb ? sh.hist[b0] : 0u, h1 = b0 + 1 < nb ? sh.hist[b0 + 1] : 0u;
     const uint32_t x = h0 + h1;
-    uint32_t incl = x;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t v = __shfl_down(incl, o, kWave);
-      if (lane + o < 64) incl += v;
-    }
-    if (lane == 0) sh.wsum[wave] = incl;
+    const uint32_t incl = wave_incl_scan_u32(x);
+    const uint32_t wtot = __builtin_amdgcn_readlane(incl, kWave - 1);
+    if (lane == 0) sh.wsum[wave] = wtot;
     __syncthreads();
     uint32_t later = 0u;
     for (int w = wave + 1; w < nw; ++w) later += sh.wsum[w];
-    const uint32_t above = incl - x + later;  // values in bins above b0 + 1
+    const uint32_t above = wtot - incl + later;  // values in bins above b0 + 1
     int bsel = -1;
     uint32_t nsel = 0u, hsel = 0u;
     if (above < nd && above + h1 >= nd) {
@@ -428,10 +440,30 @@ __device__ __forceinline__ uint64_t range_select(const Src &src, int64_t cnt, ui
       sh.hi = (hi - nlo) > width ? nlo + width : hi;
       sh.need = nsel;
       sh.thr = nlo;
+      sh.hsel = hsel;
       sh.done = (hsel == nsel || s == 0) ? 1u : 0u;
     }
     __syncthreads();
     if (sh.done) break;
+    if (sh.hsel <= (uint32_t)kWave) {
+      // at most 64 values left in the range: gather them, one wave sorts them
+      // and the need-th largest is the threshold
+      const uint64_t flo = sh.lo, fhi = sh.hi;
+      const uint32_t fneed = sh.need;
+      if (tid == 0) sh.fcnt = 0u;
+      __syncthreads();
+      src.for_each([&](bool ok, uint64_t v) {
+        lds_append(ok && v >= flo && v <= fhi, v, &sh.fcnt, sh.fin, (uint32_t)kWave, lane);
+      });
+      __syncthreads();
+      if (wave == 0) {
+        const uint32_t fc = min(sh.fcnt, (uint32_t)kWave);
+        const uint64_t y = wave_sort_desc((uint32_t)lane < fc ? sh.fin[lane] : 0ull, lane);
+        if ((uint32_t)lane == fneed - 1u) sh.thr = y;
+      }
+      __syncthreads();
+      break;
+    }
   }
   return sh.thr;
 }

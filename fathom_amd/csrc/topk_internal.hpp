@@ -133,7 +133,7 @@ __device__ __forceinline__ void wave_append(bool pred, uint64_t val, uint32_t *c
   const int leader = __ffsll((unsigned long long)m) - 1;
   uint32_t base = 0;
   if (lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
-  base = __shfl(base, leader, kWave);
+  base = __builtin_amdgcn_readlane(base, leader);
   const uint64_t slot = (uint64_t)base + __popcll(m & ((1ull << lane) - 1ull));
   if (pred && slot < cap) buf[slot] = val;
 }
@@ -148,7 +148,7 @@ __device__ __forceinline__ void wave_append_local(bool pred, uint64_t val, uint3
   const int leader = __ffsll((unsigned long long)m) - 1;
   uint32_t base = 0;
   if (lane == leader) base = atomicAdd(lcnt, (uint32_t)__popcll(m));
-  base = __shfl(base, leader, kWave);
+  base = __builtin_amdgcn_readlane(base, leader);
   const uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
   if (pred) {
     if (slot < lcap) {
