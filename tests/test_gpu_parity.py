@@ -487,6 +487,26 @@ def test_scan_topk_fallback_pass(direction):
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
 
 
+def test_scan_topk_graph_replays():
+    """The fused call captured in a HIP graph (as bench.py times it): every replay,
+    with eager work and synchronisations between replays, equals the eager call."""
+    print("[fused-graph]", flush=True)
+    x, st, plan = _scan_case(2, 100000, 2)
+    q = x["q"].to(DEV)
+    ref = st.scan_topk(q, plan, 512, x["sink"], x["local"])
+    torch.cuda.synchronize()
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        got = st.scan_topk(q, plan, 512, x["sink"], x["local"])
+    for rep in range(4):
+        gph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, ref, rtol=0, atol=0, msg=f"replay {rep}")
+        eager = st.scan_topk(q, plan, 512, x["sink"], x["local"])  # eager work between replays
+        torch.cuda.synchronize()
+        torch.testing.assert_close(eager, ref, rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("n", [70000, 16000])
 def test_scan_topk_all_ties(n):
     """Every score equal (all-zero keys): every element reaches the threshold,
