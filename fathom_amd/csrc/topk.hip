@@ -39,12 +39,6 @@ struct RangeShared {
   uint32_t need, done, hsel, fcnt;
 };
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-  const uint32_t lo = __shfl_xor((uint32_t)v, o, kWave);
-  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, kWave);
-  return ((uint64_t)hi << 32) | lo;
-}
-
 // The two values of lane pair {i & ~J, i | J} (in some order) for a compare-
 // exchange at distance J, on the VALU: DPP quad permutes (J = 1, 2), a quad
 // reversal then a half-row mirror (J = 4: i ^ 3 ^ 7), a row rotation by 8
@@ -473,7 +467,8 @@ __device__ __forceinline__ uint32_t masked_key(const float *row, int64_t i, int6
 }
 
 // Thresholds of a row from its sampled keys: each thread keeps its M largest
-// keys (2 kk <= 1024 M); T_lo is the kk-th largest of those M * 1024 values.
+// keys (2 kk <= 1024 M); T_lo is the kk-th largest of those M * 1024 values
+// (for M = 1: of the maxima of P >= kk groups of them).
 // They are kk elements of the sample >= T_lo, so T_lo <= the sample's kk-th
 // largest <= the row's: every element of the row's top kk has key >= T_lo.
 // T_hi is the r_hi-th largest of the same values (r_hi <= kk, so T_hi >= T_lo).
@@ -507,8 +502,21 @@ __device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t
     const uint64_t hi = r_hi < kk ? range_select(src, src.cnt, r_hi, sh) : lo;
     t_lo = (uint32_t)(lo >> 32);
     t_hi = (uint32_t)(hi >> 32);
-  } else {  // 1024 values: rank them and keep the two ranks asked for
-    block_rank_desc<M>(w, vals, vals + M * kSelThreads, M * kSelThreads, [&](int rank, uint64_t x) {
+  } else {
+    // P = the smallest power of two >= max(kk, 64) values: the maxima of P
+    // disjoint groups of sampled keys (thread s < P combines the 1024 / P
+    // threads s, s + P, ...), ranked by one sort of P values.  They are
+    // distinct sample elements, so the kk-th largest is a valid T_lo.
+    int P = kWave;
+    while (P < (int)kk) P <<= 1;
+    uint32_t *mx = sh.hist;  // 1024 words, free here
+    mx[threadIdx.x] = top[0];
+    __syncthreads();
+    uint32_t g = 0u;
+    if ((int)threadIdx.x < P)
+      for (int j = threadIdx.x; j < kSelThreads; j += P) g = max(g, mx[j]);
+    const uint64_t wg[1] = {((uint64_t)g << 32) | (uint32_t)(threadIdx.x + 1)};
+    block_rank_desc<1>(wg, vals, vals + kSelThreads, P, [&](int rank, uint64_t x) {
       if (rank == (int)kk - 1) sh.lo = x;
       if (rank == (int)r_hi - 1) sh.hi = x;
     });
