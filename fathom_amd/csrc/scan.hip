@@ -849,11 +849,23 @@ extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t
   return launch_scan<kEmitScores>(a, G, tiles, BH, em, (hipStream_t)stream);
 }
 
+namespace fathom {
+namespace {
+// Workspace of the fused scan + top-k: rows up to kRowSelectMax keep their
+// scores ([rows, n] fp32) for one row-select launch; longer rows the sampled
+// keys and the candidate regions.
+size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k) {
+  if (n <= kRowSelectMax) return ws_align((size_t)rows * (size_t)n * 4);
+  return topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
+}
+}  // namespace
+}  // namespace fathom
+
 extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink,
                                                    int64_t local) {
   const int64_t kk = k - sink - local;
   if (BH < 1 || G < 1 || n < 1 || kk < 0) return 0;
-  return topk_layout(BH * G, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
+  return scan_topk_ws(BH * G, n, k);
 }
 
 extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
@@ -869,18 +881,27 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
   if (kk == 0) return launch_fixed_only(rows, m, k, sink, local, idx, st);
-  const size_t need = topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
+  const size_t need = scan_topk_ws(rows, n, k);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "scan_topk: workspace %zu bytes, need %zu", workspace_bytes, need);
-  Emit em{};
-  int64_t S = 1;
-  topk_layout(rows, n, k, true, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
-  em.sel.kk = (uint32_t)kk;
   const int64_t nblk = cdiv(n, kBlk);
   ScanArgs a = make_args(q, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub);
   a.blk0 = 0;
   a.blk_end = nblk;
   a.tile0 = 0;
+  if (n <= kRowSelectMax) {
+    // short rows: the scores in the workspace, then the whole rows selected
+    // in one launch (two kernels instead of the five of the chain below)
+    Emit es{};
+    es.out = static_cast<float *>(workspace);
+    rc = launch_scan<kEmitScores>(a, G, cdiv(nblk, kTB), BH, es, st);
+    if (rc) return rc;
+    return launch_rowselect(es.out, rows, n, m, k, sink, local, idx, st);
+  }
+  Emit em{};
+  int64_t S = 1;
+  topk_layout(rows, n, k, true, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
+  em.sel.kk = (uint32_t)kk;
   const int64_t r_hi = topk_hi_rank(n, S, kk);
   em.sink = sink;
   em.lstart = (m - local) > 0 ? (m - local) : 0;

@@ -698,30 +698,103 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
 }
 
 // Exact top kk of a whole score row (rows up to kRowSelectMax): every element
-// is a candidate.  Rows up to 2 * kCandLds keep their 32-bit keys in LDS (the
-// K64 of element i is rebuilt from its key and index); longer rows would be
-// read from global memory.
+// is a candidate.  Rows up to 2 * kCandLds keep their 32-bit keys in LDS (all
+// of a thread's loads in flight together; the K64 of element i is rebuilt from
+// its key and index).  For kk <= 1024 a prefilter keeps the selection small:
+// the maxima of P >= kk interleaved groups of keys are ranked, the kk-th of
+// them, T, bounds the row's kk-th largest key from below (kk elements reach
+// it), and only the keys >= T (a few per cent of a row) are selected from --
+// unless more than kMaxK reach it (ties, clustered rows), when the whole row
+// is.  Longer rows are read from global memory.
 __global__ __launch_bounds__(kFinThreads) void rowselect_kernel(const float *__restrict__ scores, int64_t n, int64_t m,
                                                                 int64_t k, int64_t sink, int64_t local,
                                                                 int64_t *__restrict__ idx) {
+  constexpr int kLoad = 2 * kCandLds / kFinThreads;  // keys per thread
   __shared__ uint64_t cl[kCandLds];
   __shared__ uint64_t ss[kMaxK];
   __shared__ RangeShared sh;
   __shared__ uint32_t s_cnt;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int64_t row = blockIdx.x;
   const float *rs = scores + row * n;
   const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
   const int64_t kk = k - sink - local;
-  if (n <= 2 * kCandLds) {
-    uint32_t *kl = reinterpret_cast<uint32_t *>(cl);
-    for (int64_t i = threadIdx.x; i < n; i += kFinThreads) kl[i] = masked_key(rs, i, sink, lstart);
-    __syncthreads();
-    const auto src = index_src([&](int64_t i) { return ((uint64_t)kl[i] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i); }, n);
-    select_sorted(src, n, kk, m, sink, local, idx + row * k, cl, ss, sh, s_cnt, false);
-  } else {
+  int64_t *out = idx + row * k;
+  if (n > 2 * kCandLds) {
     const auto src = index_src([&](int64_t i) { return k64_of(masked_key(rs, i, sink, lstart), i); }, n);
-    select_sorted(src, n, kk, m, sink, local, idx + row * k, cl, ss, sh, s_cnt, true);
+    select_sorted(src, n, kk, m, sink, local, out, cl, ss, sh, s_cnt, true);
+    return;
   }
+  uint32_t *kl = reinterpret_cast<uint32_t *>(cl);
+  uint32_t key[kLoad];  // the thread's keys t + 1024 u stay in registers
+  {
+    float v[kLoad];
+#pragma unroll
+    for (int u = 0; u < kLoad; ++u) {
+      const int64_t i = tid + (int64_t)u * kFinThreads;
+      v[u] = i < n ? rs[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kLoad; ++u) {
+      const int64_t i = tid + (int64_t)u * kFinThreads;
+      key[u] = i < n ? ((i < sink || i >= lstart) ? kKeyNegInf : score_key(v[u])) : 0u;
+      if (i < n) kl[i] = key[u];
+    }
+  }
+  __syncthreads();
+  auto whole = [&]() {
+    const auto src = index_src([&](int64_t i) { return ((uint64_t)kl[i] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i); }, n);
+    select_sorted(src, n, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
+  };
+  if (kk > kFinThreads || n <= kMaxK) {
+    whole();
+    return;
+  }
+  // group maxima: thread t covers keys t + 1024 u; group s < P combines the
+  // threads s, s + P, ... (keys i with i mod P == s); padding keys are 0
+  int P = kWave;
+  while (P < (int)kk) P <<= 1;
+  uint32_t mk = 0u;
+#pragma unroll
+  for (int u = 0; u < kLoad; ++u) mk = max(mk, key[u]);
+  sh.hist[tid] = mk;
+  __syncthreads();
+  uint32_t gm = 0u;
+  if (tid < P)
+    for (int j = tid; j < kFinThreads; j += P) gm = max(gm, sh.hist[j]);
+  const uint64_t wg[1] = {((uint64_t)gm << 32) | (uint32_t)(tid + 1)};
+  block_rank_desc<1>(wg, ss, ss + kFinThreads, P, [&](int rank, uint64_t x) {
+    if (rank == (int)kk - 1) sh.lo = x;
+  });
+  __syncthreads();
+  const uint32_t T = (uint32_t)(sh.lo >> 32);
+  // the keys >= T: counted per thread, a workgroup prefix sum places them
+  uint32_t c = 0u;
+#pragma unroll
+  for (int u = 0; u < kLoad; ++u) c += (tid + (int64_t)u * kFinThreads < n && key[u] >= T) ? 1u : 0u;
+  const int wave = tid >> 6, nw = kFinThreads >> 6;
+  const uint32_t wi = wave_incl_scan_u32(c);
+  if (lane == kWave - 1) sh.wsum[wave] = wi;
+  __syncthreads();
+  uint32_t off = wi - c, cnt = 0u;
+  for (int w = 0; w < nw; ++w) {
+    const uint32_t ws = sh.wsum[w];
+    off += w < wave ? ws : 0u;
+    cnt += ws;
+  }
+  if (cnt > (uint32_t)kMaxK) {  // uniform
+    whole();
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < kLoad; ++u) {
+    const int64_t i = tid + (int64_t)u * kFinThreads;
+    if (i < n && key[u] >= T) ss[off++] = ((uint64_t)key[u] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+  }
+  __syncthreads();
+  // the candidates are in ss and the keys are no longer needed: survivors go to
+  // cl, the sort works in cl + 2 * kMaxK
+  select_sorted(ArraySrc{ss, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl + 2 * kMaxK, cl, sh, s_cnt, false);
 }
 
 __global__ __launch_bounds__(256) void fixed_only_kernel(int64_t rows, int64_t m, int64_t k, int64_t sink,

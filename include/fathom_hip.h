@@ -153,10 +153,11 @@ int fathom_klt_query(const float *q, const float *Vt, const float *lam, int64_t 
  * fathom_sink_local_topk on its scores (kernels/bitplane.py:319-338 then
  * :372-378, as chained by scripts/B_kernel_bench.py:74 and
  * scripts/B_e2e_offload_v2.py:203, 224-227), without materialising the score
- * tensor.  Same arguments as fathom_scan_planes over the whole sequence, plus
- * the top-k arguments of fathom_sink_local_topk; idx [BH * G, k] int64 is
- * identical to running the two entry points.  workspace:
- * fathom_scan_topk_workspace_bytes(BH, G, n, k, sink, local) bytes.
+ * tensor for rows longer than 32768 (shorter rows keep their scores in the
+ * workspace for one selection launch).  Same arguments as fathom_scan_planes
+ * over the whole sequence, plus the top-k arguments of fathom_sink_local_topk;
+ * idx [BH * G, k] int64 is identical to running the two entry points.
+ * workspace: fathom_scan_topk_workspace_bytes(BH, G, n, k, sink, local) bytes.
  */
 size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink, int64_t local);
 int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn,
