@@ -53,6 +53,20 @@ static_assert(2 * kWUnits == kWave, "two staging lanes per unit");
 static_assert(kGB == 8, "a wave stages two groups of four blocks");
 static_assert(kGB * kBlk == kRegTok, "a candidate region is one wave's blocks");
 
+// Tile geometry by NG, the block groups of four a wave computes: NG = 2 (8
+// blocks per wave, 4 waves per tile, two staging lanes per unit) everywhere but
+// the sample pass, which is latency-bound (a few workgroups per row) and uses
+// NG = 1 (4 blocks per wave, 8 waves per tile, one lane per unit): half a
+// wave's work per tile, the same scores bit for bit.
+template <int NG>
+struct Geo {
+  static constexpr int GB = 4 * NG;          // blocks per wave
+  static constexpr int WAVES = kTB / GB;     // waves per tile
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int WUNITS = kWave / NG;  // units per wave chunk
+};
+static_assert(Geo<2>::GB == kGB && Geo<2>::THREADS == kThreads && Geo<2>::WUNITS == kWUnits, "NG = 2 is the tile");
+
 enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2, kEmitFallback = 3 };
 
 struct Emit {
@@ -114,21 +128,21 @@ __device__ __forceinline__ QOp<G> load_qop(const QShared<G> &qs, int j, int lane
 
 // Four fp32 accumulators per lane and head quad: component h of v[b][hq] is the
 // score of head 4*hq + h for the lane's token of block b.
-template <int G>
+template <int G, int GB = kGB>
 struct Acc {
   static constexpr int NQ = (G + 3) / 4;
-  f32x4 v[kGB][NQ];
+  f32x4 v[GB][NQ];
   __device__ __forceinline__ void zero() {
 #pragma unroll
-    for (int b = 0; b < kGB; ++b)
+    for (int b = 0; b < GB; ++b)
 #pragma unroll
       for (int h = 0; h < NQ; ++h) v[b][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   __device__ __forceinline__ float get(int b, int g) const { return v[b][g >> 2][g & 3]; }
 };
 
-template <int G>
-__device__ __forceinline__ void accum(Acc<G> &acc, int b, const QOp<G> &q, float y) {
+template <int G, int GB>
+__device__ __forceinline__ void accum(Acc<G, GB> &acc, int b, const QOp<G> &q, float y) {
 #pragma unroll
   for (int h = 0; h < QOp<G>::NQ; ++h) acc.v[b][h] = __builtin_amdgcn_mfma_f32_4x4x1f32(q.a[h], y, acc.v[b][h], 0, 0, 0);
 }
@@ -194,16 +208,17 @@ __device__ __forceinline__ void emit_filter(const Emit &em, const Acc<G> &acc, i
   }
 }
 
-template <int G, int MODE>
-__device__ __forceinline__ void emit_group(const Emit &em, const Acc<G> &acc, int64_t bh, int64_t gb0, int64_t blk0,
+template <int G, int MODE, int GB = kGB>
+__device__ __forceinline__ void emit_group(const Emit &em, const Acc<G, GB> &acc, int64_t bh, int64_t gb0, int64_t blk0,
                                            int64_t blk_end, int64_t n, int wave, int lane, int64_t samp_tile,
                                            uint32_t skipm) {
-  if (MODE == kEmitFilter) {
+  if constexpr (MODE == kEmitFilter) {
+    static_assert(GB == kGB, "candidate regions are 8-block waves");
     emit_filter<G>(em, acc, bh, gb0, blk0, blk_end, n, lane, skipm);
     return;
   }
 #pragma unroll
-  for (int r = 0; r < kGB; ++r) {
+  for (int r = 0; r < GB; ++r) {
     const int64_t b = gb0 + r;
     const int64_t tok = b * kBlk + lane;
     const bool valid = b >= blk0 && b < blk_end && tok < n;
@@ -216,7 +231,7 @@ __device__ __forceinline__ void emit_group(const Emit &em, const Acc<G> &acc, in
       } else {
         const bool masked = tok < em.sink || tok >= em.lstart;
         const uint32_t key = valid ? (masked ? kKeyNegInf : score_key(v)) : 0u;
-        em.samp[row * em.samp_cap + samp_tile * kTileTok + (wave * kGB + r) * kBlk + lane] = key;
+        em.samp[row * em.samp_cap + samp_tile * kTileTok + (wave * GB + r) * kBlk + lane] = key;
       }
     }
   }
@@ -251,6 +266,7 @@ struct Chunk {
 };
 
 // The chunk starting at slot s (s < SF[3]).
+template <int WU = kWUnits>
 __device__ __forceinline__ Chunk chunk_from(const PlanStreams &ps, int s) {
   Chunk ck;
   ck.s0 = s;
@@ -261,7 +277,7 @@ __device__ __forceinline__ Chunk chunk_from(const PlanStreams &ps, int s) {
     const int lo = c ? ps.SF[c - 1] : 0;
     if (open && s < ps.SF[c]) {
       if (u0 < 0) u0 = (c ? ps.UE[c - 1] : 0) + (s - lo) * (c + 1);
-      const int take = min(ps.SF[c] - s, (kWUnits - used) / (c + 1));
+      const int take = min(ps.SF[c] - s, (WU - used) / (c + 1));
       used += take * (c + 1);
       s += take;
       if (s < ps.SF[c]) open = false;
@@ -283,18 +299,19 @@ __device__ __forceinline__ Chunk chunk_from(const PlanStreams &ps, int s) {
 // positions, OR-ing them and one rotation right by t leave the lane's C-bit
 // code of block k in byte k.  P, Q: the scale pair of each channel slot and
 // block (see lane_value).
+template <int NG = 2>
 struct WaveBuf {
-  alignas(16) uint32_t oct[kWUnits][2][8];
-  alignas(16) float P[kWUnits][kGB];
-  alignas(16) float Q[kWUnits][kGB];
+  alignas(16) uint32_t oct[Geo<NG>::WUNITS][NG][8];
+  alignas(16) float P[Geo<NG>::WUNITS][Geo<NG>::GB];
+  alignas(16) float Q[Geo<NG>::WUNITS][Geo<NG>::GB];
 };
 
-template <int G>
+template <int G, int NG = 2>
 struct TileShared {
   alignas(16) float w[kMaxD][QShared<G>::QS];  // head weights by plan slot
   uint16_t unit[4 * kMaxD];                    // plan unit -> (j * 4 + p) << 2 | (C - 1 - p)
   uint16_t slot[kMaxD];                        // plan slot -> j | class << 8
-  WaveBuf wb[kWaves];
+  WaveBuf<NG> wb[Geo<NG>::WAVES];
 };
 
 // What a lane loads for one chunk: the four plane words of its (unit, group)
@@ -325,10 +342,10 @@ __device__ __forceinline__ void group_base(const ScanArgs &a, int64_t bh, int64_
 
 // Issues the global loads of chunk ck: lane l stages unit l >> 1 for block
 // group l & 1 and the scales of channel slot l & 31 for group l >> 5.
-template <int G, bool FAST>
-__device__ __forceinline__ void stage_load(Staged &r, const ScanArgs &a, const TileShared<G> &sh, const Chunk &ck,
+template <int G, bool FAST, int NG = 2>
+__device__ __forceinline__ void stage_load(Staged &r, const ScanArgs &a, const TileShared<G, NG> &sh, const Chunk &ck,
                                            const LaneAddr &la, int64_t gb0, int64_t bh, int lane) {
-  const int u = ck.u0 + (lane >> 1), g = lane & 1;
+  const int u = ck.u0 + (NG == 2 ? lane >> 1 : lane), g = NG == 2 ? lane & 1 : 0;
 #pragma unroll
   for (int k = 0; k < 4; ++k) r.w[k] = 0ull;
   r.rot = 0u;
@@ -357,7 +374,7 @@ __device__ __forceinline__ void stage_load(Staged &r, const ScanArgs &a, const T
       }
     }
   }
-  const int cs = ck.s0 + (lane & 31), gs = lane >> 5;
+  const int cs = ck.s0 + (NG == 2 ? lane & 31 : lane), gs = NG == 2 ? lane >> 5 : 0;
   r.s[0] = r.s[1] = 0u;
   r.scls = 0;
   if (cs < ck.s1) {
@@ -390,8 +407,9 @@ __device__ __forceinline__ void stage_load(Staged &r, const ScanArgs &a, const T
 // Writes a loaded chunk to the wave's buffer: plane words as octet dwords
 // (two 4 x 4 byte transposes per lane, rotated for the unit's plane) and the
 // scale pairs.
-__device__ __forceinline__ void stage_store(WaveBuf &wb, const Staged &r, const Chunk &ck, int lane) {
-  const int u = lane >> 1, g = lane & 1;
+template <int NG = 2>
+__device__ __forceinline__ void stage_store(WaveBuf<NG> &wb, const Staged &r, const Chunk &ck, int lane) {
+  const int u = NG == 2 ? lane >> 1 : lane, g = NG == 2 ? lane & 1 : 0;
   if (ck.u0 + u < ck.u1) {
     uint32_t out[8];
 #pragma unroll
@@ -413,7 +431,7 @@ __device__ __forceinline__ void stage_store(WaveBuf &wb, const Staged &r, const 
     dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
     dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
   }
-  const int cs = lane & 31, gs = lane >> 5;
+  const int cs = NG == 2 ? lane & 31 : lane, gs = NG == 2 ? lane >> 5 : 0;
   if (ck.s0 + cs < ck.s1) {
     float P[4], Q[4];
 #pragma unroll
@@ -440,9 +458,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // start at chunk unit u0; w: the head weights of those slots.  In slot order,
 // four blocks per group: one dword read per (plane, group) brings the lane's
 // bits of the group's four blocks, two 16-byte reads the scale pairs.
-template <int C, int G>
-__device__ __forceinline__ void compute_slots(const WaveBuf &wb, const float (*w)[QShared<G>::QS], int s0, int s1,
-                                              int u0, int lane, uint32_t sign, Acc<G> &acc) {
+template <int C, int G, int NG = 2>
+__device__ __forceinline__ void compute_slots(const WaveBuf<NG> &wb, const float (*w)[QShared<G>::QS], int s0, int s1,
+                                              int u0, int lane, uint32_t sign, Acc<G, Geo<NG>::GB> &acc) {
   const int o = lane >> 3, t = lane & 7;
   // depth 1: the shift bringing block k's bit to bit 31; deeper: plane p's mask
   uint32_t sh[4], mk[C];
@@ -451,19 +469,19 @@ __device__ __forceinline__ void compute_slots(const WaveBuf &wb, const float (*w
 #pragma unroll
   for (int p = 0; p < C; ++p) mk[p] = 0x01010101u << ((t + C - 1 - p) & 7);
   const uint32_t *ob = &wb.oct[u0][0][o];
-  for (int ci = s0; ci < s1; ++ci, ob += C * 16) {
+  for (int ci = s0; ci < s1; ++ci, ob += C * NG * 8) {
     QOp<G> q;
 #pragma unroll
     for (int h = 0; h < QOp<G>::NQ; ++h) q.a[h] = w[ci][4 * h + (lane & 3)];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
+    for (int g = 0; g < NG; ++g) {
       const float4 P4 = *reinterpret_cast<const float4 *>(&wb.P[ci][4 * g]);
       float4 Q4 = make_float4(0.f, 0.f, 0.f, 0.f);
       if (C > 1) Q4 = *reinterpret_cast<const float4 *>(&wb.Q[ci][4 * g]);
       const float P[4] = {P4.x, P4.y, P4.z, P4.w}, Q[4] = {Q4.x, Q4.y, Q4.z, Q4.w};
       uint32_t d[C];
 #pragma unroll
-      for (int p = 0; p < C; ++p) d[p] = ob[p * 16 + g * 8];
+      for (int p = 0; p < C; ++p) d[p] = ob[p * NG * 8 + g * 8];
       float y[4];
       if (C == 1) {
 #pragma unroll
@@ -485,11 +503,11 @@ __device__ __forceinline__ void compute_slots(const WaveBuf &wb, const float (*w
 // Workgroup prologue: the plan streams in LDS -- per slot its channel and
 // class and the head weights (w = -q at depth 1, q * 2^-C deeper: exact
 // power-of-two scalings), per unit its plane word index and rotation.
-template <int G>
-__device__ __forceinline__ void tile_prologue(TileShared<G> &sh, const ScanArgs &a, const int (&nc)[4],
+template <int G, int NG = 2>
+__device__ __forceinline__ void tile_prologue(TileShared<G, NG> &sh, const ScanArgs &a, const int (&nc)[4],
                                               const PlanStreams &ps, int64_t bh) {
   constexpr int QS = QShared<G>::QS;
-  for (int e = threadIdx.x; e < ps.SF[3]; e += kThreads) {
+  for (int e = threadIdx.x; e < ps.SF[3]; e += Geo<NG>::THREADS) {
     const int c = (e >= ps.SF[0]) + (e >= ps.SF[1]) + (e >= ps.SF[2]);
     const int lo = c == 0 ? 0 : c == 1 ? ps.SF[0] : c == 2 ? ps.SF[1] : ps.SF[2];
     const int ub = (c == 0 ? 0 : c == 1 ? ps.UE[0] : c == 2 ? ps.UE[1] : ps.UE[2]) + (e - lo) * (c + 1);
@@ -507,42 +525,43 @@ __device__ __forceinline__ void tile_prologue(TileShared<G> &sh, const ScanArgs 
 
 // One tile (list entry L of the launch) of a workgroup: the plan streams are in
 // LDS; each wave stages and computes its own 8 blocks, then emits them.
-template <int G, int MODE, bool FAST>
-__device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, TileShared<G> &sh, const PlanStreams &ps,
-                                         int64_t L, int wave, int lane, uint32_t skipm) {
+template <int G, int MODE, bool FAST, int NG = 2>
+__device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, TileShared<G, NG> &sh,
+                                         const PlanStreams &ps, int64_t L, int wave, int lane, uint32_t skipm) {
+  constexpr int GB = Geo<NG>::GB;
   const int64_t bh = blockIdx.y;
   const int64_t tb0 = (a.tile0 + L * a.tile_stride) * kTB;
-  const int64_t gb0 = tb0 + wave * kGB;  // the wave's first block
+  const int64_t gb0 = tb0 + wave * GB;  // the wave's first block
   LaneAddr la{0, 0, false, false};
   {
-    const int64_t pblk = gb0 + 4 * (lane & 1), sblk = gb0 + 4 * (lane >> 5);
+    const int64_t pblk = gb0 + (NG == 2 ? 4 * (lane & 1) : 0), sblk = gb0 + (NG == 2 ? 4 * (lane >> 5) : 0);
     int64_t unused;
     la.pin = pblk < a.nsb * a.sub;
     la.sin = sblk < a.nsb * a.sub;
     if (la.pin) group_base(a, bh, pblk, la.pbase, unused);
     if (la.sin) group_base(a, bh, sblk, unused, la.sbase);
   }
-  Acc<G> acc;
+  Acc<G, GB> acc;
   acc.zero();
-  WaveBuf &wb = sh.wb[wave];
+  WaveBuf<NG> &wb = sh.wb[wave];
   if (tb0 < a.blk_end && tb0 + kTB > a.blk0 && ps.SF[3] > 0) {  // uniform over the workgroup
     Staged r;
     // the sign-bit mask as an opaque VGPR value (VOP3 encodings take no literal)
     uint32_t sign;
     asm("v_mov_b32 %0, 0x80000000" : "=v"(sign));
-    Chunk cur = chunk_from(ps, 0);
-    stage_load<G, FAST>(r, a, sh, cur, la, gb0, bh, lane);
+    Chunk cur = chunk_from<Geo<NG>::WUNITS>(ps, 0);
+    stage_load<G, FAST, NG>(r, a, sh, cur, la, gb0, bh, lane);
     // chunks in plan order; the next chunk is loaded while the current one is
     // computed.  Waves run independently: each stages and computes its own blocks.
     while (true) {
       wave_lds_sync();  // the previous chunk's reads are done
-      stage_store(wb, r, cur, lane);
+      stage_store<NG>(wb, r, cur, lane);
       wave_lds_sync();
       const bool more = cur.s1 < ps.SF[3];
       Chunk nxt = cur;
       if (more) {
-        nxt = chunk_from(ps, cur.s1);
-        stage_load<G, FAST>(r, a, sh, nxt, la, gb0, bh, lane);
+        nxt = chunk_from<Geo<NG>::WUNITS>(ps, cur.s1);
+        stage_load<G, FAST, NG>(r, a, sh, nxt, la, gb0, bh, lane);
       }
       const float (*w)[QShared<G>::QS] = sh.w + cur.s0;
 #pragma unroll
@@ -550,25 +569,25 @@ __device__ __forceinline__ void scan_one(const ScanArgs &a, const Emit &em, Tile
         const int lo = max(cur.s0, c ? ps.SF[c - 1] : 0), hi = min(cur.s1, ps.SF[c]);
         if (lo < hi) {
           const int ul = (c ? ps.UE[c - 1] : 0) + (lo - (c ? ps.SF[c - 1] : 0)) * (c + 1) - cur.u0;
-          if (c == 0) compute_slots<1, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
-          if (c == 1) compute_slots<2, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
-          if (c == 2) compute_slots<3, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
-          if (c == 3) compute_slots<4, G>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+          if (c == 0) compute_slots<1, G, NG>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+          if (c == 1) compute_slots<2, G, NG>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+          if (c == 2) compute_slots<3, G, NG>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
+          if (c == 3) compute_slots<4, G, NG>(wb, w, lo - cur.s0, hi - cur.s0, ul, lane, sign, acc);
         }
       }
       if (!more) break;
       cur = nxt;
     }
   }
-  emit_group<G, MODE>(em, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, L, skipm);
+  emit_group<G, MODE, GB>(em, acc, bh, gb0, a.blk0, a.blk_end, a.n, wave, lane, L, skipm);
 }
 
 // One tile per workgroup (grid.x = list entries), except the fallback pass:
 // a grid-stride loop of few workgroups over the list, so that rows which need
 // no fallback (every row, normally) cost only those workgroups' launches.
-template <int G, int MODE, bool FAST>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4 && MODE != kEmitFallback ? 5 : 4))) void scan_tile_kernel(ScanArgs a, Emit em) {
-  __shared__ TileShared<G> sh;
+template <int G, int MODE, bool FAST, int NG>
+__global__ __launch_bounds__(Geo<NG>::THREADS) __attribute__((amdgpu_waves_per_eu(G <= 4 && MODE != kEmitFallback ? 5 : 4))) void scan_tile_kernel(ScanArgs a, Emit em) {
+  __shared__ TileShared<G, NG> sh;
   __shared__ uint32_t s_tot[G];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -583,7 +602,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4
     for (int g = 0; g < G; ++g) {
       const uint4 *rc = reinterpret_cast<const uint4 *>(em.sel.rc1 + (bh * G + g) * em.sel.nreg);
       uint32_t part = 0u;
-      for (int64_t i = tid; i < nq; i += kThreads) {
+      for (int64_t i = tid; i < nq; i += Geo<NG>::THREADS) {
         const uint4 c = rc[i];
         part += c.x + c.y + c.z + c.w;
       }
@@ -599,12 +618,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 4
 #pragma unroll
   for (int c = 0; c < 4; ++c) nc[c] = c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
   const PlanStreams ps = plan_streams(nc);
-  tile_prologue<G>(sh, a, nc, ps, bh);
+  tile_prologue<G, NG>(sh, a, nc, ps, bh);
   __syncthreads();  // plan streams ready
-  if (MODE == kEmitFallback) {
-    for (int64_t L = blockIdx.x; L < a.ntiles; L += gridDim.x) scan_one<G, kEmitFilter, FAST>(a, em, sh, ps, L, wave, lane, skipm);
+  if constexpr (MODE == kEmitFallback) {
+    for (int64_t L = blockIdx.x; L < a.ntiles; L += gridDim.x) scan_one<G, kEmitFilter, FAST, NG>(a, em, sh, ps, L, wave, lane, skipm);
   } else {
-    scan_one<G, MODE, FAST>(a, em, sh, ps, blockIdx.x, wave, lane, 0u);
+    scan_one<G, MODE, FAST, NG>(a, em, sh, ps, blockIdx.x, wave, lane, 0u);
   }
 }
 
@@ -760,10 +779,12 @@ void launch_chan4_g(const Chan4Args &a, int64_t tiles, int64_t BH, const Emit &e
 // --------------------------------------------------------------------- launch
 template <int G, int MODE>
 void launch_g(const ScanArgs &a, int64_t tiles, int64_t BH, const Emit &em, hipStream_t st) {
+  constexpr int NG = MODE == kEmitSample ? 1 : 2;
+  constexpr int NT = Geo<NG>::THREADS;
   if (a.fast)
-    scan_tile_kernel<G, MODE, true><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
+    scan_tile_kernel<G, MODE, true, NG><<<dim3((unsigned)tiles, (unsigned)BH), NT, 0, st>>>(a, em);
   else
-    scan_tile_kernel<G, MODE, false><<<dim3((unsigned)tiles, (unsigned)BH), kThreads, 0, st>>>(a, em);
+    scan_tile_kernel<G, MODE, false, NG><<<dim3((unsigned)tiles, (unsigned)BH), NT, 0, st>>>(a, em);
 }
 
 constexpr int64_t kFallbackWGs = 64;  // workgroups per row of the fallback pass
