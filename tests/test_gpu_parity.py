@@ -205,7 +205,8 @@ def _topk_case(rows, k, sink, local, m=None):
 
 @pytest.mark.parametrize("n,k,sink,local", [(1000, 128, 4, 64), (16384, 128, 4, 64), (131072, 512, 4, 32),
                                             (100000, 2048, 4, 32), (3000, 2048, 4, 32), (600, 40, 0, 0),
-                                            (32768, 512, 4, 32), (32769, 512, 4, 32), (32768, 2048, 0, 0)])
+                                            (32768, 512, 4, 32), (32769, 512, 4, 32), (32768, 2048, 0, 0),
+                                            (65536, 1024, 0, 0)])
 def test_topk_random_bitexact(n, k, sink, local):
     """Rows up to 32768 take the one-kernel row selection, longer rows the
     sample / select / filter / finalize chain; both must equal the oracle."""
