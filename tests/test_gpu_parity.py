@@ -159,6 +159,28 @@ def test_scan_matches_oracle(cfg, n, BH, sub):
     _scores_close(scores, ref)
 
 
+@pytest.mark.parametrize("G,n", [(2, 40000), (3, 20000), (5, 40000), (6, 20000), (8, 40000), (8, 20000)])
+def test_scan_and_fused_topk_every_group_size(G, n):
+    """The scan is instantiated per head count G (1-8) and the configurations
+    reach only G = 1, 4, 7: scores against the oracle, and the fused top-k
+    (chain above 32768 tokens, row select below) against the unfused one, bit
+    for bit.  (PlaneStore keeps D = 128, kernels/bitplane.py:313.)"""
+    print(f"[scan-G] G={G} n={n}", flush=True)
+    BH, k = 2, 256
+    x = W.synth_layer(BH, n, G, seed=100 * G + n % 7)
+    g = ((x["q"] ** 2) * x["var"][:, None, :]).sum(1)
+    st = bp.PlaneStore(x["K"].to(DEV))
+    plan = bp.make_plan(g.to(DEV), 48.0)
+    q = x["q"].to(DEV)
+    scores = st.scan(q, plan)
+    code_r, sc_r = O.quantise_u4(x["K"].float().numpy())
+    ref = O.scan_planes(x["q"].numpy(), code_r, sc_r.astype(np.float16).astype(np.float32), plan["t"].cpu().numpy())
+    _scores_close(scores.cpu().numpy(), ref)
+    want = bp.sink_local_topk(scores, k, 4, 32)
+    got = st.scan_topk(q, plan, k, 4, 32)
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("budget", [40.0, 48.0, 80.0, 0.0, 512.0])
 def test_scan_budgets_c4_shape(budget):
     x, st, plan = _scan_case(4, 4096, 2, budget=budget)
