@@ -238,6 +238,32 @@ def test_topk_random_bitexact(n, k, sink, local):
     _topk_case(rows, k, sink, local)
 
 
+def test_topk_edge_k_and_errors():
+    """kk = k - sink - local at its edges: 0 (only the fixed positions), the
+    whole row, one token, more than the unmasked tokens (masked -inf keys fill
+    the rest by index); then the argument errors."""
+    rng = np.random.default_rng(7)
+    rows = rng.standard_normal((2, 3, 5000)).astype(np.float32)
+    _topk_case(rows[..., :1000], 36, 4, 32)     # kk = 0
+    _topk_case(rows[..., :300], 300, 0, 0)      # kk = n
+    _topk_case(rows[..., :1], 1, 0, 0)          # one token
+    _topk_case(rows[..., :40], 50, 4, 32)       # kk = 14, four unmasked tokens
+    t = torch.from_numpy(rows).to(DEV)
+    for n, k, sink, local in ((1000, 30, 4, 32),     # k < sink + local
+                              (1000, 1037, 4, 32),   # kk > n
+                              (5000, 2049, 0, 0)):   # kk above the largest supported
+        with pytest.raises(ValueError):
+            bp.sink_local_topk(t[..., :n].contiguous(), k, sink, local)
+    x, st, plan = _scan_case(2, 2000, 2)
+    q = x["q"].to(DEV)
+    sc = st.scan(q, plan)
+    for k, sink, local in ((36, 4, 32), (2000, 0, 0), (100, 4, 32)):
+        torch.testing.assert_close(st.scan_topk(q, plan, k, sink, local), bp.sink_local_topk(sc, k, sink, local),
+                                   rtol=0, atol=0)
+    with pytest.raises(ValueError):
+        st.scan_topk(q, plan, 30, 4, 32)
+
+
 def test_topk_ties_nan_inf_negzero():
     rng = np.random.default_rng(1)
     n = 5000
