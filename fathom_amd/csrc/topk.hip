@@ -832,13 +832,14 @@ size_t topk_sel_layout(int64_t rows, int64_t cand_cap, int64_t nreg, char *base,
 size_t topk_layout(int64_t rows, int64_t n, int64_t k, bool regions, char *base, uint32_t **samp, int64_t *samp_cap,
                    TopkSel *sel, int64_t *S_out) {
   const int64_t kk = k > 0 ? k : 0;
-  const int64_t S = topk_tile_stride(n, kk);
-  const int64_t cap = topk_sample_tiles(n, S) * kTileTok;
+  const int64_t tile = regions ? kRegTok : kTileTok;
+  const int64_t S = topk_tile_stride(n, kk, tile);
+  const int64_t cap = topk_sample_tiles(n, S, tile) * tile;
   const size_t samp_b = ws_align((size_t)rows * (size_t)cap * 4);
   if (samp) *samp = reinterpret_cast<uint32_t *>(base);
   if (samp_cap) *samp_cap = cap;
   if (S_out) *S_out = S;
-  const int64_t cand_cap = regions ? cdiv(n, kTileTok) * kTileTok : n;
+  const int64_t cand_cap = regions ? cdiv(n, 4 * kRegTok) * 4 * kRegTok : n;
   return samp_b + topk_sel_layout(rows, cand_cap, regions ? cand_cap / kRegTok : 0, base ? base + samp_b : nullptr, sel);
 }
 
@@ -926,7 +927,7 @@ extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t
   s.kk = (uint32_t)kk;
   if (n <= kRowSelectMax) return launch_rowselect(scores, rows, n, m, k, sink, local, idx, st);
   const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
-  const int64_t r_hi = topk_hi_rank(n, S, kk);
+  const int64_t r_hi = topk_hi_rank(n, S, kk, kTileTok);
   rc = launch_sample_scores(scores, rows, n, S, sink, lstart, samp, samp_cap, st);
   if (rc) return rc;
   rc = launch_select_keys(samp, rows, samp_cap, kk, r_hi, s, st);

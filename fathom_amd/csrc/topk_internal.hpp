@@ -30,8 +30,8 @@
 
 namespace fathom {
 
-constexpr int64_t kTileTok = 2048;  // tokens per scan tile (32 blocks)
-constexpr int64_t kRegTok = 512;    // tokens per candidate region (8 blocks: one wave of a scan tile)
+constexpr int64_t kTileTok = 2048;  // tokens per sample tile of the score-row top-k
+constexpr int64_t kRegTok = 1024;   // tokens per candidate region and sample tile of the fused scan (one wave-tile)
 constexpr int64_t kMaxSample = 65536; // sampled keys per row (held in registers by select)
 
 constexpr int64_t kAlpha = 4;  // expected first-pass candidates per row, in units of kk
@@ -61,32 +61,34 @@ struct TopkSel {
   __host__ __device__ uint32_t *cnt2(int64_t row) const { return cand2_cnt + row * kCntStride; }
 };
 
-// Sample stride in tiles: about 8 sampled tiles per row, more where the sample
-// must hold 2 kk keys or where about 16 sampled keys must reach the first-pass
-// threshold (kAlpha * kk * sample / n >= 16), at most kMaxSample keys.
-inline int64_t topk_tile_stride(int64_t n, int64_t kk) {
-  const int64_t ntiles = cdiv(n, kTileTok);
-  int64_t want = 8;
+// Sample stride in tiles of `tile` tokens: about 16384 sampled tokens per row,
+// more where the sample must hold 2 kk keys or where about 16 sampled keys
+// must reach the first-pass threshold (kAlpha * kk * sample / n >= 16), at
+// most kMaxSample keys.  The stride rounds up, so the sample never exceeds
+// that many tiles.
+inline int64_t topk_tile_stride(int64_t n, int64_t kk, int64_t tile) {
+  const int64_t ntiles = cdiv(n, tile);
+  int64_t want = cdiv(8 * kTileTok, tile);
   if (kk > 0) {
-    const int64_t a = cdiv(2 * kk, kTileTok), b = cdiv(16 * n, kAlpha * kk * kTileTok);
+    const int64_t a = cdiv(2 * kk, tile), b = cdiv(16 * n, kAlpha * kk * tile);
     want = a > want ? a : want;
     want = b > want ? b : want;
   }
-  const int64_t cap = kMaxSample / kTileTok;
+  const int64_t cap = kMaxSample / tile;
   if (want > cap) want = cap;
-  const int64_t S = ntiles / want;
+  const int64_t S = cdiv(ntiles, want);
   return S < 1 ? 1 : S;
 }
 
-inline int64_t topk_sample_tiles(int64_t n, int64_t S) { return cdiv(cdiv(n, kTileTok), S); }
+inline int64_t topk_sample_tiles(int64_t n, int64_t S, int64_t tile) { return cdiv(cdiv(n, tile), S); }
 
 // Rank in the sample of the first-pass threshold: about kAlpha * kk of the row's
 // n elements are expected at or above it (kk when the sample is the row).
-inline int64_t topk_hi_rank(int64_t n, int64_t S, int64_t kk) {
+inline int64_t topk_hi_rank(int64_t n, int64_t S, int64_t kk, int64_t tile) {
   int64_t sampled = 0;
-  for (int64_t t = 0, nt = topk_sample_tiles(n, S); t < nt; ++t) {
-    const int64_t left = n - t * S * kTileTok;
-    sampled += left < kTileTok ? (left > 0 ? left : 0) : kTileTok;
+  for (int64_t t = 0, nt = topk_sample_tiles(n, S, tile); t < nt; ++t) {
+    const int64_t left = n - t * S * tile;
+    sampled += left < tile ? (left > 0 ? left : 0) : tile;
   }
   const int64_t r = (kAlpha * kk * sampled + n - 1) / n;
   return r < 1 ? 1 : (r > kk ? kk : r);
@@ -100,8 +102,9 @@ inline size_t ws_align(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t topk_sel_layout(int64_t rows, int64_t cand_cap, int64_t nreg, char *base, TopkSel *s);
 
 // Whole top-k workspace: sampled keys [rows, samp_cap] + selection state with
-// candidate room for a full row (regions: whole scan tiles, the list layout
-// otherwise).  S is sized for kk = k (an upper bound on k - sink - local; a
+// candidate room for a full row (regions: whole groups of four regions, the
+// list layout otherwise).  Samples are tiles of kRegTok tokens with regions,
+// kTileTok otherwise.  S is sized for kk = k (an upper bound on k - sink - local; a
 // larger kk only means a denser sample).
 size_t topk_layout(int64_t rows, int64_t n, int64_t k, bool regions, char *base, uint32_t **samp, int64_t *samp_cap,
                    TopkSel *sel, int64_t *S_out);

@@ -767,8 +767,9 @@ def _full_depth_plan(act, nact, D=128):
 
 @pytest.mark.parametrize("G,n,r", [(4, 5000, 32), (7, 3000, 16), (1, 700, 128), (3, 2100, 0)])
 def test_scan_chan4_matches_oracle_and_plane_scan(G, n, r):
-    """Chan4 scores against the float64 oracle, and bit-identical to the plane scan of a
-    plan with t = 4 on the same channels (same y = 2a(c - 7.5), weights q/16, order)."""
+    """Chan4 scores against the float64 oracle, and the plane scan of a plan with
+    t = 4 on the same channels against the same oracle scores (the two stores hold
+    the same codes; their kernels sum in different orders)."""
     print(f"[scan-chan4] G={G} n={n} r={r}", flush=True)
     BH = 3
     K = _keys(BH, n, dtype=torch.bfloat16, edge=False)
@@ -784,10 +785,10 @@ def test_scan_chan4_matches_oracle_and_plane_scan(G, n, r):
     ps = bp.PlaneStore(Kd)
     plane = ps.scan(qd, _full_depth_plan(act, nact))
     torch.cuda.synchronize()
-    assert torch.equal(got, plane), "chan4 scan differs from the depth-4 plane scan"
     code, sc = O.quantise_u4(K.float().numpy())
     ref = O.scan_chan4(q.numpy(), code, sc, act.cpu().numpy(), nact.cpu().numpy())
     _scores_close(got.cpu().numpy(), ref)
+    _scores_close(plane.cpu().numpy(), ref)
     # a block sub-range leaves the rest of `out` untouched
     out = torch.full_like(got, 7.0)
     cs.scan(qd, act, nact, out=out, blocks=(3, 9))
