@@ -70,7 +70,7 @@ struct h2x2 {
   h2 a, b;
 };
 
-enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2, kEmitFallback = 3 };
+enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2 };
 
 struct ScanArgs {
   const float *q;          // [BH, G, D]
@@ -92,6 +92,7 @@ struct Emit {
   int64_t samp_cap;
   TopkSel sel;       // thresholds + candidate regions
   int64_t sink, lstart;
+  int fallback_check;  // candidate pass: the last workgroup of a row runs the fallback if needed
 };
 
 // Wave-uniform loads through the constant address space (scalar loads).
@@ -127,8 +128,8 @@ struct Shared {
   uint32_t desc[kMaxUnits];        // unit -> plane word index (j * 4 + p) | slot << 16
   uint16_t schan[kMaxD];           // channel slot -> channel
   uint16_t a[kWaves][kMaxD][kWB];  // per wave: scales of the slots' channels by block (f16 bits)
-  uint32_t qmax[4 * NQ];           // largest |q| of each head (float bits)
-  int sig[4 * NQ];                 // sigma_g
+  float qs[4 * NQ][kMaxD];         // the queries (0 for heads >= G)
+  int sig[4 * NQ];                 // sigma_g: the exponent of the head's largest |q|
 };
 
 // Quad (4-lane) reductions: every lane of the quad gets the same value, summed
@@ -151,7 +152,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Workgroup prologue: the plan tables in LDS (units in class order: the class
 // 1 list, then 2, 3, 4; a channel's planes consecutive), padded with zero
-// weights to a whole number of chunks.  Returns the unit count.
+// weights to a whole number of chunks.  One round of global loads: the
+// queries (32 threads per head, which also reduce the head's largest |q|)
+// and the class lists, then the tables from LDS.  Returns the unit count.
 template <int NQ>
 __device__ __forceinline__ int plan_tables(Shared<NQ> &sh, const ScanArgs &a, int64_t bh, int &nact) {
   const int tid = threadIdx.x;
@@ -167,24 +170,43 @@ __device__ __forceinline__ int plan_tables(Shared<NQ> &sh, const ScanArgs &a, in
     UE[c] = u;
   }
   nact = s;
-  if (tid < 4 * NQ) sh.qmax[tid] = 0u;
-  __syncthreads();
-  const float *qb = a.q + bh * a.G * a.D;
-  for (int e = tid; e < a.G * a.D; e += kThreads) atomicMax(&sh.qmax[e / a.D], __float_as_uint(fabsf(qb[e])));
-  __syncthreads();
-  if (tid < 4 * NQ) sh.sig[tid] = __builtin_amdgcn_frexp_expf(__uint_as_float(sh.qmax[tid]));
+  static_assert(4 * NQ * 32 <= kThreads, "32 threads per head");
+  {
+    const int h = tid >> 5, part = tid & 31;
+    if (h < 4 * NQ) {
+      float qv[kMaxD / 32];
+#pragma unroll
+      for (int k = 0; k < kMaxD / 32; ++k) {
+        const int j = part + 32 * k;
+        qv[k] = (h < a.G && j < a.D) ? a.q[(bh * a.G + h) * a.D + j] : 0.0f;
+      }
+      float m = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kMaxD / 32; ++k) {
+        sh.qs[h][part + 32 * k] = qv[k];
+        m = fmaxf(m, fabsf(qv[k]));
+      }
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
+      if (part == 0) sh.sig[h] = __builtin_amdgcn_frexp_expf(m);
+    }
+  }
+  for (int e = tid; e < nact; e += kThreads) {
+    const int c = (e >= SF[0]) + (e >= SF[1]) + (e >= SF[2]);
+    const int lo = c == 0 ? 0 : SF[c - 1];
+    const int jr = a.cls[(bh * a.bmax + c) * a.D + (e - lo)];
+    sh.schan[e] = (uint16_t)min(max(jr, 0), a.D - 1);  // memory-safe; make_plan lists only valid channels
+  }
   __syncthreads();
   for (int e = tid; e < nact; e += kThreads) {
     const int c = (e >= SF[0]) + (e >= SF[1]) + (e >= SF[2]);
     const int lo = c == 0 ? 0 : SF[c - 1];
     const int ub = (c == 0 ? 0 : UE[c - 1]) + (e - lo) * (c + 1);
-    const int jr = a.cls[(bh * a.bmax + c) * a.D + (e - lo)];
-    const int j = min(max(jr, 0), a.D - 1);  // memory-safe; make_plan lists only valid channels
-    sh.schan[e] = (uint16_t)j;
+    const int j = sh.schan[e];
     const float cf = ldexpf(1.0f, -(c + 1)) - 1.0f;
 #pragma unroll
     for (int h = 0; h < 4 * NQ; ++h) {
-      const float qv = h < a.G ? qb[h * a.D + j] : 0.0f;
+      const float qv = sh.qs[h][j];
       sh.qc[h][e] = qv * cf;
       for (int p = 0; p <= c; ++p) sh.qt[h][ub + p] = ldexpf(qv, -(p + sh.sig[h]));
     }
@@ -514,13 +536,25 @@ __device__ __forceinline__ void emit_sample(const Emit &em, const Tile<NQ, RS> &
 
 // Candidate emission of a wave-tile into its region (tokens [beta0 * 64, +
 // 1024)) of each row: keys >= the row's threshold, ranked within the wave by
-// ballots, and the region's count.  A head whose largest score in the wave is
-// below the threshold (the common case) writes only its count: the largest
-// score comes from the NaN-propagating maximum of the exact products acc *
-// 2^-e_r, which rounds like the scores themselves.  Heads in skipm emit nothing.
+// ballots, and the region's count.  Heads in skipm emit nothing.
+//
+// In a tile with no masked token, a token step first runs a prefilter, one
+// compare of the accumulators with a threshold in their own domain, T_w =
+// ((thr - C) - margin) / f_w.  The score is RN(acc f_w + C) with acc f_w exact,
+// so a score >= thr needs acc f_w + C >= thr - ulp(thr); the margin covers
+// that ulp and the rounding of thr - C, so no passing token fails the
+// prefilter (NaN passes both).  Only steps where some lane passes it compute
+// scores and keys.
+__device__ __forceinline__ float acc_threshold(float thr, float C, float f) {
+  if (!(f > 0.0f) || !(f < INFINITY) || !(fabsf(C) < INFINITY)) return __int_as_float(0x7FC00000);  // NaN: all pass
+  const float margin = (fabsf(thr) + fabsf(C)) * 0x1p-20f + 0x1p-126f;
+  return ((thr - C) - margin) * (1.0f / f);
+}
+
 template <int NQ>
-__device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t, const Shared<NQ> &sh, const ScanArgs &a,
-                                            int64_t bh, int64_t beta0, int lane, bool fallback, uint32_t skipm) {
+__device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t, const Shared<NQ> &sh,
+                                            const ScanArgs &a, int64_t bh, int64_t beta0, int lane, bool fallback,
+                                            uint32_t skipm, uint32_t (&tot)[4 * NQ]) {
   const int b = lane >> 2, i = lane & 3;
   const int64_t region = beta0 / kWB;
   const int64_t tok0 = (beta0 + b) * kBlk + 16 * i;
@@ -536,79 +570,53 @@ __device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t
     if ((skipm >> h) & 1u) continue;
     const int64_t row = bh * a.G + h;
     const float thr_f = threshold_value(ld_uniform(thr + row));
-    float f[4];
+    float f[4], T[4];
     head_factors(f, t, sh, h);
-    bool any = true;
-    if (plain) {
-      // the lane's largest score: per step class w the largest accumulator
-      // (the score is increasing in it), NaN-propagating
-      float smax = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const f4 *ac = t.acc[h >> 2];
-        const float m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(ac[w][h & 3], ac[4 + w][h & 3]),
-                                                      __builtin_elementwise_maximum(ac[8 + w][h & 3], ac[12 + w][h & 3]));
-        smax = __builtin_elementwise_maximum(smax, fmaf(m, f[w], t.cst[h]));
-      }
-      any = __ballot(!(smax < thr_f)) != 0ull;
-    }
+    for (int w = 0; w < 4; ++w) T[w] = plain ? acc_threshold(thr_f, t.cst[h], f[w]) : __int_as_float(0x7FC00000);
+    uint64_t *dst = em.sel.cand + row * em.sel.cand_cap + t0;
     uint32_t off = 0u;
-    if (any) {
-      uint64_t *dst = em.sel.cand + row * em.sel.cand_cap + t0;
 #pragma unroll
-      for (int r = 0; r < kR; ++r) {
-        const int64_t tok = tok0 + r;
-        const float v = tile_score<NQ, 1>(t, f, r, h);
-        bool valid = true;
-        float vm = v;
-        if (!plain) {
-          const int64_t blk = beta0 + b;
-          valid = blk >= a.blk0 && blk < a.blk_end && tok < a.n;
-          vm = (tok < em.sink || tok >= em.lstart) ? -INFINITY : v;
-        }
-        const bool pass = valid && !(vm < thr_f);
-        const uint64_t msk = __ballot(pass);
-        if (msk) {  // uniform: most steps of a head with candidates have none
-          if (pass) dst[off + (uint32_t)__popcll(msk & lt)] = k64_of(vm == -INFINITY ? kKeyNegInf : score_key(vm), tok);
-          off += (uint32_t)__popcll(msk);
-        }
+    for (int r = 0; r < kR; ++r) {
+      if (__ballot(!(t.acc[h >> 2][r][h & 3] < T[r & 3])) == 0ull) continue;  // uniform
+      const int64_t tok = tok0 + r;
+      const float v = tile_score<NQ, 1>(t, f, r, h);
+      bool valid = true;
+      float vm = v;
+      if (!plain) {
+        const int64_t blk = beta0 + b;
+        valid = blk >= a.blk0 && blk < a.blk_end && tok < a.n;
+        vm = (tok < em.sink || tok >= em.lstart) ? -INFINITY : v;
       }
+      const bool pass = valid && !(vm < thr_f);
+      const uint64_t msk = __ballot(pass);
+      if (pass) dst[off + (uint32_t)__popcll(msk & lt)] = k64_of(vm == -INFINITY ? kKeyNegInf : score_key(vm), tok);
+      off += (uint32_t)__popcll(msk);
     }
     if (lane == 0) rc[row * em.sel.nreg + region] = off;
+    tot[h] += off;
   }
 }
 
 // --------------------------------------------------------------------- kernel
 // Grid (workgroups, BH); the waves of the grid's row take the list entries L
-// in a grid-stride loop.  The fallback pass first sums every head's
-// first-pass region counts: heads with at least kk candidates skip it, and a
-// workgroup whose heads all skip returns at once.
+// in a grid-stride loop.  The candidate pass ends with the fallback check.
+// Every cross-workgroup value goes through returning atomics, which resolve
+// at one coherence point (no fence, no cache writeback): a workgroup adds its
+// per-head candidate totals to the row's counters, waits for them, then counts
+// itself done on the row's completion counter; the workgroup that counts last
+// reads the totals back and, for heads with fewer than kk candidates (a sample
+// that misled T_hi), rescans the row with T_lo into the regions under the
+// second count array -- slowly, with its four waves alone, but only for such
+// rows.  Nothing waits on another workgroup.
 template <int NQ, int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 1 && MODE != kEmitSample ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
   __shared__ Shared<NQ> sh;
-  __shared__ uint32_t s_tot[8];
+  __shared__ uint32_t s_tot[8], s_wt[kWaves][8];
+  __shared__ uint32_t s_last;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
-  uint32_t skipm = 0u;
-  if constexpr (MODE == kEmitFallback) {
-    if (tid < 8) s_tot[tid] = 0u;
-    __syncthreads();
-    const int64_t nq = em.sel.nreg / 4;  // regions per row: a multiple of 4
-    for (int g = 0; g < a.G; ++g) {
-      const uint4 *rc = reinterpret_cast<const uint4 *>(em.sel.rc1 + (bh * a.G + g) * em.sel.nreg);
-      uint32_t part = 0u;
-      for (int64_t k = tid; k < nq; k += kThreads) {
-        const uint4 c = rc[k];
-        part += c.x + c.y + c.z + c.w;
-      }
-      part = __builtin_amdgcn_readlane(wave_incl_scan_u32(part), kWave - 1);
-      if (lane == 0 && part) atomicAdd(&s_tot[g], part);
-    }
-    __syncthreads();
-    for (int g = 0; g < a.G; ++g) skipm |= (s_tot[g] >= em.sel.kk ? 1u : 0u) << g;
-    if (skipm == (1u << a.G) - 1u) return;  // uniform
-  }
   int nact = 0;
   const int U = plan_tables<NQ>(sh, a, bh, nact);
   uint16_t(*aw)[kWB] = sh.a[wave];
@@ -625,31 +633,61 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 
       emit_sample(em, t, sh, a, bh, beta0, L, lane);
       wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
     }
-    return;
   } else {
     Tile<NQ, 1> t;
     t.r0 = 0;
-    // candidate passes also write the (zero) counts of the padding regions past the row
-    constexpr bool kCand = MODE == kEmitFilter || MODE == kEmitFallback;
+    // the candidate pass also writes the (zero) counts of the padding regions past the row
+    constexpr bool kCand = MODE == kEmitFilter;
     const int64_t nlist = kCand && em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
-    for (int64_t L = (int64_t)blockIdx.x * kWaves + wave; L < nlist; L += (int64_t)gridDim.x * kWaves) {
-      if (kCand && L >= a.nwt) {
-        if (lane < a.G && !((skipm >> lane) & 1u)) (MODE == kEmitFallback ? em.sel.rc2 : em.sel.rc1)[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
-        continue;
+    int64_t L0 = (int64_t)blockIdx.x * kWaves + wave, Ls = (int64_t)gridDim.x * kWaves;
+    uint32_t skipm = 0u;
+    bool fb = false;
+    uint32_t tot[4 * NQ];
+#pragma unroll
+    for (int h = 0; h < 4 * NQ; ++h) tot[h] = 0u;
+#pragma nounroll
+    for (int pass = 0; pass < (kCand ? 2 : 1); ++pass) {
+      if (pass == 1) {  // the fallback check (candidate pass only)
+        if (!em.fallback_check) return;  // uniform
+        if (lane == 0)
+#pragma unroll
+          for (int h = 0; h < 4 * NQ; ++h) s_wt[wave][h] = tot[h];
+        __syncthreads();
+        if (tid < a.G) {
+          const uint32_t add = s_wt[0][tid] + s_wt[1][tid] + s_wt[2][tid] + s_wt[3][tid];
+          const uint32_t was = atomicAdd(em.sel.cnt1(bh * a.G + tid), add);
+          asm volatile("" ::"v"(was));  // completed before the barrier, so before the done count
+        }
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(em.sel.cnt2(bh * a.G), 1u) == gridDim.x - 1 ? 1u : 0u;
+        __syncthreads();
+        if (!s_last) return;  // uniform
+        if (tid < a.G) s_tot[tid] = atomicAdd(em.sel.cnt1(bh * a.G + tid), 0u);
+        __syncthreads();
+        for (int g = 0; g < a.G; ++g) skipm |= (s_tot[g] >= em.sel.kk ? 1u : 0u) << g;
+        if (skipm == (1u << a.G) - 1u) return;  // uniform: the common case
+        fb = true;
+        L0 = wave;
+        Ls = kWaves;
       }
-      const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
-      if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
-      scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
-      if constexpr (MODE == kEmitScores) emit_scores<NQ>(em, t, sh, a, bh, beta0, lane);
-      if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, false, 0u);
-      if constexpr (MODE == kEmitFallback) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, true, skipm);
-      wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
+      uint32_t *rcp = fb ? em.sel.rc2 : em.sel.rc1;
+      for (int64_t L = L0; L < nlist; L += Ls) {
+        if (kCand && L >= a.nwt) {
+          if (lane < a.G && !((skipm >> lane) & 1u)) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
+          continue;
+        }
+        const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
+        if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
+        scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
+        if constexpr (MODE == kEmitScores) emit_scores<NQ>(em, t, sh, a, bh, beta0, lane);
+        if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, fb, skipm, tot);
+        wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
+      }
     }
   }
 }
 
 // --------------------------------------------------------------------- launch
-constexpr int64_t kFallbackWGs = 64;  // workgroups per row of the fallback pass
 constexpr int64_t kTargetWaves = 4096;  // waves of a full launch (4 per SIMD on 256 CUs)
 
 template <int MODE>
@@ -658,9 +696,7 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, hip
   ScanArgs a = a0;
   a.nwt = nwt;
   int64_t wgs = cdiv(nwt, kWaves);
-  if (MODE == kEmitFallback) {
-    wgs = wgs < kFallbackWGs ? wgs : kFallbackWGs;
-  } else if (MODE == kEmitSample) {
+  if (MODE == kEmitSample) {
     wgs = nwt;  // one tile per workgroup
   } else {
     // enough waves to fill the chip, each taking a whole number of tiles
@@ -804,11 +840,10 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, r_hi, em.sel, st);
   if (rc) return rc;
   a.wt_stride = 1;
+  // T_hi may exceed a row's kk-th largest key (r_hi < kk): the candidate pass
+  // then checks every row and rescans those with fewer than kk candidates
+  em.fallback_check = r_hi < kk ? 1 : 0;
   rc = launch_scan<kEmitFilter>(a, nwt, BH, em, st);
   if (rc) return rc;
-  if (r_hi < kk) {  // T_hi may exceed a row's kk-th largest key: rows with < kk candidates scan again with T_lo
-    rc = launch_scan<kEmitFallback>(a, nwt, BH, em, st);
-    if (rc) return rc;
-  }
   return launch_finalize(rows, m, k, sink, local, em.sel, idx, st);
 }
