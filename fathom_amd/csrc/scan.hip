@@ -143,6 +143,16 @@ __device__ __forceinline__ float quad_max(float v) {
   return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
 }
 
+// A CU's waves of equal priority issue oldest first, so the workgroups placed
+// first on a CU race ahead and the last ones run the kernel's tail at low
+// occupancy.  Waves with more tiles left take a higher priority instead.
+__device__ __forceinline__ void set_priority_by_tiles_left(int64_t left) {
+  if (left >= 3) __builtin_amdgcn_s_setprio(3);
+  else if (left == 2) __builtin_amdgcn_s_setprio(2);
+  else if (left == 1) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // Orders a wave's LDS accesses: every lane's writes before any lane's reads.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -678,6 +688,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 
         }
         const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
         if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
+        set_priority_by_tiles_left((nlist - 1 - L) / Ls);
         scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
         if constexpr (MODE == kEmitScores) emit_scores<NQ>(em, t, sh, a, bh, beta0, lane);
         if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, fb, skipm, tot);
