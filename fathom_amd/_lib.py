@@ -35,6 +35,8 @@ PROTOTYPES = {
     "fathom_scan_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "fathom_scan_topk": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _vp, _vp, _sz, _vp]),
+    "fathom_scan_topk_stages": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                       _i64, _i64, _vp, _vp, _sz, _i32, _vp]),
     "fathom_topk_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "fathom_sink_local_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "fathom_gather_rows": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),

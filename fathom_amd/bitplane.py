@@ -31,6 +31,8 @@ from . import _lib
 
 BLK, SUB, D = 64, 16, 128
 SBT = BLK * SUB
+# stages of PlaneStore.scan_topk_stages (FATHOM_STAGE_* of include/fathom_hip.h)
+STAGE_SAMPLE, STAGE_SELECT, STAGE_CANDIDATES, STAGE_FINALIZE, STAGE_ALL = 1, 2, 4, 8, 15
 
 __all__ = ["BLK", "SUB", "D", "SBT", "quantise_u4", "dequant_planes", "pack_planes", "unpack_planes",
            "to_superblocks", "pack_chan4", "bytes_planes", "bytes_chan4", "make_plan", "make_plan_torch",
@@ -312,6 +314,32 @@ class PlaneStore:
                   int(self.nsb), sub, m, int(k), int(sink), int(local), _ptr(idx), _ptr(ws), nbytes,
                   _stream(q.device))
         return idx
+
+    def scan_topk_stages(self, q, plan, k, stages, ws=None, idx=None, sink=4, local=32, m=None):
+        """Stages of scan_topk (bit mask of STAGE_*) on a caller-kept workspace
+        (bench.py times the candidate pass alone this way; the reference has no
+        counterpart).  Returns (idx, ws); pass both back to run later stages
+        over the state the earlier ones left."""
+        _need_gpu(q)
+        BH, G, d = q.shape
+        n = self.n
+        m = n if m is None else int(m)
+        sub = int(getattr(self, "sub", SUB))
+        qc = q.contiguous().float()
+        L = _lib.lib()
+        nbytes = L.fathom_scan_topk_workspace_bytes(BH, G, n, int(k), int(sink), int(local))
+        if idx is None:
+            idx = torch.empty(BH, G, int(k), dtype=torch.int64, device=q.device)
+        if ws is None:
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        if ws.numel() < nbytes:
+            raise ValueError(f"workspace of {ws.numel()} bytes, need {nbytes}")
+        cls, clsn = _plan_classes(plan, BH, d)
+        _lib.call("fathom_scan_topk_stages", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1],
+                  ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), n,
+                  int(self.nsb), sub, m, int(k), int(sink), int(local), _ptr(idx), _ptr(ws), nbytes, int(stages),
+                  _stream(q.device))
+        return idx, ws
 
     def nbytes(self):
         return self.BH * self.nsb * D * 4 * int(getattr(self, "sub", SUB)) * 8 + \

@@ -807,19 +807,22 @@ extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_
   return scan_topk_ws(BH * G, n, k);
 }
 
-extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
-                                const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
-                                int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink,
-                                int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes, void *stream) {
+namespace fathom {
+namespace {
+int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
+                  const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m,
+                  int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes,
+                  int stages, void *stream) {
   int rc = check_scan(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, "scan_topk");
   if (rc) return rc;
   if (!idx) return fail(FATHOM_ERR_INVALID, "scan_topk: null output");
+  if (stages & ~FATHOM_STAGE_ALL) return fail(FATHOM_ERR_INVALID, "scan_topk: unknown stage bits 0x%x", stages);
   const int64_t rows = BH * G;
   rc = check_topk_args(rows, n, m, k, sink, local, "scan_topk");
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
-  if (kk == 0) return launch_fixed_only(rows, m, k, sink, local, idx, st);
+  if (kk == 0) return (stages & FATHOM_STAGE_FINALIZE) ? launch_fixed_only(rows, m, k, sink, local, idx, st) : FATHOM_OK;
   const size_t need = scan_topk_ws(rows, n, k);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "scan_topk: workspace %zu bytes, need %zu", workspace_bytes, need);
@@ -830,13 +833,15 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   a.wt0 = 0;
   const int64_t nwt = cdiv(nblk, kWB);
   if (n <= kRowSelectMax) {
-    // short rows: the scores in the workspace, then the whole rows selected
-    // in one launch (two kernels instead of the five of the chain below)
+    // short rows: the scores in the workspace (the candidate stage), then the
+    // whole rows selected in one launch (the finalize stage)
     Emit es{};
     es.out = static_cast<float *>(workspace);
-    rc = launch_scan<kEmitScores>(a, nwt, BH, es, st);
-    if (rc) return rc;
-    return launch_rowselect(es.out, rows, n, m, k, sink, local, idx, st);
+    if (stages & FATHOM_STAGE_CANDIDATES) {
+      rc = launch_scan<kEmitScores>(a, nwt, BH, es, st);
+      if (rc) return rc;
+    }
+    return (stages & FATHOM_STAGE_FINALIZE) ? launch_rowselect(es.out, rows, n, m, k, sink, local, idx, st) : FATHOM_OK;
   }
   Emit em{};
   int64_t S = 1;
@@ -845,16 +850,41 @@ extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D
   const int64_t r_hi = topk_hi_rank(n, S, kk, kRegTok);
   em.sink = sink;
   em.lstart = (m - local) > 0 ? (m - local) : 0;
-  a.wt_stride = S;
-  rc = launch_scan<kEmitSample>(a, topk_sample_tiles(n, S, kRegTok), BH, em, st);
-  if (rc) return rc;
-  rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, r_hi, em.sel, st);
-  if (rc) return rc;
-  a.wt_stride = 1;
-  // T_hi may exceed a row's kk-th largest key (r_hi < kk): the candidate pass
-  // then checks every row and rescans those with fewer than kk candidates
-  em.fallback_check = r_hi < kk ? 1 : 0;
-  rc = launch_scan<kEmitFilter>(a, nwt, BH, em, st);
-  if (rc) return rc;
-  return launch_finalize(rows, m, k, sink, local, em.sel, idx, st);
+  if (stages & FATHOM_STAGE_SAMPLE) {
+    a.wt_stride = S;
+    rc = launch_scan<kEmitSample>(a, topk_sample_tiles(n, S, kRegTok), BH, em, st);
+    if (rc) return rc;
+  }
+  if (stages & FATHOM_STAGE_SELECT) {
+    rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, r_hi, em.sel, st);
+    if (rc) return rc;
+  }
+  if (stages & FATHOM_STAGE_CANDIDATES) {
+    a.wt_stride = 1;
+    // T_hi may exceed a row's kk-th largest key (r_hi < kk): the candidate pass
+    // then checks every row and rescans those with fewer than kk candidates
+    em.fallback_check = r_hi < kk ? 1 : 0;
+    rc = launch_scan<kEmitFilter>(a, nwt, BH, em, st);
+    if (rc) return rc;
+  }
+  return (stages & FATHOM_STAGE_FINALIZE) ? launch_finalize(rows, m, k, sink, local, em.sel, idx, st) : FATHOM_OK;
+}
+}  // namespace
+}  // namespace fathom
+
+extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
+                                const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
+                                int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink,
+                                int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes, void *stream) {
+  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx,
+                       workspace, workspace_bytes, FATHOM_STAGE_ALL, stream);
+}
+
+extern "C" int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
+                                       const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
+                                       int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink,
+                                       int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes,
+                                       int stages, void *stream) {
+  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx,
+                       workspace, workspace_bytes, stages, stream);
 }

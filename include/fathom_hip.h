@@ -102,7 +102,8 @@ int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D,
  * out[bh, g, tok] = sum_j q[bh, g, j] * value_{t_j}(tok, j) over the channels of
  * the plan's depth classes 1..min(bmax, 4), for the 64-token blocks [blk0, blk1)
  * (tokens < n); other tokens of `out` are not written.
- *   q         [BH, G, D] float32, 1 <= G <= 8, D <= 256
+ *   q         [BH, G, D] float32, 1 <= G <= 8, D <= 128 (the reference's D = 128,
+ *             kernels/bitplane.py:313)
  *   cls, clsn from fathom_make_plan ([BH, bmax, D] and [BH, bmax] int32)
  *   planes_sb [BH, nsb, D, 4, sub] uint64, scales_sb [BH, nsb, D, sub] fp16
  *             (HBM, or mapped pinned host memory: the scan then reads over PCIe)
@@ -164,6 +165,27 @@ int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int
                      int bmax, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
                      int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/*
+ * The stages of fathom_scan_topk, run separately on one workspace: `stages` is
+ * a bitmask of FATHOM_STAGE_*; fathom_scan_topk runs FATHOM_STAGE_ALL, in the
+ * order sample, select, candidates, finalize.  A stage reads what the earlier
+ * stages left in the workspace, so a partial call repeats a later stage over
+ * the state of the last full one (same arguments).  Rows of at most 32768
+ * tokens have two stages only: candidates (the scores into the workspace) and
+ * finalize (the selection over them).  It exists for stage timing (bench.py
+ * times the candidate pass, the dominant kernel, on its own) and has no
+ * counterpart in the reference.
+ */
+#define FATHOM_STAGE_SAMPLE 1
+#define FATHOM_STAGE_SELECT 2
+#define FATHOM_STAGE_CANDIDATES 4
+#define FATHOM_STAGE_FINALIZE 8
+#define FATHOM_STAGE_ALL 15
+int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
+                            const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb, int64_t n,
+                            int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
+                            int64_t *idx, void *workspace, size_t workspace_bytes, int stages, void *stream);
 
 /*
  * sink_local_topk (kernels/bitplane.py:372-378; inline form with the current

@@ -49,14 +49,18 @@ Parity status per function (how each is pinned; the tests hold the checks):
   zero rows, recent-buffer rows), shift invariance, the one-hot limit.
 * klt_params: orthonormal basis, lam = variance of the rotated calibration keys,
   score invariance q.(k - mu) = (q Vt).((k - mu) Vt), ordering by w.
-* klt_query: the invariance above; GPU gains against it within fp32 tolerance.
+* klt_query: score invariance under a random non-symmetric orthonormal basis
+  (a transposed rotation fails it) and an explicit per-channel gain loop.
+* qblock: equals the plane-prefix dequantisation at fp32 scales (bit-exact), and
+  sketch_planes_scores equals the sum of per-level qblock contractions.
 * allocate: hand-worked example; brute-force optimum on convex equal-step tables
   (where greedy marginal allocation is optimal).
 * gather_runs / copy_index_runs: pure-Python word loops; the copy-index run
   list equals, slot by slot, the reference's offp/lenp/offs/lens formulas
   (hand-computed example in the tests), and scanning the staged copy equals
   scanning the full store (the reference's own PLANES_CHECK criterion).
-* sketch_planes_scores (CPU baseline): equals scan_planes on fp32-scaled codes.
+* sketch_planes_scores (CPU baseline): equals scan_planes on fp32-scaled codes;
+  oracle/sketch_torch.py (the torch restatement bench.py times) equals it.
 """
 import math
 

@@ -37,7 +37,39 @@ def test_capsio_reads_slices(tmp_path):
     assert torch.equal(f.get_slice("k0")[-1], t["k0"][-1])
     assert torch.equal(f["v3"], t["v3"]) and torch.equal(f.get_tensor("ids"), t["ids"])
     assert f.get_slice("k0")[3:3].shape == (0, 300, 128)
+    assert torch.equal(f.get_slice("q0")[30:], t["q0"][30:]) and torch.equal(f.get_slice("v3")[..., 2], t["v3"][..., 2])
+    assert torch.equal(f.get_slice("ids")[1:9:3], t["ids"][1:9:3])
+    assert f.metadata_dict() == {"model": "synthetic"}
     f.close()
+
+
+def test_capsio_rejects_malformed_headers(tmp_path):
+    import json
+    import struct
+    from safetensors.torch import save_file
+    path = tmp_path / "x.safetensors"
+    save_file({"a": torch.zeros(4, 3)}, str(path))
+    raw = path.read_bytes()
+    hlen = struct.unpack("<Q", raw[:8])[0]
+    hdr = json.loads(raw[8:8 + hlen])
+
+    def write(h, body):
+        b = json.dumps(h).encode()
+        path.write_bytes(struct.pack("<Q", len(b)) + b + body)
+
+    body = raw[8 + hlen:]
+    write(dict(hdr, a=dict(hdr["a"], data_offsets=[0, 64])), body)      # range past the file
+    with pytest.raises(ValueError):
+        capsio.safe_open(str(path))
+    write(dict(hdr, a=dict(hdr["a"], shape=[4, 4])), body)              # bytes != shape * dtype
+    with pytest.raises(ValueError):
+        capsio.safe_open(str(path))
+    write(dict(hdr, a=dict(hdr["a"], dtype="C64")), body)               # unknown dtype
+    with pytest.raises(ValueError):
+        capsio.safe_open(str(path))
+    path.write_bytes(struct.pack("<Q", 1 << 40))                        # header longer than the file
+    with pytest.raises(ValueError):
+        capsio.safe_open(str(path))
 
 
 def test_chunk_bounds():

@@ -481,8 +481,90 @@ def test_klt_basis_identities():
         assert (np.diff(p["w"][b]) <= 0).all()
         q = rng.standard_normal((3, d))
         np.testing.assert_allclose((q @ V) @ (Kc @ V).T, q @ Kc.T, rtol=1e-9, atol=1e-9)
-    qr, g = O.klt_query(Q[:, :4], p["Vt"], p["lam"])
-    np.testing.assert_allclose(g, (qr ** 2 * p["lam"][:, None]).sum(1))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_klt_query_invariance_and_gain_loop(seed):
+    """klt_query against what the rotation fixes (scripts/R_ruler.py:82-84):
+    with any orthonormal, non-symmetric basis Vt, the rotated query scores the
+    rotated centred keys exactly as q scores the centred keys, and the gains are
+    sum_g qr^2 lam by an explicit loop.  A transposed rotation breaks the first."""
+    rng = np.random.default_rng(seed)
+    BH, G, d, n = 2, 3, 12, 50
+    Vt = np.stack([np.linalg.qr(rng.standard_normal((d, d)))[0] for _ in range(BH)])
+    assert not np.allclose(Vt[0], Vt[0].T)
+    lam = rng.random((BH, d)) + 0.1
+    q = rng.standard_normal((BH, G, d))
+    k = rng.standard_normal((BH, n, d)) * 3
+    mu = rng.standard_normal((BH, d))
+    qr, gain = O.klt_query(q, Vt, lam)
+    for b in range(BH):
+        kr = (k[b] - mu[b]) @ Vt[b]                      # the store's rotation of the keys
+        np.testing.assert_allclose(qr[b] @ kr.T, q[b] @ (k[b] - mu[b]).T, rtol=1e-10, atol=1e-10)
+        bad = (q[b] @ Vt[b].T) @ kr.T                    # the query rotated the other way
+        assert not np.allclose(bad, q[b] @ (k[b] - mu[b]).T, atol=1e-3)
+        for e in range(d):
+            acc = 0.0
+            for g in range(G):
+                qe = sum(q[b, g, j] * Vt[b, j, e] for j in range(d))
+                acc += qe * qe * lam[b, e]
+            assert abs(gain[b, e] - acc) <= 1e-12 * max(1.0, abs(acc))
+
+
+# ----------------------------------------------------------------------------- CPU scorer (sketch)
+def test_qblock_is_the_quantiser_at_fp32_scales():
+    """sketch.qblock (scripts/sketch.py:8-17) at t bits equals the depth-t
+    dequantisation of the 4-bit codes quantised with fp32 block scales (the
+    prefix theorem with fp32 absmax), and a 0-bit column is dropped."""
+    rng = np.random.default_rng(7)
+    n, d = 150, 10
+    x = (rng.standard_normal((n, d)) * np.exp(rng.standard_normal(d))).astype(np.float32)
+    code, sc = O.quantise_u4(x, "f32")
+    for t in range(1, 5):
+        np.testing.assert_array_equal(O.qblock(x, np.full(d, t)), O.dequant_planes(code, sc, t))
+    bits = np.array([4, 0, 2, 1, 0, 3, 4, 4, 1, 2])
+    out = O.qblock(x, bits)
+    assert (out[:, bits == 0] == 0).all()
+    for j in range(d):
+        if bits[j]:
+            np.testing.assert_array_equal(out[:, j], O.dequant_planes(code, sc, bits[j])[:, j])
+
+
+def test_sketch_scores_are_qblock_level_sums():
+    """The CPU scorer is the sum over depth levels of the level's channels of q
+    times the qblock quantisation at that level (scripts/sketch.py:122-130)."""
+    rng = np.random.default_rng(8)
+    n, d, G = 260, 24, 2
+    k = (rng.standard_normal((n, d)) * np.exp(rng.standard_normal(d))).astype(np.float32)
+    q = rng.standard_normal((G, d)).astype(np.float32)
+    var = k[16:].var(0, ddof=1)
+    s, t = O.sketch_planes_scores(q, k, var, 30)
+    ref = np.zeros((G, n))
+    for lvl in range(1, 5):
+        m = (t == lvl)
+        if m.any():
+            ref += (q * m[None]).astype(np.float64) @ O.qblock(k, np.full(d, lvl)).T.astype(np.float64)
+    np.testing.assert_allclose(s, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
+def test_torch_cpu_scorer_matches_oracle():
+    """The torch restatement timed as the CPU baseline (oracle/sketch_torch.py)
+    against the numpy oracle: same depths, scores within fp32 summation noise,
+    same top-k on tie-free scores."""
+    import torch
+    from oracle import sketch_torch as ST
+    from fathom_amd import workloads as W
+    x = W.config_inputs(1, n=4096)
+    k = x["K"][0].float()
+    q = x["q"][0]
+    var = x["var"][0]
+    s_np, t_np = O.sketch_planes_scores(q.numpy(), k.numpy(), var.numpy(), x["budget"])
+    s_t, t_t = ST.planes_scores(q, k, var, x["budget"])
+    np.testing.assert_array_equal(t_t.numpy(), t_np)
+    np.testing.assert_allclose(s_t.numpy(), s_np, rtol=1e-5, atol=1e-5 * np.abs(s_np).max())
+    idx_t = ST.sink_local_topk(s_t, 128, 4, 64)
+    idx_o = O.sink_local_topk(s_t.numpy()[None], 128, 4, 64)[0]
+    np.testing.assert_array_equal(np.sort(idx_t.numpy(), -1), np.sort(idx_o, -1))
 
 
 def test_allocate_worked_example():
