@@ -672,7 +672,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 
         if (tid == 0) s_last = atomicAdd(em.sel.cnt2(bh * a.G), 1u) == gridDim.x - 1 ? 1u : 0u;
         __syncthreads();
         if (!s_last) return;  // uniform
-        if (tid < a.G) s_tot[tid] = atomicAdd(em.sel.cnt1(bh * a.G + tid), 0u);
+        // every other workgroup of the row has added its totals and counted
+        // itself done: take the totals and leave both counters at zero, so a
+        // candidate pass run again on its own (the stage entry point) starts
+        // from the state the selection kernel leaves
+        if (tid < a.G) s_tot[tid] = atomicExch(em.sel.cnt1(bh * a.G + tid), 0u);
+        if (tid == 0) atomicExch(em.sel.cnt2(bh * a.G), 0u);
         __syncthreads();
         for (int g = 0; g < a.G; ++g) skipm |= (s_tot[g] >= em.sel.kk ? 1u : 0u) << g;
         if (skipm == (1u << a.G) - 1u) return;  // uniform: the common case

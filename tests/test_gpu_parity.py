@@ -539,6 +539,44 @@ def test_scan_topk_fallback_pass(direction, n):
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("fallback", [False, True])
+def test_scan_topk_stages_repeat(fallback):
+    """The stage entry point: the stages run one by one on one workspace, and the
+    candidate pass run again on its own over the state the last full call left
+    (the way bench.py times it), give the fused call's indices -- also for rows
+    whose tight threshold falls short, where the candidate pass's own fallback
+    check must see this pass's totals, not the sum over repeats."""
+    print(f"[fused-stages] fallback={fallback}", flush=True)
+    if fallback:
+        BH, d, n = 2, 128, 90000
+        K = torch.zeros(BH, n, d)
+        K[:, :, 0] = torch.linspace(3, -3, n)[None]
+        K[:, :, 1] = torch.randn(BH, n, generator=torch.Generator().manual_seed(3)) * 0.01
+        st = bp.PlaneStore(K.to(DEV))
+        q = torch.zeros(BH, 4, d)
+        q[:, :, 0] = 1.0
+        q[:, 1::2, 1] = 1.0
+        g = torch.ones(BH, d)
+        g[:, 0], g[:, 1] = 1000.0, 10.0
+        q, plan = q.to(DEV), bp.make_plan(g.to(DEV), 6.0)
+        sink, local = 4, 32
+    else:
+        x, st, plan = _scan_case(2, 100000, 2)
+        q, sink, local = x["q"].to(DEV), x["sink"], x["local"]
+    ref = bp.sink_local_topk(st.scan(q, plan), 512, sink, local)
+    idx, ws = None, None
+    for stage in (bp.STAGE_SAMPLE, bp.STAGE_SELECT, bp.STAGE_CANDIDATES, bp.STAGE_FINALIZE):
+        idx, ws = st.scan_topk_stages(q, plan, 512, stage, ws, idx, sink, local)
+    torch.testing.assert_close(idx, ref, rtol=0, atol=0)
+    for rep in range(3):
+        for _ in range(rep + 1):
+            st.scan_topk_stages(q, plan, 512, bp.STAGE_CANDIDATES, ws, idx, sink, local)
+        idx.fill_(-1)
+        st.scan_topk_stages(q, plan, 512, bp.STAGE_FINALIZE, ws, idx, sink, local)
+        torch.testing.assert_close(idx, ref, rtol=0, atol=0, msg=f"repeat {rep}")
+    torch.testing.assert_close(st.scan_topk(q, plan, 512, sink, local), ref, rtol=0, atol=0)
+
+
 def test_scan_topk_graph_replays():
     """The fused call captured in a HIP graph (as bench.py times it): every replay,
     with eager work and synchronisations between replays, equals the eager call."""
