@@ -37,6 +37,8 @@ PROTOTYPES = {
                                 _i64, _vp, _vp, _sz, _vp]),
     "fathom_scan_topk_stages": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _i64, _vp, _vp, _sz, _i32, _vp]),
+    "fathom_scan_topk_noalloc": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                        _i64, _i64, _vp, _vp]),
     "fathom_topk_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "fathom_sink_local_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "fathom_gather_rows": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),

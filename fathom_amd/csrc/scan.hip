@@ -47,6 +47,7 @@
 // dword per lane and unit: 64 lanes read the unit's 16 blocks as one 128-byte
 // run of a superblock store.
 #include "topk_internal.hpp"
+#include "scan_internal.hpp"
 
 namespace fathom {
 namespace {
@@ -794,7 +795,6 @@ extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t
 }
 
 namespace fathom {
-namespace {
 // Workspace of the fused scan + top-k: rows up to kRowSelectMax keep their
 // scores ([rows, n] fp32) for one row-select launch; longer rows the sampled
 // keys and the candidate regions.
@@ -802,7 +802,6 @@ size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k) {
   if (n <= kRowSelectMax) return ws_align((size_t)rows * (size_t)n * 4);
   return topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
-}  // namespace
 }  // namespace fathom
 
 extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink,
@@ -813,7 +812,6 @@ extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_
 }
 
 namespace fathom {
-namespace {
 int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
                   const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m,
                   int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes,
@@ -874,7 +872,6 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   }
   return (stages & FATHOM_STAGE_FINALIZE) ? launch_finalize(rows, m, k, sink, local, em.sel, idx, st) : FATHOM_OK;
 }
-}  // namespace
 }  // namespace fathom
 
 extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,

@@ -188,6 +188,24 @@ int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, co
                             int64_t *idx, void *workspace, size_t workspace_bytes, int stages, void *stream);
 
 /*
+ * fathom_scan_topk without a workspace argument, for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * The workspace is a static device array of the library, of
+ * FATHOM_NOALLOC_SCRATCH_BYTES, one per device that calls it (held until the
+ * process ends); shapes whose fathom_scan_topk_workspace_bytes exceed it are
+ * rejected with FATHOM_ERR_WORKSPACE before any launch.  The call allocates
+ * nothing (no hipMalloc, no library allocation).  Calls that overlap on one
+ * device (several streams or threads) share the array and race.  Results are
+ * those of fathom_scan_topk on the same arguments.
+ */
+#define FATHOM_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
+                             const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb, int64_t n,
+                             int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
+                             int64_t *idx, void *stream);
+
+/*
  * sink_local_topk (kernels/bitplane.py:372-378; inline form with the current
  * length m at scripts/B_e2e_offload_v2.py:224-227).  For each of `rows` rows of
  * scores [rows, n] float32: mask [0, sink) and [max(m - local, 0), n) to -inf,

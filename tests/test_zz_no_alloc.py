@@ -1,0 +1,79 @@
+"""fathom_scan_topk_noalloc (the fused scan + top-k on the library's static
+scratch array) against fathom_scan_topk on a caller workspace: the same index
+sets, bit for bit, on consecutive calls whose shapes shrink (the array keeps
+the previous call's state), on both the candidate-chain and the row-select
+paths; shapes past the array are refused before any launch; the calls after
+the first change no device memory."""
+import ctypes
+
+import pytest
+import torch
+
+from fathom_amd import _lib
+from fathom_amd import bitplane as bp
+from fathom_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+SCRATCH = 64 << 20  # FATHOM_NOALLOC_SCRATCH_BYTES
+
+
+def _case(BH, G, n, seed):
+    x = W.synth_layer(BH, n, G, seed=seed)
+    g = ((x["q"] ** 2) * x["var"][:, None, :]).sum(1)
+    st = bp.PlaneStore(x["K"].to(DEV))
+    plan = bp.make_plan(g.to(DEV), 56.0)
+    return st, plan, x["q"].to(DEV).float().contiguous()
+
+
+def _noalloc(st, plan, q, k, sink, local, m, idx):
+    BH, G, d = q.shape
+    cls, clsn = bp._plan_classes(plan, BH, d)
+    rc = _lib.lib().fathom_scan_topk_noalloc(
+        bp._ptr(q), BH, G, d, bp._ptr(cls), bp._ptr(clsn), cls.shape[1], ctypes.c_void_p(st.planes32.data_ptr()),
+        ctypes.c_void_p(st.scales_k.data_ptr()), st.n, int(st.nsb), int(getattr(st, "sub", bp.SUB)), m, k, sink, local, bp._ptr(idx),
+        bp._stream(q.device))
+    _lib.check(rc, "fathom_scan_topk_noalloc")
+    return idx
+
+
+def test_noalloc_equals_workspace_entry_on_shrinking_calls():
+    # (BH, G, n, k, sink, local, m): the chain path twice, the second call
+    # smaller, then the row-select path (n <= 32768) on the same array
+    cases = [(2, 4, 200_000, 512, 4, 32, None), (1, 3, 70_001, 256, 4, 64, 70_010), (2, 7, 20_000, 300, 4, 32, None)]
+    prepared = []
+    for i, (BH, G, n, k, sink, local, m) in enumerate(cases):
+        print(f"[noalloc] prepare BH={BH} G={G} n={n} k={k}", flush=True)
+        st, plan, q = _case(BH, G, n, seed=31 + i)
+        m = n if m is None else m
+        ref = st.scan_topk(q, plan, k, sink, local, m=m)
+        assert _lib.lib().fathom_scan_topk_workspace_bytes(BH, G, n, k, sink, local) <= SCRATCH
+        prepared.append((st, plan, q, k, sink, local, m, ref, torch.full_like(ref, -1)))
+    torch.cuda.synchronize()
+    for st, plan, q, k, sink, local, m, ref, idx in prepared:
+        print(f"[noalloc] call BH={q.shape[0]} G={q.shape[1]} n={st.n} k={k}", flush=True)
+        _noalloc(st, plan, q, k, sink, local, m, idx)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(idx, ref, rtol=0, atol=0)
+    # once the array is resident, calls take no device memory
+    free0 = torch.cuda.mem_get_info()[0]
+    for st, plan, q, k, sink, local, m, ref, idx in prepared:
+        idx.fill_(-1)
+        _noalloc(st, plan, q, k, sink, local, m, idx)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(idx, ref, rtol=0, atol=0)
+    assert torch.cuda.mem_get_info()[0] == free0
+
+
+def test_noalloc_refuses_shapes_past_the_array():
+    L = _lib.lib()
+    need = L.fathom_scan_topk_workspace_bytes(8, 4, 1 << 20, 512, 4, 32)
+    assert need > SCRATCH
+    null = ctypes.c_void_p(0)
+    rc = L.fathom_scan_topk_noalloc(null, 8, 4, 128, null, null, 4, null, null, 1 << 20, (1 << 20) // 1024, 16,
+                                    1 << 20, 512, 4, 32, null, null)
+    assert rc == _lib.ERR_WORKSPACE
+    assert b"static array holds" in L.fathom_last_error()
+    rc = L.fathom_scan_topk_noalloc(null, 8, 9, 128, null, null, 4, null, null, 4096, 4, 16, 4096, 64, 4, 32, null,
+                                    null)
+    assert rc == _lib.ERR_INVALID
