@@ -12,11 +12,16 @@ the same steps; the unfused pair must select the same indices.
 `value` counts scanned token*heads per second of scan + top-k with the index
 resident in HBM (n * BH / t_scan_topk, t_scan_topk the GPU time of one fused
 call: 20 calls captured in one HIP graph, checked equal to the eager call).
-The roofline object is for the scan kernel (one launch timed the same way,
-algorithmic bytes = bytes_planes).  The same step with the
-plane index and the K/V rows in mapped pinned host memory (the scan reads over
-PCIe) is reported under "host_resident", and config 5's full decode step (36
-layers, batch 4 x 8 KV heads, n = 32768, per-layer budgets) under "decode_step".
+The roofline object is for the dominant kernel of that call, the candidate
+pass (scan_wave_kernel<1, 2>), run on its own through the stage entry point
+(20 launches in one HIP graph, events on the launching stream; algorithmic
+bytes = bytes_planes), with the whole call's and the whole step's fractions
+and the instruction-issue ceiling beside it.  The same step with the plane
+index and the K/V rows in mapped pinned host memory (the scan reads over PCIe)
+is reported under "host_resident", and config 5's full decode step (36 layers,
+batch 4 x 8 KV heads, n = 32768, per-layer budgets) under "decode_step".  Every
+index set measured (host-resident, copy-index, pipelined, graph replays) must
+equal the HBM path's, or the run raises.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-host] [--no-cpu]
 """
@@ -32,6 +37,10 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
 PCIE_PEAK_GBPS = 64.0         # PCIe 5.0 x16, per direction
+SIMDS = 256 * 4               # MI355X: 256 CUs x 4 SIMDs
+CLOCK_HZ = 2.4e9              # MI355X peak engine clock
+VALU_CYCLES = 4               # a wave64 VALU instruction occupies a 16-lane SIMD 4 cycles
+CAND_KERNEL = "scan_wave_kernel<1, 2>"
 
 
 def parse():
@@ -367,40 +376,134 @@ def run_config4(torch, bp, W, dev):
             "runs": res}
 
 
-def cpu_baseline(x_cpu, reps=3):
-    """The oracle's port of the reference CPU scorer (scripts/sketch.py:110-131 planes
-    branch + exact top-k) on one KV head of the same distribution, 1 thread."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
-    from oracle import fathom_oracle as O
+def run_stages(torch, bp, store, x, plan, ref_idx):
+    """GPU time of each stage of the fused call (sample, select, candidates,
+    finalize), each repeated over the state of one full call on one workspace
+    (20 launches in one HIP graph).  The indices after the repeats must equal
+    the fused call's."""
+    q, k, sink, local = x["q"], x["k"], x["sink"], x["local"]
+    idx, ws = store.scan_topk_stages(q, plan, k, bp.STAGE_ALL, sink=sink, local=local)
+    torch.cuda.synchronize()
+    if not bool(torch.equal(idx, ref_idx)):
+        raise RuntimeError("stage entry point (all stages) disagrees with the fused call")
+    ms = {}
+    for name, stage in (("sample", bp.STAGE_SAMPLE), ("select", bp.STAGE_SELECT),
+                        ("candidates", bp.STAGE_CANDIDATES), ("finalize", bp.STAGE_FINALIZE)):
+        ms[name] = _graph_ms(torch, lambda stage=stage: store.scan_topk_stages(q, plan, k, stage, ws, idx, sink, local))
+    idx.fill_(-1)
+    store.scan_topk_stages(q, plan, k, bp.STAGE_CANDIDATES | bp.STAGE_FINALIZE, ws, idx, sink, local)
+    torch.cuda.synchronize()
+    if not bool(torch.equal(idx, ref_idx)):
+        raise RuntimeError("repeated candidate passes changed the selected indices")
+    return ms
 
-    K = x_cpu["K"][0].float().numpy()
-    q = x_cpu["q"][0].numpy()
-    var = x_cpu["var"][0].numpy()
-    n = K.shape[0]
-    times = []
-    with threadpool_limits(limits=1):
-        for _ in range(reps + 1):
-            t0 = time.perf_counter()
-            s, _ = O.sketch_planes_scores(q, K, var, x_cpu["budget"])
-            O.sink_local_topk(s[None], x_cpu["k"], x_cpu["sink"], x_cpu["local"])
-            times.append(time.perf_counter() - t0)
-    med = statistics.median(times[1:])
-    return {"value": n / med, "unit": "scanned tokens/s", "cores": 1, "kind": "port",
-            "sample": f"1 KV head x {n} tokens x G={q.shape[0]} of the same synthetic distribution, "
-                      f"oracle sketch-planes scorer (B={x_cpu['budget']:g}) + exact sink/local top-k, "
-                      f"median of {reps} after 1 warm-up, {med:.2f} s each"}
+
+def run_step_graph(torch, bp, off, x, store, K, V, ref_idx):
+    """GPU time of one whole step (make_plan -> fused scan + top-k -> attention
+    over the gathered rows, all 8 KV heads) as a HIP graph; its indices must
+    equal the eager step's."""
+    q = x["q"]
+    box = {}
+
+    def step():
+        plan = bp.make_plan(x["g"], x["budget"])
+        box["idx"] = store.scan_topk(q, plan, x["k"], x["sink"], x["local"])
+        box["out"] = off.gather_attention(q, box["idx"], x["n"], K, V, x["n"])
+        return box["idx"]
+
+    ms, idx = _graph_run(torch, step)
+    if not bool(torch.equal(idx, ref_idx)):
+        raise RuntimeError("graph-replayed step disagrees with the eager step")
+    return ms
+
+
+def _profile_lines(name):
+    p = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(p):
+        return {}
+    out = {}
+    for line in open(p):
+        if ":" in line and not line.startswith(("|", "#", " ")):
+            key, val = line.split(":", 1)
+            try:
+                out[key.strip()] = float(val.split()[0])
+            except (ValueError, IndexError):
+                pass
+    return out
 
 
 def read_traffic():
-    """HBM bytes per scan launch measured by rocprofv3 --pmc (committed summary), or None."""
-    p = os.path.join(ROOT, "profiles", "scan_c3_hbm_traffic.md")
-    if not os.path.exists(p):
+    """HBM bytes per candidate-pass launch from rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE (committed summary, scaled by the copy-kernel calibration), or None."""
+    return _profile_lines("scan_c3_candidate_hbm_traffic.md").get("traffic_bytes_per_launch")
+
+
+def issue_ceiling(scan_bytes, blockrows, achieved):
+    """Instruction-issue ceiling of the candidate pass from its committed
+    rocprofv3 --pmc counts (per launch): the VALU instructions other than MFMA
+    occupy a SIMD VALU_CYCLES cycles each, the MFMAs their measured busy
+    cycles; spread evenly over the chip's SIMDs at the peak clock, the larger
+    of the two is the shortest time the launch could take, and
+    algorithmic bytes / that time the highest rate it could reach."""
+    c = _profile_lines("scan_c3_candidate_counters.md")
+    if not {"SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES"} <= set(c):
         return None
-    for line in open(p):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":")[1])
-    return None
+    valu, mfma = c["SQ_INSTS_VALU"], c["SQ_INSTS_MFMA"]
+    valu_s = VALU_CYCLES * (valu - mfma) / (SIMDS * CLOCK_HZ)
+    mfma_s = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (SIMDS * CLOCK_HZ)
+    t = max(valu_s, mfma_s)
+    ceil = scan_bytes / t / 1e9
+    return {"valu_per_block_row": valu / blockrows, "mfma_per_block_row": mfma / blockrows,
+            "salu_per_block_row": c.get("SQ_INSTS_SALU", 0.0) / blockrows,
+            "valu_issue_us": valu_s * 1e6, "mfma_busy_us": mfma_s * 1e6,
+            "ceiling_GBps": ceil, "frac_of_ceiling": achieved / ceil,
+            "source": "profiles/scan_c3_candidate_counters.md (per-launch counts, C3 shape)"}
+
+
+def cpu_baseline(W):
+    """The reference's torch CPU path (scripts/sketch.py:110-131 planes branch:
+    water-filling plan + per-level qblock contraction; then the exact sink/local
+    top-k with torch.topk), restated in oracle/sketch_torch.py, on one KV head
+    (G query heads) of the same synthetic distribution: the C3 shape at all
+    threads and, bounded, a quarter of it at 1 thread; C1 at both."""
+    import torch
+    from oracle import sketch_torch as S
+
+    threads_all = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        threads_all = min(threads_all, int(env))  # the box's CPU share
+    saved = torch.get_num_threads()
+
+    def timed(x, threads, reps=5):
+        torch.set_num_threads(threads)
+        K, q, var = x["K"][0].float(), x["q"][0].float(), x["var"][0].float()
+        ts = []
+        for _ in range(reps + 1):
+            t0 = time.perf_counter()
+            S.scan_topk(q, K, var, x["budget"], x["k"], x["sink"], x["local"])
+            ts.append(time.perf_counter() - t0)
+        med = statistics.median(ts[1:])
+        return {"tokens_per_s": K.shape[0] / med, "s": med, "n": K.shape[0], "G": q.shape[0], "threads": threads}
+
+    try:
+        x3 = W.config_inputs(3, device="cpu", BH=1)
+        c3_all = timed(x3, threads_all)
+        del x3
+        x3q = W.config_inputs(3, device="cpu", BH=1, n=1 << 18)
+        c3_one = timed(x3q, 1)
+        del x3q
+        x1 = W.config_inputs(1, device="cpu")
+        c1_all, c1_one = timed(x1, threads_all), timed(x1, 1)
+    finally:
+        torch.set_num_threads(saved)
+    return {"value": c3_all["tokens_per_s"], "unit": "token*heads/s", "cores": threads_all, "kind": "port",
+            "sample": f"torch restatement of scripts/sketch.py:110-131 + torch.topk sink/local top-k, one KV head "
+                      f"(G={c3_all['G']}) x {c3_all['n']} tokens of the C3 distribution, B=48, k=512, "
+                      f"torch.set_num_threads({threads_all}) (os.cpu_count()={os.cpu_count()}), "
+                      f"median of 5 after 1 warm-up: {c3_all['s']:.3f} s",
+            "single_thread": dict(c3_one, sample="C3 distribution, 262144 tokens (a quarter of the C3 row), 1 thread"),
+            "config1": {"all_threads": c1_all, "single_thread": c1_one}}
 
 
 def main():
@@ -438,10 +541,15 @@ def main():
     value = n * BH / (scan_topk_ms * 1e-3)
     scores = torch.empty(BH, x["G"], n, device=dev)
     scan_ms = _graph_ms(torch, lambda: store.scan(x["q"], hbm["plan"], out=scores))
-    achieved = hbm["scan_bytes"] / (scan_ms * 1e-3) / 1e9
     del scores
+    fused_stage_ms = run_stages(torch, bp, store, x, hbm["plan"], hbm["idx"])
+    cand_ms = fused_stage_ms["candidates"]
+    achieved = hbm["scan_bytes"] / (cand_ms * 1e-3) / 1e9
+    step_ms = None if a.stages_only else run_step_graph(torch, bp, off, x, store, x["K"], V, hbm["idx"])
     log(f"[bench] HBM: stages {json.dumps({k: round(v, 4) for k, v in st.items()})} ms, "
-        f"{hbm['bits_per_token']:.2f} bits/token, scan {achieved:.1f} GB/s, fused (graph) {scan_topk_ms:.4f} ms")
+        f"{hbm['bits_per_token']:.2f} bits/token, fused (graph) {scan_topk_ms:.4f} ms, "
+        f"fused stages {json.dumps({k: round(v, 4) for k, v in fused_stage_ms.items()})} ms, "
+        f"candidate pass {achieved:.1f} GB/s, step (graph) {step_ms} ms")
 
     host = None
     if not a.no_host and not a.stages_only:
@@ -460,6 +568,8 @@ def main():
             hstore.planes32, hstore.scales_k = pl_dev, sc_dev
             hr = run_regime(torch, bp, off, x, hstore, K_dev, V_dev, max(3, a.steps // 2), 2)
             same = bool(torch.equal(hr["idx"], hbm["idx"]))
+            if not same:
+                raise RuntimeError("host-resident (zero-copy) index sets differ from the HBM path's")
             hs = hr["stage_ms"]
             tot = hs["plan"] + hs["scan_topk"] + hs["attn"]
             pcie_bytes = hr["scan_bytes"] + hr["row_bytes"]
@@ -476,6 +586,10 @@ def main():
             torch.cuda.synchronize()
             h2d = 4 * src.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9
             ci = run_copy_index(torch, bp, off, x, K_dev, V_dev, max(3, a.steps // 2), 2)
+            if not bool(torch.equal(ci["idx"], hbm["idx"])):
+                raise RuntimeError("copy-index index sets differ from the HBM path's")
+            if not bool(torch.equal(ci["pipelined_idx"], hbm["idx"])):
+                raise RuntimeError("pipelined (4-chunk) index sets differ from the HBM path's")
             cs = ci["stage_ms"]
             ci_tot = cs["plan"] + cs["copy"] + cs["scan_topk"] + cs["attn"]
             ci_bytes = ci["scan_bytes"] + ci["row_bytes"]
@@ -535,8 +649,7 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        xs = W.config_inputs(a.config, device="cpu", n=min(x["n"], 1 << 20), BH=1)
-        cpu = cpu_baseline(xs, reps=5)
+        cpu = cpu_baseline(W)
         log(f"[bench] cpu baseline: {json.dumps(cpu)}")
 
     rec = {
@@ -551,11 +664,22 @@ def main():
         "scan_topk_ms": scan_topk_ms,
         "scan_topk_timing": "20 fused calls captured in one HIP graph, 3 replays (eager per-stage time: stage_ms)",
         "unfused_scan_plus_topk_ms": st["scan"] + st["topk"],
-        "roofline": {"bound": "hbm", "kernel": "scan_tile_kernel<4, 0> (PlaneStore.scan)", "achieved": achieved,
-                     "launch_ms": scan_ms,
-                     "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
-                     "algorithmic_bytes_per_launch": hbm["scan_bytes"]},
+        "roofline": {"bound": "hbm", "kernel": CAND_KERNEL + " (candidate pass of the fused scan + top-k)",
+                     "achieved": achieved, "launch_ms": cand_ms, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
+                     "algorithmic_bytes_per_launch": hbm["scan_bytes"],
+                     "timing": "stage entry point, candidate pass alone, 20 launches in one HIP graph, 3 replays",
+                     "issue_ceiling": issue_ceiling(hbm["scan_bytes"], BH * -(-n // 64), achieved),
+                     "whole_call": {"ms": scan_topk_ms, "GBps": hbm["scan_bytes"] / (scan_topk_ms * 1e-3) / 1e9,
+                                    "frac": hbm["scan_bytes"] / (scan_topk_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                                    "stage_ms": {k: round(v, 5) for k, v in fused_stage_ms.items()}},
+                     "step": None if step_ms is None else {
+                         "ms": step_ms, "bytes": hbm["scan_bytes"] + hbm["row_bytes"],
+                         "GBps": (hbm["scan_bytes"] + hbm["row_bytes"]) / (step_ms * 1e-3) / 1e9,
+                         "frac": (hbm["scan_bytes"] + hbm["row_bytes"]) / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                         "what": "make_plan + fused scan/top-k + attention over the union-gathered rows, one HIP "
+                                 "graph; bytes = plane/scale bytes + distinct K/V rows"},
+                     "scores_mode_scan_ms": scan_ms},
         "host_resident": host,
         "decode_step": decode,
         "kernel_table": ktab,

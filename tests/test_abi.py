@@ -59,3 +59,26 @@ def test_python_api_rejects_host_tensors():
         bp.quantise_u4(torch.zeros(2, 64, 128))
     with pytest.raises(ValueError, match="GPU"):
         bp.make_plan(torch.ones(2, 128), 48)
+
+
+def test_host_mapped_allocation_failure_raises_memory_error():
+    """A pinned mapped allocation that cannot be satisfied (here 4 PiB) becomes
+    MemoryError with the library's message, and nothing is leaked or mapped."""
+    from fathom_amd import offload as off
+
+    class Huge:  # stands in for a tensor too large to pin; host_mapped reads only these
+        dtype = torch.float32
+
+        def numel(self):
+            return 1 << 50
+
+        def element_size(self):
+            return 4
+
+    with pytest.raises(MemoryError, match="hipHostMalloc"):
+        off.host_mapped(Huge())
+    hp, dp = ctypes.c_void_p(), ctypes.c_void_p()
+    rc = _lib.lib().fathom_host_alloc_mapped(1 << 52, 1, ctypes.byref(hp), ctypes.byref(dp))
+    assert rc == _lib.ERR_ALLOC and hp.value is None and dp.value is None
+    with pytest.raises(MemoryError):
+        _lib.check(rc, "fathom_host_alloc_mapped")
