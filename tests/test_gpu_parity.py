@@ -116,6 +116,16 @@ def test_make_plan_bitexact(d, bmax):
         np.testing.assert_array_equal(got[key].cpu().numpy(), ref[key], err_msg=key)
 
 
+def test_make_plan_torch_is_the_plan_depths():
+    """make_plan_torch (the reference's torch plan, kernels/bitplane.py:118-126):
+    the float depths [BH, D] of make_plan, equal to the oracle's plan."""
+    x = W.config_inputs(2, n=128, BH=4)
+    t = bp.make_plan_torch(x["g"].to(DEV), x["budget"])
+    assert t.dtype == torch.float32 and tuple(t.shape) == (4, 128)
+    np.testing.assert_array_equal(t.cpu().numpy(), O.make_plan(x["g"].numpy(), x["budget"])["t"].astype(np.float32))
+    assert torch.equal(t, bp.make_plan(x["g"].to(DEV), x["budget"])["t"].float())
+
+
 def test_make_plan_scalar_budget_and_iters():
     rng = np.random.default_rng(9)
     g = np.exp(rng.standard_normal((8, 128)) * 2).astype(np.float32)
@@ -351,6 +361,52 @@ def test_gather_union_matches_oracle(host):
         np.testing.assert_array_equal(Ks.cpu().view(torch.int16).numpy(), rK)
         np.testing.assert_array_equal(Vs.cpu().view(torch.int16).numpy(), rV)
         np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
+    finally:
+        for h in hps:
+            off.free_host(h)
+
+
+@pytest.mark.parametrize("host", [False, True])
+def test_select_and_gather_matches_oracle(host):
+    """select_and_gather (one decode step's selection, scripts/B_e2e_offload_v2.py:
+    181, 203, 224-241) over an HBM or host-resident store: plan, scores, indices
+    and union rows against the oracle (indices given the GPU scores, rows given
+    the indices)."""
+    print(f"[select_and_gather] host={host}", flush=True)
+    x = W.config_inputs(2, n=40000, BH=2)
+    K = x["K"]
+    V = W.synth_values(2, x["n"])
+    st = bp.PlaneStore(K.to(DEV))
+    hps = []
+    try:
+        if host:
+            _, pl, h = off.host_mapped(st.planes_k)
+            hps.append(h)
+            _, sc, h = off.host_mapped(st.scales_k)
+            hps.append(h)
+            st.planes32, st.scales_k = pl, sc
+            _, Ksrc, h = off.host_mapped(K)
+            hps.append(h)
+            _, Vsrc, h = off.host_mapped(V)
+            hps.append(h)
+        else:
+            Ksrc, Vsrc = K.to(DEV), V.to(DEV)
+        r = off.select_and_gather(st, x["q"].to(DEV), x["var"].to(DEV), x["budget"], 512, Ksrc, Vsrc,
+                                  x["sink"], x["local"])
+        torch.cuda.synchronize()
+        qd, vd = x["q"].to(DEV).float(), x["var"].to(DEV)
+        g = ((qd ** 2) * vd[:, None, :]).sum(1)          # the gain as select_and_gather forms it
+        pr = O.make_plan(g.cpu().numpy(), x["budget"])
+        np.testing.assert_array_equal(r["plan"]["t"].cpu().numpy(), pr["t"])
+        code, scl = O.quantise_u4(K.float().numpy())
+        ref_s = O.scan_planes(x["q"].numpy(), code, scl.astype(np.float16).astype(np.float32), pr["t"])
+        _scores_close(r["scores"].cpu().numpy(), ref_s)
+        idx = r["idx"].cpu().numpy()
+        np.testing.assert_array_equal(idx, O.sink_local_topk(r["scores"].cpu().numpy(), 512, x["sink"], x["local"]))
+        rK, rV, rnu = O.gather_union(idx, x["n"], K.view(torch.int16).numpy(), V.view(torch.int16).numpy())
+        np.testing.assert_array_equal(r["n_unique"].cpu().numpy(), rnu)
+        np.testing.assert_array_equal(r["K"].cpu().view(torch.int16).numpy(), rK)
+        np.testing.assert_array_equal(r["V"].cpu().view(torch.int16).numpy(), rV)
     finally:
         for h in hps:
             off.free_host(h)
@@ -835,6 +891,24 @@ def test_scan_chan4_matches_oracle_and_plane_scan(G, n, r):
     assert (out[..., :3 * 64] == 7.0).all() and (out[..., 9 * 64:] == 7.0).all()
 
 
+def test_scan_chan4_reference_matches_oracle():
+    """scan_chan4_reference (the reference's dense formula, kernels/bitplane.py:365-370:
+    full-depth dequantisation masked to the active channels, then q @ .T) against
+    the float64 chan4 oracle, and against the chan4 kernel."""
+    BH, G, n = 2, 4, 3000
+    K = _keys(BH, n, dtype=torch.bfloat16, edge=False)
+    q = torch.randn(BH, G, 128, generator=torch.Generator().manual_seed(9))
+    active = torch.zeros(BH, 128, dtype=torch.bool)
+    active.scatter_(1, q.abs().sum(1).topk(40, -1).indices, True)
+    cs = bp.Chan4Store(K.to(DEV))
+    got = bp.scan_chan4_reference(q.to(DEV), cs.code, cs.scales_blk, active.to(DEV))
+    act, nact = bp.channel_list(active.to(DEV))
+    code, sc = O.quantise_u4(K.float().numpy())
+    ref = O.scan_chan4(q.numpy(), code, sc, act.cpu().numpy(), nact.cpu().numpy())
+    _scores_close(got.cpu().numpy(), ref)
+    _scores_close(cs.scan(q.to(DEV), act, nact).cpu().numpy(), ref)
+
+
 def test_scan_chan4_host_resident():
     K = _keys(2, 9000, dtype=torch.bfloat16, edge=False)
     q = torch.randn(2, 4, 128).to(DEV)
@@ -906,6 +980,38 @@ def test_klt_store_scan_and_topk(budget):
     _scores_close(s.cpu().numpy(), ref)
     idx = st.scan_topk(q, plan, 2048, 4, 32)
     torch.testing.assert_close(idx, bp.sink_local_topk(s, 2048, 4, 32), rtol=0, atol=0)
+
+
+def test_klt_full_depth_within_quantisation_bound():
+    """A full-depth KLT store (budget 512 = 4 bits on all 128 rotated channels)
+    scores q.(K - mu) to within the 4-bit quantiser's bound: every rotated key
+    value lies within a_be / 16 of its dequantised code (a_be the block scale of
+    rotated channel e), so |score - q.(K - mu)| <= sum_e |qr_e| a_be / 16, with
+    qr = q Vt.  The bound holds because Vt is orthonormal (q.(K - mu) = qr.Kr)
+    and is met with a slack only for the fp16 rounding of the scales and fp32
+    summation."""
+    print("[klt] full depth bound", flush=True)
+    from fathom_amd import klt
+    x, Qcal = _klt_case()
+    Kd = x["K"].to(DEV)
+    p = klt.klt_params(Kd, Qcal.to(DEV))
+    st = klt.KLTPlaneStore(Kd, p)
+    q = x["q"].to(DEV)
+    plan = st.plan(q, 512.0)
+    assert (plan["t"] == 4).all()
+    s = st.scan(q, plan).cpu().double().numpy()
+    qr, _ = st.query(q)
+    qr = qr.cpu().double().numpy()
+    mu = p["mu"].cpu().double().numpy()
+    Kc = x["K"].double().numpy() - mu[:, None, :]
+    exact = np.einsum("bgd,bnd->bgn", x["q"].double().numpy(), Kc)
+    a = st.scales_blk.cpu().double().numpy()                       # [BH, nblk, D]
+    bound_blk = np.einsum("bgd,bkd->bgk", np.abs(qr), a) / 16.0
+    bound = np.repeat(bound_blk, 64, axis=-1)[..., :x["n"]]
+    err = np.abs(s - exact)
+    slack = 2e-3 * bound + 1e-5 * np.abs(exact).max(-1, keepdims=True)
+    assert (err <= bound + slack).all(), f"max err/bound {(err / bound).max():.4f}"
+    assert (err / bound).max() > 0.3                                # the bound is not vacuous here
 
 
 # ----------------------------------------------------------------------------- chunked copy/scan pipeline
