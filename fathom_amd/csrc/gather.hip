@@ -16,12 +16,15 @@
 //           recent-token device buffer, or a zero row for negative tokens) and
 //           writes it to every position of its chain, so each distinct host
 //           row crosses PCIe exactly once;
-//   attend  (gather_attention) workgroups of 128 distinct tokens read each
-//           token's K and V rows once, straight into registers, and form the
-//           softmax numerators of every query head that selected the token,
-//           weighted by the number of times that head selected it; each
-//           workgroup writes a partial (max, sum, weighted V) triple per head
-//           and a second kernel merges a row's triples in split order.
+//   attend  (gather_attention) workgroups of 64 tokens -- distinct tokens of
+//           the union (host-resident rows: each row crosses PCIe once), or
+//           plain selected positions (rows in device memory: no union pass)
+//           -- read the K and V rows, 16 lanes per 256-byte row so every load
+//           instruction reads whole rows, and form the softmax numerators of
+//           every query head, weighted by the times the head selected the
+//           token; each workgroup writes a partial (max, sum, weighted V)
+//           triple per head and a second kernel merges a row's triples in
+//           split order.
 #include "common.hpp"
 
 namespace fathom {
@@ -35,9 +38,9 @@ constexpr int kHashSlots = 16384;                  // >= kMaxGK: the table never
 constexpr int kMaxHeads = 8;                       // query heads counted per token
 constexpr uint32_t kTokNeg = 0xFFFFFFFEu;          // token key of negative indices
 constexpr int kAttnD = 128;                        // head dimension of gather_attention
-constexpr int kAttnWaves = 2;
+constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * kWave;
-constexpr int kAttnTok = kAttnThreads;             // distinct tokens per workgroup (one per thread)
+constexpr int kAttnTok = 16 * kAttnWaves;          // distinct tokens per workgroup (16 per wave)
 constexpr int kPartStride = kAttnD + 2;            // (max, sum, weighted V[128])
 constexpr int kMaxSplit = kMaxGK / kAttnTok;       // workgroups per row at most
 
@@ -242,185 +245,298 @@ __device__ __forceinline__ float wave_max_f(float v) {
 template <int G>
 struct AttnShared {
   float q[G][kAttnD];            // the row's query heads
-  float p[kAttnTok][G];          // softmax numerators of the workgroup's tokens
-  int64_t vrow[kAttnTok];        // V row offset in bytes from its base (-1: zero row)
-  uint8_t vrec[kAttnTok];        // 1: the row is in the recent buffer
+  uint64_t kaddr[kAttnTok];      // K and V row addresses of the workgroup's tokens (0: zero row)
+  uint64_t vaddr[kAttnTok];
+  uint4 cnt[kAttnTok];           // per-head selection counts (0 past the row's distinct tokens)
   float wm[kAttnWaves][G], wl[kAttnWaves][G];
-  float2 o[G][kWave];            // the second wave's weighted V sums
+  float o[kAttnWaves][G][kAttnD];  // the waves' weighted V sums
 };
 
-// Partial softmax attention of one workgroup's 128 distinct tokens for the G
-// query heads of row bh, in two phases:
-//   scores  thread t owns distinct token u0 + t: it reads the whole 256-byte K
-//           row (16 x 16-byte loads) and forms q_g . K for every head g with
-//           the query read from LDS (broadcast), so no cross-lane reductions;
-//           the workgroup's max M_g and numerators c_g e^(s - M_g) follow;
-//   values  lane l of each wave owns dimensions 2l and 2l + 1 and sums
-//           p_g(token) V[token] over its wave's 64 tokens (one coalesced
-//           256-byte V row per wave and token, 8 rows in flight).
+// Sum (MAX = false) or maximum over the 16 lanes of a DPP row: quad_perm
+// [1,0,3,2], [2,3,0,1], then row_half_mirror and row_mirror, each pairing
+// halves whose lanes already agree.
+template <bool MAX>
+__device__ __forceinline__ float row16_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
+  return op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));
+}
+
+// Sum or maximum of the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the same lane of
+// the four DPP rows): the gfx950 row swaps v_permlane32_swap and
+// v_permlane16_swap give each lane its partner's value.
+template <bool MAX>
+__device__ __forceinline__ float across_rows(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  const uint32_t x = __float_as_uint(v);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  v = op(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+  const uint32_t y = __float_as_uint(v);
+  const auto p16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
+  return op(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4 *gptr4;
+
+// Softmax attention over the kAttnTok tokens whose K/V row addresses and
+// per-head counts are in sh (kaddr, vaddr, cnt; the whole workgroup calls it,
+// after a barrier that completes them).  Wave w takes tokens 16 w .. 16 w +
+// 15; lane l reads dims 8 (l & 15) .. + 7 of the rows of tokens 16 w + 4 j +
+// (l >> 4), j < 4, so each load instruction reads four whole 256-byte rows,
+// and the K and V rows are loaded together.  Then:
+//   scores  partial dots of 8 dims per lane, summed over the 16 lanes of a
+//           row (DPP); the tokens' maximum M_g and the numerators
+//           c_g e^(s - M_g) (c_g: the times head g selected the token);
+//   values  each lane sums p V over its dims and tokens, and the four row
+//           groups of a wave are summed by row swaps.
+// Leaves each wave's maximum, numerator sum and weighted V sums of every head
+// in sh.wm, sh.wl and sh.o (complete after the caller's next barrier).  Rows
+// without data (address 0) score 0 and add nothing to V; qa: any 256 readable
+// bytes, read in their place.
 template <int G>
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4))) void attn_partial_kernel(const float *__restrict__ q, UnionWs w,
-                                                                    int64_t GK, RowSrc rs, float scale,
-                                                                    float *__restrict__ part, int64_t nsplit) {
-  __shared__ AttnShared<G> sh;
+__device__ __forceinline__ void attn_tokens(AttnShared<G> &sh, uint64_t qa, float scale) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t bh = blockIdx.y, split = blockIdx.x;
-  const int64_t U = w.U[bh];
-  for (int e = tid; e < G * kAttnD; e += kAttnThreads) sh.q[e / kAttnD][e % kAttnD] = q[bh * G * kAttnD + e];
-  // ---- scores
-  const int64_t u = split * kAttnTok + tid;
-  uint4 cn = make_uint4(0u, 0u, 0u, 0u);
-  const uint4 *krow = nullptr;
-  int64_t vrow = -1;
-  bool rec = false;
-  if (u < U) {
-    const uint64_t ent = w.ulist[bh * GK + u];
-    cn = w.cnt[bh * GK + (uint32_t)ent];
-    const int64_t row = rs.locate((uint32_t)(ent >> 32), bh, rec);
-    if (row >= 0) {
-      krow = reinterpret_cast<const uint4 *>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
-      vrow = row * rs.row_bytes;
-    }
+  const int rg = lane >> 4, ds = lane & 15;
+  u32x4 kv[4], vv[4];
+  bool has[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = 16 * wave + 4 * j + rg;
+    const uint64_t ka = sh.kaddr[t], va = sh.vaddr[t];
+    has[j] = ka != 0ull;
+    kv[j] = reinterpret_cast<gptr4>(ka ? ka : qa)[ds];
+    vv[j] = reinterpret_cast<gptr4>(va ? va : qa)[ds];
   }
-  sh.vrow[tid] = vrow;
-  sh.vrec[tid] = rec ? 1 : 0;
-  // unconditional loads (no branch per load): threads without a row read the
-  // query array instead and their scores are replaced below
-  const uint4 *kp = krow ? krow : reinterpret_cast<const uint4 *>(q);
-  uint4 kv[kAttnD / 8];
+  // ---- scores
+  float s[4][G];
 #pragma unroll
-  for (int j = 0; j < kAttnD / 8; ++j) kv[j] = kp[j];
-  __syncthreads();  // q staged
-  float s[G];
+  for (int g = 0; g < G; ++g) {
+    const float4 q0 = *reinterpret_cast<const float4 *>(&sh.q[g][8 * ds]);
+    const float4 q1 = *reinterpret_cast<const float4 *>(&sh.q[g][8 * ds + 4]);
+    const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-  for (int g = 0; g < G; ++g) s[g] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kAttnD / 8; ++j) {
-    const uint32_t d4[4] = {kv[j].x, kv[j].y, kv[j].z, kv[j].w};
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float4 qa = *reinterpret_cast<const float4 *>(&sh.q[g][8 * j]);
-      const float4 qb = *reinterpret_cast<const float4 *>(&sh.q[g][8 * j + 4]);
-      const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t d4[4] = {kv[j].x, kv[j].y, kv[j].z, kv[j].w};
+      float a = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t h = d4[e >> 1];
-        const float kf = __uint_as_float((e & 1) ? (h & 0xFFFF0000u) : (h << 16));
-        s[g] = fmaf(qq[e], kf, s[g]);
+        a = fmaf(qq[e], __uint_as_float((e & 1) ? (h & 0xFFFF0000u) : (h << 16)), a);
       }
-      // keep the query reads of at most 4 heads in flight (hoisting them all
-      // costs G * 128 registers)
-      if ((g & 3) == 3 || g == G - 1) __builtin_amdgcn_sched_barrier(0);
+      s[j][g] = a;
     }
   }
-  // every head's reductions before any lane-0 branch, so no score is computed late
-  float c[G], wr[G];
+  float c[4][G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    c[g] = (float)head_count(cn, g);
-    s[g] = c[g] > 0.0f ? (krow ? s[g] * scale : 0.0f) : -INFINITY;  // a zero row scores 0
-    wr[g] = wave_max_f(s[g]);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) sh.wm[wave][g] = wr[g];
-  }
-  __syncthreads();
-  float M[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    M[g] = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < kAttnWaves; ++v) M[g] = fmaxf(M[g], sh.wm[v][g]);
-    const float p = c[g] > 0.0f ? c[g] * expf(s[g] - M[g]) : 0.0f;
-    sh.p[tid][g] = p;
-    wr[g] = wave_sum_f(p);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) sh.wl[wave][g] = wr[g];
-  }
-  __syncthreads();
-  // ---- values: wave v sums tokens [64 v, 64 v + 64)
-  float2 o[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) o[g] = make_float2(0.0f, 0.0f);
-  const int t0 = wave * kWave;
-#pragma unroll 1
-  for (int r0 = 0; r0 < kWave; r0 += 8) {
-    uint32_t vv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {  // unconditional loads; rows without data read q and are zeroed
-      const int64_t vr = sh.vrow[t0 + r0 + i];
-      const char *vb = vr >= 0 ? (sh.vrec[t0 + r0 + i] ? rs.Vrec : rs.V) + vr : reinterpret_cast<const char *>(q);
-      vv[i] = reinterpret_cast<const uint32_t *>(vb)[lane];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t vi = sh.vrow[t0 + r0 + i] >= 0 ? vv[i] : 0u;
-      const float vx = __uint_as_float(vi << 16), vy = __uint_as_float(vi & 0xFFFF0000u);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = sh.p[t0 + r0 + i][g];
-        o[g].x = fmaf(p, vx, o[g].x);
-        o[g].y = fmaf(p, vy, o[g].y);
-      }
-    }
-  }
-  if (wave == 1) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) sh.o[g][lane] = o[g];
-  }
-  __syncthreads();
-  if (wave == 0) {
+  for (int j = 0; j < 4; ++j) {
+    const uint4 cn = sh.cnt[16 * wave + 4 * j + rg];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float *pp = part + ((bh * nsplit + split) * G + g) * kPartStride;
-      if (lane == 0) {
-        pp[0] = M[g];
-        pp[1] = sh.wl[0][g] + sh.wl[1][g];
-      }
-      pp[2 + 2 * lane] = o[g].x + sh.o[g][lane].x;
-      pp[3 + 2 * lane] = o[g].y + sh.o[g][lane].y;
+      c[j][g] = (float)head_count(cn, g);
+      const float sc = row16_reduce<false>(s[j][g]);
+      s[j][g] = c[j][g] > 0.0f ? (has[j] ? sc * scale : 0.0f) : -INFINITY;  // a zero row scores 0
     }
+  }
+  // ---- softmax over the tokens
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
+    m = across_rows<true>(m);
+    if (lane == 0) sh.wm[wave][g] = m;
+  }
+  __syncthreads();
+  float l[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kAttnWaves; ++v) M = fmaxf(M, sh.wm[v][g]);
+    float ls = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s[j][g] = c[j][g] > 0.0f ? c[j][g] * expf(s[j][g] - M) : 0.0f;  // the numerator p
+      ls += s[j][g];
+    }
+    l[g] = ls;
+  }
+  // ---- values: the lane's 8 dims over its 4 tokens, then over the wave's rows
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t d4[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t h = has[j] ? d4[e >> 1] : 0u;
+        o[e] = fmaf(s[j][g], __uint_as_float((e & 1) ? (h & 0xFFFF0000u) : (h << 16)), o[e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = across_rows<false>(o[e]);
+    if (rg == 0) {
+      *reinterpret_cast<float4 *>(&sh.o[wave][g][8 * ds]) = make_float4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<float4 *>(&sh.o[wave][g][8 * ds + 4]) = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    const float lw = across_rows<false>(l[g]);
+    if (lane == 0) sh.wl[wave][g] = lw;
+  }
+}
+
+// Partial attention of one workgroup's kAttnTok distinct tokens of the union
+// list (tokens [split * kAttnTok, + kAttnTok) of row bh): the (M, sum,
+// weighted V) triple of every head.
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(const float *__restrict__ q, UnionWs w, int64_t GK,
+                                                                    RowSrc rs, float scale, float *__restrict__ part,
+                                                                    int64_t nsplit) {
+  __shared__ AttnShared<G> sh;
+  const int tid = threadIdx.x;
+  const int64_t bh = blockIdx.y, split = blockIdx.x;
+  const int64_t U = w.U[bh];
+  for (int e = tid; e < G * kAttnD; e += kAttnThreads) sh.q[e / kAttnD][e % kAttnD] = q[bh * G * kAttnD + e];
+  if (tid < kAttnTok) {
+    const int64_t u = split * kAttnTok + tid;
+    uint4 cn = make_uint4(0u, 0u, 0u, 0u);
+    uint64_t ka = 0ull, va = 0ull;
+    if (u < U) {
+      const uint64_t ent = w.ulist[bh * GK + u];
+      cn = w.cnt[bh * GK + (uint32_t)ent];
+      bool rec;
+      const int64_t row = rs.locate((uint32_t)(ent >> 32), bh, rec);
+      if (row >= 0) {
+        ka = reinterpret_cast<uint64_t>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
+        va = reinterpret_cast<uint64_t>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes);
+      }
+    }
+    sh.kaddr[tid] = ka;
+    sh.vaddr[tid] = va;
+    sh.cnt[tid] = cn;
+  }
+  __syncthreads();
+  attn_tokens<G>(sh, reinterpret_cast<uint64_t>(q), scale);
+  __syncthreads();
+  float *pb = part + (bh * nsplit + split) * G * kPartStride;
+  for (int e = tid; e < G * kAttnD; e += kAttnThreads) {
+    const int g = e / kAttnD, d = e % kAttnD;
+    float acc = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kAttnWaves; ++v) acc += sh.o[v][g][d];
+    pb[g * kPartStride + 2 + d] = acc;
+  }
+  if (tid < G) {
+    float Mg = -INFINITY, Lg = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kAttnWaves; ++v) {
+      Mg = fmaxf(Mg, sh.wm[v][tid]);
+      Lg += sh.wl[v][tid];
+    }
+    pb[tid * kPartStride] = Mg;
+    pb[tid * kPartStride + 1] = Lg;
+  }
+}
+
+// Attention straight over the selected positions (no union, for rows in
+// device memory and callers that do not ask for n_unique): workgroup s of row
+// bh takes positions [s kAttnTok, + kAttnTok) of the row's G * k, each with a
+// count of one for its own head (position p belongs to head p / k), so a row
+// selected by several heads, or several times by one, is read once per
+// position and counted as often as it is selected.
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_direct_kernel(const float *__restrict__ q,
+                                                                   const int64_t *__restrict__ idx, int64_t GK,
+                                                                   int64_t k, RowSrc rs, float scale,
+                                                                   float *__restrict__ part, int64_t nsplit) {
+  __shared__ AttnShared<G> sh;
+  const int tid = threadIdx.x;
+  const int64_t bh = blockIdx.y, split = blockIdx.x;
+  for (int e = tid; e < G * kAttnD; e += kAttnThreads) sh.q[e / kAttnD][e % kAttnD] = q[bh * G * kAttnD + e];
+  if (tid < kAttnTok) {
+    const int64_t p = split * kAttnTok + tid;
+    uint4 cn = make_uint4(0u, 0u, 0u, 0u);
+    uint64_t ka = 0ull, va = 0ull;
+    if (p < GK) {
+      const uint32_t g = (uint32_t)(p / k);
+      const uint32_t one = 1u << (16 * (g & 1));
+      cn = make_uint4(g >> 1 == 0 ? one : 0u, g >> 1 == 1 ? one : 0u, g >> 1 == 2 ? one : 0u, g >> 1 == 3 ? one : 0u);
+      bool rec;
+      const int64_t row = rs.locate(tok_key(idx[bh * GK + p]), bh, rec);
+      if (row >= 0) {
+        ka = reinterpret_cast<uint64_t>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
+        va = reinterpret_cast<uint64_t>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes);
+      }
+    }
+    sh.kaddr[tid] = ka;
+    sh.vaddr[tid] = va;
+    sh.cnt[tid] = cn;
+  }
+  __syncthreads();
+  attn_tokens<G>(sh, reinterpret_cast<uint64_t>(q), scale);
+  __syncthreads();
+  float *pb = part + (bh * nsplit + split) * G * kPartStride;
+  for (int e = tid; e < G * kAttnD; e += kAttnThreads) {
+    const int g = e / kAttnD, d = e % kAttnD;
+    float acc = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kAttnWaves; ++v) acc += sh.o[v][g][d];
+    pb[g * kPartStride + 2 + d] = acc;
+  }
+  if (tid < G) {
+    float Mg = -INFINITY, Lg = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kAttnWaves; ++v) {
+      Mg = fmaxf(Mg, sh.wm[v][tid]);
+      Lg += sh.wl[v][tid];
+    }
+    pb[tid * kPartStride] = Mg;
+    pb[tid * kPartStride + 1] = Lg;
   }
 }
 
 // out[bh, g, d] = sum_s O_s e^(M_s - M) / sum_s L_s e^(M_s - M) over the
-// row's splits (<= kMaxSplit), in split order.
+// row's splits, by every thread for its own dimension d with no barrier:
+// M = max_s M_s first, then the weighted sums in split order, kB splits per
+// round of loads (rows of at most kB splits: one round).  A split where a head
+// selected nothing (M_s = -inf) adds nothing to it.
 __global__ __launch_bounds__(kAttnD) void attn_merge_kernel(const float *__restrict__ part, int64_t G,
                                                             int64_t nsplit, float *__restrict__ out) {
-  __shared__ float wt[kMaxSplit];
-  __shared__ float s_L;
+  constexpr int kB = 32;
   const int64_t r = blockIdx.x;  // bh * G + g
   const int64_t bh = r / G, g = r % G;
   const int d = threadIdx.x;
   const float *base = part + (bh * nsplit * G + g) * kPartStride;  // split s at + s * G * kPartStride
   const int64_t sstride = G * kPartStride;
-  if (d < nsplit) wt[d] = base[d * sstride];
-  __syncthreads();
-  if (d == 0) {
-    float M = -INFINITY;
-    for (int s = 0; s < (int)nsplit; ++s) M = fmaxf(M, wt[s]);
-    float L = 0.0f;
-    for (int s = 0; s < (int)nsplit; ++s) {
-      const float e = wt[s] == -INFINITY ? 0.0f : expf(wt[s] - M);
-      wt[s] = e;
-      L = fmaf(base[s * sstride + 1], e, L);
+  float M = -INFINITY;
+  if (nsplit > kB)
+    for (int s = 0; s < (int)nsplit; ++s) M = fmaxf(M, base[s * sstride]);
+  float L = 0.0f, O = 0.0f;
+  for (int s0 = 0; s0 < (int)nsplit; s0 += kB) {
+    float ms[kB], ls[kB], os[kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const bool in = s0 + i < nsplit;
+      const float *b = base + (in ? (s0 + i) : 0) * sstride;
+      ms[i] = in ? b[0] : -INFINITY;
+      ls[i] = in ? b[1] : 0.0f;
+      os[i] = in ? b[2 + d] : 0.0f;
     }
-    s_L = L;
-  }
-  __syncthreads();
-  float Od = 0.0f;
-  for (int s0 = 0; s0 < (int)nsplit; s0 += 8) {
-    float ov[8];
+    if (nsplit <= kB) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ov[i] = s0 + i < nsplit ? base[(s0 + i) * sstride + 2 + d] : 0.0f;
+      for (int i = 0; i < kB; ++i) M = fmaxf(M, ms[i]);
+    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (s0 + i < nsplit) Od = fmaf(ov[i], wt[s0 + i], Od);
+    for (int i = 0; i < kB; ++i) {
+      const float e = ms[i] == -INFINITY ? 0.0f : expf(ms[i] - M);  // an empty split adds nothing
+      L = fmaf(ls[i], e, L);
+      O = fmaf(os[i], e, O);
+    }
   }
-  out[r * kAttnD + d] = Od / s_L;
+  out[r * kAttnD + d] = O / L;
 }
 
 int hash_bits(int64_t GK) {
@@ -440,6 +556,13 @@ void launch_attn_g(const float *q, const UnionWs &w, int64_t BH, int64_t GK, con
                    int64_t nsplit, hipStream_t st) {
   attn_partial_kernel<G><<<dim3((unsigned)nsplit, (unsigned)BH), kAttnThreads, 0, st>>>(q, w, GK, rs, scale, part,
                                                                                          nsplit);
+}
+
+template <int G>
+void launch_direct_g(const float *q, const int64_t *idx, int64_t BH, int64_t GK, int64_t k, const RowSrc &rs,
+                     float scale, float *part, int64_t nsplit, hipStream_t st) {
+  attn_direct_kernel<G><<<dim3((unsigned)nsplit, (unsigned)BH), kAttnThreads, 0, st>>>(q, idx, GK, k, rs, scale, part,
+                                                                                        nsplit);
 }
 
 }  // namespace
@@ -518,21 +641,38 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
   UnionWs w;
   const size_t off = union_ws_layout(BH, GK, static_cast<char *>(workspace), &w);
   float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + off);
-  int rc = launch_union(idx, BH, GK, k, n, w, n_unique, st);
-  if (rc) return rc;
   const RowSrc rs{(const char *)Ksrc, (const char *)Vsrc, (const char *)Krec, (const char *)Vrec,
                   cap, nrec, n, (int64_t)kAttnD * 2};
-  switch (G) {
-    case 1: launch_attn_g<1>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
-    case 2: launch_attn_g<2>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
-    case 3: launch_attn_g<3>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
-    case 4: launch_attn_g<4>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
-    case 5: launch_attn_g<5>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
-    case 6: launch_attn_g<6>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
-    case 7: launch_attn_g<7>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
-    default: launch_attn_g<8>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+  int rc;
+  if (!n_unique) {
+    // per position, no union
+    switch (G) {
+      case 1: launch_direct_g<1>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+      case 2: launch_direct_g<2>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+      case 3: launch_direct_g<3>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+      case 4: launch_direct_g<4>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+      case 5: launch_direct_g<5>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+      case 6: launch_direct_g<6>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+      case 7: launch_direct_g<7>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+      default: launch_direct_g<8>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
+    }
+    rc = launch_status("attn_direct_kernel");
+  } else {
+    // the union list (each distinct row read once), then its groups of kAttnTok tokens
+    rc = launch_union(idx, BH, GK, k, n, w, n_unique, st);
+    if (rc) return rc;
+    switch (G) {
+      case 1: launch_attn_g<1>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+      case 2: launch_attn_g<2>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+      case 3: launch_attn_g<3>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+      case 4: launch_attn_g<4>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+      case 5: launch_attn_g<5>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+      case 6: launch_attn_g<6>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+      case 7: launch_attn_g<7>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+      default: launch_attn_g<8>(q, w, BH, GK, rs, scale, part, nsplit, st); break;
+    }
+    rc = launch_status("attn_partial_kernel");
   }
-  rc = launch_status("attn_partial_kernel");
   if (rc) return rc;
   attn_merge_kernel<<<(unsigned)(BH * G), kAttnD, 0, st>>>(part, G, nsplit, out);
   return launch_status("attn_merge_kernel");

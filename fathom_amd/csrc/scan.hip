@@ -556,10 +556,13 @@ __device__ __forceinline__ void emit_sample(const Emit &em, const Tile<NQ, RS> &
 // that ulp and the rounding of thr - C, so no passing token fails the
 // prefilter (NaN passes both).  Only steps where some lane passes it compute
 // scores and keys.
-__device__ __forceinline__ float acc_threshold(float thr, float C, float f) {
-  if (!(f > 0.0f) || !(f < INFINITY) || !(fabsf(C) < INFINITY)) return __int_as_float(0x7FC00000);  // NaN: all pass
+// f = 2^fe exactly, so dividing by it is an exact ldexp (when f is a normal
+// power of two; otherwise every token takes the exact path).
+__device__ __forceinline__ float acc_threshold(float thr, float C, float f, int fe) {
+  if (!(f > 0.0f) || !(f < INFINITY) || !(fabsf(C) < INFINITY) || fe < -126 || fe > 127)
+    return __int_as_float(0x7FC00000);  // NaN: all pass
   const float margin = (fabsf(thr) + fabsf(C)) * 0x1p-20f + 0x1p-126f;
-  return ((thr - C) - margin) * (1.0f / f);
+  return ldexpf((thr - C) - margin, -fe);
 }
 
 template <int NQ>
@@ -584,7 +587,8 @@ __device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t
     float f[4], T[4];
     head_factors(f, t, sh, h);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) T[w] = plain ? acc_threshold(thr_f, t.cst[h], f[w]) : __int_as_float(0x7FC00000);
+    for (int w = 0; w < 4; ++w)
+      T[w] = plain ? acc_threshold(thr_f, t.cst[h], f[w], sh.sig[h] + t.sx - bit_exp(w)) : __int_as_float(0x7FC00000);
     uint64_t *dst = em.sel.cand + row * em.sel.cand_cap + t0;
     uint32_t off = 0u;
 #pragma unroll

@@ -260,15 +260,18 @@ def gather_union(idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, dtype=torch.bflo
     return Ks, Vs, nu
 
 
-def gather_attention(q, idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, scale=None):
-    """Exact attention over the selected rows, fused with their union gather:
+def gather_attention(q, idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, scale=None, unique=None):
+    """Exact attention over the selected rows, fused with their gather:
     out[bh, g] = softmax(scale * q[bh, g] . K[idx[bh, g]]) . V[idx[bh, g]] in fp32
     over bf16 rows of D = 128 (scripts/B_kernel_bench.py:22-27;
     scripts/B_e2e_offload_v2.py:228-244).  Row sources as in gather_union: tokens
     < n from Ksrc/Vsrc [BH, cap, D] (tensor or DevPtr, HBM or mapped host), tokens
-    >= n from Krec/Vrec, negative tokens as zero rows; each distinct token of a row
-    is read once.  scale defaults to D ** -0.5.  Returns (out [BH, G, D] fp32,
-    n_unique [BH] int32)."""
+    >= n from Krec/Vrec, negative tokens as zero rows.  unique=True forms each row's
+    union first, so each distinct token is read once, and returns its size;
+    unique=False reads the rows per selected position with one launch fewer (for
+    rows in device memory) and returns n_unique None; the default is True for
+    mapped host rows (DevPtr) and False for tensors.  scale defaults to D ** -0.5.
+    Returns (out [BH, G, D] fp32, n_unique [BH] int32 or None)."""
     _need_gpu(q, idx)
     BH, G, k = idx.shape
     if q.shape != (BH, G, D):
@@ -280,7 +283,9 @@ def gather_attention(q, idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, scale=Non
     qf = q.float().contiguous()
     flat = idx.contiguous().to(torch.int64)
     out = torch.empty(BH, G, D, device=dev, dtype=torch.float32)
-    nu = torch.empty(BH, device=dev, dtype=torch.int32)
+    if unique is None:
+        unique = isinstance(Ksrc, DevPtr)
+    nu = torch.empty(BH, device=dev, dtype=torch.int32) if unique else None
     nbytes = _lib.lib().fathom_gather_attention_workspace_bytes(BH, G, k)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     nrec = 0

@@ -251,9 +251,13 @@ int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t n, c
  * positions j of idx[bh, g] (fp32 math on bf16 rows; a token selected twice
  * counts twice).  Rows come from the same sources as fathom_gather_union
  * (Ksrc/Vsrc [BH, cap, 128] bf16 for tokens < n, Krec/Vrec [BH, nrec, 128]
- * for tokens >= n, zero rows for negative tokens), each distinct token of a
- * row read once.  q [BH, G, 128] fp32, idx [BH, G, k] int64, out [BH, G, 128]
- * fp32; G <= 8, G*k <= 16384; n_unique as in fathom_gather_union.
+ * for tokens >= n, zero rows for negative tokens).  With n_unique set, the
+ * row's union is formed first and each distinct token is read once (the
+ * host-resident case: every row crosses PCIe once), and n_unique is as in
+ * fathom_gather_union; with n_unique NULL the rows are read per selected
+ * position, with no union pass (rows in device memory: one launch fewer).
+ * Both give the same attention up to fp32 summation order.  q [BH, G, 128]
+ * fp32, idx [BH, G, k] int64, out [BH, G, 128] fp32; G <= 8, G*k <= 16384.
  * workspace: fathom_gather_attention_workspace_bytes(BH, G, k) bytes.
  */
 size_t fathom_gather_attention_workspace_bytes(int64_t BH, int64_t G, int64_t k);

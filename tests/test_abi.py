@@ -39,7 +39,7 @@ def test_workspace_queries_and_argument_errors_without_gpu():
     assert L.fathom_topk_workspace_bytes(32, 1 << 20, 512) >= 32 * (1 << 20) * 8
     e = 8 * 2048  # per position: chain link, chain start, head counts, distinct-token entry
     assert L.fathom_gather_union_workspace_bytes(8, 2048) == e * (4 + 4 + 16 + 8) + 256
-    nsplit = 2048 // 128  # partial softmax triples of 128 distinct tokens each
+    nsplit = 2048 // 64  # partial softmax triples of 64 tokens (or positions) each
     assert (L.fathom_gather_attention_workspace_bytes(8, 4, 512)
             == e * (4 + 4 + 16 + 8) + 256 + 8 * nsplit * 4 * 130 * 4)
     rc = L.fathom_gather_attention(None, None, 1, 4, 512, 10, None, None, 10, None, None, 0, 1.0, None, None,

@@ -738,14 +738,19 @@ def test_gather_attention_matches_oracle(host, G, k):
         else:
             Ksrc, Vsrc = K.to(DEV), V.to(DEV)
         it = torch.from_numpy(idx).to(DEV)
-        out, nu = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, Kr.to(DEV), Vr.to(DEV))
-        out2, _ = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, Kr.to(DEV), Vr.to(DEV))
-        torch.cuda.synchronize()
         ref, rnu = O.gather_attention(q.numpy(), idx, n, K.float().numpy(), V.float().numpy(),
                                       Kr.float().numpy(), Vr.float().numpy())
-        _attn_close(out.cpu().numpy(), ref)
-        np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
-        assert torch.equal(out, out2), "two calls on the same input differ"
+        # over the union (each distinct row once) and per selected position
+        for unique in (True, False):
+            out, nu = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, Kr.to(DEV), Vr.to(DEV), unique=unique)
+            out2, _ = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, Kr.to(DEV), Vr.to(DEV), unique=unique)
+            torch.cuda.synchronize()
+            _attn_close(out.cpu().numpy(), ref)
+            if unique:
+                np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
+            else:
+                assert nu is None
+            assert torch.equal(out, out2), f"two calls on the same input differ (unique={unique})"
     finally:
         for h in hps:
             off.free_host(h)
@@ -779,9 +784,11 @@ def test_decode_layer_c5(layer):
     idx = st.scan_topk(q, plan, x["k"], x["sink"], x["local"])
     ref_idx = bp.sink_local_topk(st.scan(q, plan), x["k"], x["sink"], x["local"])
     torch.testing.assert_close(idx, ref_idx, rtol=0, atol=0)
-    out, nu = off.gather_attention(q, idx, 8192, K.to(DEV), V.to(DEV), 8192)
+    out, _ = off.gather_attention(q, idx, 8192, K.to(DEV), V.to(DEV), 8192)
+    out_u, nu = off.gather_attention(q, idx, 8192, K.to(DEV), V.to(DEV), 8192, unique=True)
     ref, rnu = O.gather_attention(x["q"].numpy(), idx.cpu().numpy(), 8192, K.float().numpy(), V.float().numpy())
     _attn_close(out.cpu().numpy(), ref)
+    _attn_close(out_u.cpu().numpy(), ref)
     np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
 
 
