@@ -16,15 +16,15 @@
 //           recent-token device buffer, or a zero row for negative tokens) and
 //           writes it to every position of its chain, so each distinct host
 //           row crosses PCIe exactly once;
-//   attend  (gather_attention) workgroups of 64 tokens -- distinct tokens of
-//           the union (host-resident rows: each row crosses PCIe once), or
-//           plain selected positions (rows in device memory: no union pass)
-//           -- read the K and V rows, 16 lanes per 256-byte row so every load
-//           instruction reads whole rows, and form the softmax numerators of
-//           every query head, weighted by the times the head selected the
-//           token; each workgroup writes a partial (max, sum, weighted V)
-//           triple per head and a second kernel merges a row's triples in
-//           split order.
+//   attend  (gather_attention) the K and V rows are read 16 lanes per 256-byte
+//           row, so every load instruction reads whole rows, and form the
+//           softmax numerators of the query heads, weighted by the times a
+//           head selected the token.  Over the union (host-resident rows:
+//           each row crosses PCIe once), workgroups of 64 distinct tokens
+//           write a partial (max, sum, weighted V) triple per head and a
+//           second kernel merges a row's triples in split order; without it
+//           (rows in device memory), one workgroup per query head folds its
+//           own positions 256 at a time and writes the output: one launch.
 #include "common.hpp"
 
 namespace fathom {
@@ -242,14 +242,15 @@ __device__ __forceinline__ float wave_max_f(float v) {
   return v;
 }
 
-template <int G>
+// LDS of an attention workgroup of NW waves (16 tokens per wave).
+template <int G, int NW = kAttnWaves>
 struct AttnShared {
   float q[G][kAttnD];            // the row's query heads
-  uint64_t kaddr[kAttnTok];      // K and V row addresses of the workgroup's tokens (0: zero row)
-  uint64_t vaddr[kAttnTok];
-  uint4 cnt[kAttnTok];           // per-head selection counts (0 past the row's distinct tokens)
-  float wm[kAttnWaves][G], wl[kAttnWaves][G];
-  float o[kAttnWaves][G][kAttnD];  // the waves' weighted V sums
+  uint64_t kaddr[16 * NW];       // K and V row addresses of the workgroup's tokens (0: zero row)
+  uint64_t vaddr[16 * NW];
+  uint4 cnt[16 * NW];            // per-head selection counts (0 past the row's distinct tokens)
+  float wm[NW][G], wl[NW][G];
+  float o[NW][G][kAttnD];        // the waves' weighted V sums
 };
 
 // Sum (MAX = false) or maximum over the 16 lanes of a DPP row: quad_perm
@@ -281,7 +282,7 @@ __device__ __forceinline__ float across_rows(float v) {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) u32x4 *gptr4;
 
-// Softmax attention over the kAttnTok tokens whose K/V row addresses and
+// Softmax attention over the 16 NW tokens whose K/V row addresses and
 // per-head counts are in sh (kaddr, vaddr, cnt; the whole workgroup calls it,
 // after a barrier that completes them).  Wave w takes tokens 16 w .. 16 w +
 // 15; lane l reads dims 8 (l & 15) .. + 7 of the rows of tokens 16 w + 4 j +
@@ -296,8 +297,8 @@ typedef const __attribute__((address_space(1))) u32x4 *gptr4;
 // in sh.wm, sh.wl and sh.o (complete after the caller's next barrier).  Rows
 // without data (address 0) score 0 and add nothing to V; qa: any 256 readable
 // bytes, read in their place.
-template <int G>
-__device__ __forceinline__ void attn_tokens(AttnShared<G> &sh, uint64_t qa, float scale) {
+template <int G, int NW = kAttnWaves>
+__device__ __forceinline__ void attn_tokens(AttnShared<G, NW> &sh, uint64_t qa, float scale) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rg = lane >> 4, ds = lane & 15;
   u32x4 kv[4], vv[4];
@@ -353,7 +354,7 @@ __device__ __forceinline__ void attn_tokens(AttnShared<G> &sh, uint64_t qa, floa
   for (int g = 0; g < G; ++g) {
     float M = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < kAttnWaves; ++v) M = fmaxf(M, sh.wm[v][g]);
+    for (int v = 0; v < NW; ++v) M = fmaxf(M, sh.wm[v][g]);
     float ls = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -441,61 +442,78 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(const float 
   }
 }
 
-// Attention straight over the selected positions (no union, for rows in
-// device memory and callers that do not ask for n_unique): workgroup s of row
-// bh takes positions [s kAttnTok, + kAttnTok) of the row's G * k, each with a
-// count of one for its own head (position p belongs to head p / k), so a row
-// selected by several heads, or several times by one, is read once per
-// position and counted as often as it is selected.
-template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_direct_kernel(const float *__restrict__ q,
-                                                                   const int64_t *__restrict__ idx, int64_t GK,
-                                                                   int64_t k, RowSrc rs, float scale,
-                                                                   float *__restrict__ part, int64_t nsplit) {
-  __shared__ AttnShared<G> sh;
+// Attention of one query head per workgroup (no union, rows in device memory,
+// n_unique not asked for): workgroup (g, bh) of kHeadWaves waves takes head
+// g's k selected positions 16 kHeadWaves at a time, each with a count of one
+// (a row selected twice counts twice), folds every group into a running (M,
+// sum, weighted V) with the usual rescaling, and writes out[bh, g] itself --
+// one launch, no partial triples.
+constexpr int kHeadWaves = 16;
+constexpr int kHeadTok = 16 * kHeadWaves;
+
+__global__ __launch_bounds__(kHeadWaves * kWave) void attn_head_kernel(const float *__restrict__ q,
+                                                                       const int64_t *__restrict__ idx, int64_t G,
+                                                                       int64_t k, RowSrc rs, float scale,
+                                                                       float *__restrict__ out) {
+  __shared__ AttnShared<1, kHeadWaves> sh;
+  __shared__ float runO[kAttnD];
+  __shared__ float runM, runL;
   const int tid = threadIdx.x;
-  const int64_t bh = blockIdx.y, split = blockIdx.x;
-  for (int e = tid; e < G * kAttnD; e += kAttnThreads) sh.q[e / kAttnD][e % kAttnD] = q[bh * G * kAttnD + e];
-  if (tid < kAttnTok) {
-    const int64_t p = split * kAttnTok + tid;
-    uint4 cn = make_uint4(0u, 0u, 0u, 0u);
-    uint64_t ka = 0ull, va = 0ull;
-    if (p < GK) {
-      const uint32_t g = (uint32_t)(p / k);
-      const uint32_t one = 1u << (16 * (g & 1));
-      cn = make_uint4(g >> 1 == 0 ? one : 0u, g >> 1 == 1 ? one : 0u, g >> 1 == 2 ? one : 0u, g >> 1 == 3 ? one : 0u);
-      bool rec;
-      const int64_t row = rs.locate(tok_key(idx[bh * GK + p]), bh, rec);
-      if (row >= 0) {
-        ka = reinterpret_cast<uint64_t>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
-        va = reinterpret_cast<uint64_t>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes);
+  const int64_t g = blockIdx.x, bh = blockIdx.y;
+  const float *qg = q + (bh * G + g) * kAttnD;
+  const int64_t *ig = idx + (bh * G + g) * k;
+  if (tid < kAttnD) {
+    sh.q[0][tid] = qg[tid];
+    runO[tid] = 0.0f;
+  }
+  if (tid == 0) {
+    runM = -INFINITY;
+    runL = 0.0f;
+  }
+  for (int64_t c0 = 0; c0 < k; c0 += kHeadTok) {
+    if (tid < kHeadTok) {
+      const int64_t j = c0 + tid;
+      uint4 cn = make_uint4(0u, 0u, 0u, 0u);
+      uint64_t ka = 0ull, va = 0ull;
+      if (j < k) {
+        cn.x = 1u;  // head 0 of the workgroup, selected once at this position
+        bool rec;
+        const int64_t row = rs.locate(tok_key(ig[j]), bh, rec);
+        if (row >= 0) {
+          ka = reinterpret_cast<uint64_t>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
+          va = reinterpret_cast<uint64_t>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes);
+        }
       }
+      sh.kaddr[tid] = ka;
+      sh.vaddr[tid] = va;
+      sh.cnt[tid] = cn;
     }
-    sh.kaddr[tid] = ka;
-    sh.vaddr[tid] = va;
-    sh.cnt[tid] = cn;
-  }
-  __syncthreads();
-  attn_tokens<G>(sh, reinterpret_cast<uint64_t>(q), scale);
-  __syncthreads();
-  float *pb = part + (bh * nsplit + split) * G * kPartStride;
-  for (int e = tid; e < G * kAttnD; e += kAttnThreads) {
-    const int g = e / kAttnD, d = e % kAttnD;
-    float acc = 0.0f;
+    __syncthreads();
+    attn_tokens<1, kHeadWaves>(sh, reinterpret_cast<uint64_t>(qg), scale);
+    __syncthreads();
+    // fold the group into the running triple (every thread reads runM first)
+    float mc = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < kAttnWaves; ++v) acc += sh.o[v][g][d];
-    pb[g * kPartStride + 2 + d] = acc;
-  }
-  if (tid < G) {
-    float Mg = -INFINITY, Lg = 0.0f;
+    for (int v = 0; v < kHeadWaves; ++v) mc = fmaxf(mc, sh.wm[v][0]);
+    const float Mo = runM, Mn = fmaxf(Mo, mc);
+    const float eo = Mo == -INFINITY ? 0.0f : expf(Mo - Mn), ec = mc == -INFINITY ? 0.0f : expf(mc - Mn);
+    if (tid < kAttnD) {
+      float oc = 0.0f;
 #pragma unroll
-    for (int v = 0; v < kAttnWaves; ++v) {
-      Mg = fmaxf(Mg, sh.wm[v][tid]);
-      Lg += sh.wl[v][tid];
+      for (int v = 0; v < kHeadWaves; ++v) oc += sh.o[v][0][tid];
+      runO[tid] = runO[tid] * eo + oc * ec;
     }
-    pb[tid * kPartStride] = Mg;
-    pb[tid * kPartStride + 1] = Lg;
+    __syncthreads();  // every thread has read runM
+    if (tid == 0) {
+      float lc = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kHeadWaves; ++v) lc += sh.wl[v][0];
+      runL = runL * eo + lc * ec;
+      runM = Mn;
+    }
+    __syncthreads();  // sh is rewritten by the next group
   }
+  if (tid < kAttnD) out[(bh * G + g) * kAttnD + tid] = runO[tid] / runL;
 }
 
 // out[bh, g, d] = sum_s O_s e^(M_s - M) / sum_s L_s e^(M_s - M) over the
@@ -556,13 +574,6 @@ void launch_attn_g(const float *q, const UnionWs &w, int64_t BH, int64_t GK, con
                    int64_t nsplit, hipStream_t st) {
   attn_partial_kernel<G><<<dim3((unsigned)nsplit, (unsigned)BH), kAttnThreads, 0, st>>>(q, w, GK, rs, scale, part,
                                                                                          nsplit);
-}
-
-template <int G>
-void launch_direct_g(const float *q, const int64_t *idx, int64_t BH, int64_t GK, int64_t k, const RowSrc &rs,
-                     float scale, float *part, int64_t nsplit, hipStream_t st) {
-  attn_direct_kernel<G><<<dim3((unsigned)nsplit, (unsigned)BH), kAttnThreads, 0, st>>>(q, idx, GK, k, rs, scale, part,
-                                                                                        nsplit);
 }
 
 }  // namespace
@@ -645,18 +656,9 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
                   cap, nrec, n, (int64_t)kAttnD * 2};
   int rc;
   if (!n_unique) {
-    // per position, no union
-    switch (G) {
-      case 1: launch_direct_g<1>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-      case 2: launch_direct_g<2>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-      case 3: launch_direct_g<3>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-      case 4: launch_direct_g<4>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-      case 5: launch_direct_g<5>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-      case 6: launch_direct_g<6>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-      case 7: launch_direct_g<7>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-      default: launch_direct_g<8>(q, idx, BH, GK, k, rs, scale, part, nsplit, st); break;
-    }
-    rc = launch_status("attn_direct_kernel");
+    // one workgroup per query head over its own positions, no union, no merge
+    attn_head_kernel<<<dim3((unsigned)G, (unsigned)BH), kHeadWaves * kWave, 0, st>>>(q, idx, G, k, rs, scale, out);
+    return launch_status("attn_head_kernel");
   } else {
     // the union list (each distinct row read once), then its groups of kAttnTok tokens
     rc = launch_union(idx, BH, GK, k, n, w, n_unique, st);
