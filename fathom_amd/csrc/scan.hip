@@ -397,6 +397,50 @@ __device__ __forceinline__ float tile_score(const Tile<NQ, RS> &t, const float (
 
 constexpr int kScaleBatch = 8;  // scale loads in flight per lane
 
+// The tile's scale pass: lane i of a block takes the slots s = i (mod 4),
+// kScaleBatch loads in flight; the per-head constants C, the block exponent
+// s_b, and the scales rescaled by 2^-s_b into the wave's LDS buffer.
+template <int NQ, int RS>
+__device__ __forceinline__ void scale_pass(Tile<NQ, RS> &t, const Shared<NQ> &sh, uint16_t (*aw)[kWB],
+                                           __amdgpu_buffer_rsrc_t sr, uint32_t soff, uint32_t sub2, int nact, int lane) {
+  const int b = lane >> 2, i = lane & 3;
+  float amax = 0.0f;
+#pragma unroll
+  for (int h = 0; h < 4 * NQ; ++h) t.cst[h] = 0.0f;
+  for (int s0 = 0; s0 < nact; s0 += 4 * kScaleBatch) {
+    uint16_t raw[kScaleBatch];
+    uint32_t jo[kScaleBatch];
+#pragma unroll
+    for (int m = 0; m < kScaleBatch; ++m) {
+      const int s = s0 + 4 * m + i;
+      jo[m] = (s < nact ? sh.schan[s] : 0u) * sub2 + soff;
+    }
+#pragma unroll
+    for (int m = 0; m < kScaleBatch; ++m) {
+      raw[m] = __builtin_amdgcn_raw_buffer_load_b16(sr, jo[m], 0, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < kScaleBatch; ++m) {
+      const int s = s0 + 4 * m + i;
+      if (s < nact) {
+        aw[s][b] = raw[m];
+        const float av = f16_bits_to_float(raw[m]);
+        amax = fmaxf(amax, av);
+#pragma unroll
+        for (int h = 0; h < 4 * NQ; ++h) t.cst[h] = fmaf(sh.qc[h][s], av, t.cst[h]);
+      }
+    }
+  }
+  amax = quad_max(amax);
+#pragma unroll
+  for (int h = 0; h < 4 * NQ; ++h) t.cst[h] = quad_sum(t.cst[h]);
+  t.sx = __builtin_amdgcn_frexp_expf(amax) - 13;  // a * 2^-sx < 2^13
+  wave_lds_sync();
+  for (int s = i; s < nact; s += 4)
+    aw[s][b] = float_to_f16_bits(ldexpf(f16_bits_to_float(aw[s][b]), -t.sx));
+  wave_lds_sync();
+}
+
 // Scans one wave-tile (blocks beta0 .. beta0 + 15 of row bh) into t.  The first
 // chunk's plane loads are issued before the scale pass, so the two round
 // trips overlap.
@@ -436,42 +480,7 @@ __device__ __forceinline__ void scan_tile(Tile<NQ, RS> &t, const ScanArgs &a, co
   for (int hq = 0; hq < NQ; ++hq)
 #pragma unroll
     for (int k = 0; k < Tile<NQ, RS>::NR; ++k) t.acc[hq][k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  // scales: lane i of a block takes the slots s = i (mod 4), kScaleBatch loads in flight
-  float amax = 0.0f;
-#pragma unroll
-  for (int h = 0; h < 4 * NQ; ++h) t.cst[h] = 0.0f;
-  for (int s0 = 0; s0 < nact; s0 += 4 * kScaleBatch) {
-    uint16_t raw[kScaleBatch];
-    uint32_t jo[kScaleBatch];
-#pragma unroll
-    for (int m = 0; m < kScaleBatch; ++m) {
-      const int s = s0 + 4 * m + i;
-      jo[m] = (s < nact ? sh.schan[s] : 0u) * sub2 + ta.soff;
-    }
-#pragma unroll
-    for (int m = 0; m < kScaleBatch; ++m) {
-      raw[m] = __builtin_amdgcn_raw_buffer_load_b16(ta.sr, jo[m], 0, 0);
-    }
-#pragma unroll
-    for (int m = 0; m < kScaleBatch; ++m) {
-      const int s = s0 + 4 * m + i;
-      if (s < nact) {
-        aw[s][b] = raw[m];
-        const float av = f16_bits_to_float(raw[m]);
-        amax = fmaxf(amax, av);
-#pragma unroll
-        for (int h = 0; h < 4 * NQ; ++h) t.cst[h] = fmaf(sh.qc[h][s], av, t.cst[h]);
-      }
-    }
-  }
-  amax = quad_max(amax);
-#pragma unroll
-  for (int h = 0; h < 4 * NQ; ++h) t.cst[h] = quad_sum(t.cst[h]);
-  t.sx = __builtin_amdgcn_frexp_expf(amax) - 13;  // a * 2^-sx < 2^13
-  wave_lds_sync();
-  for (int s = i; s < nact; s += 4)
-    aw[s][b] = float_to_f16_bits(ldexpf(f16_bits_to_float(aw[s][b]), -t.sx));
-  wave_lds_sync();
+  scale_pass<NQ, RS>(t, sh, aw, ta.sr, ta.soff, sub2, nact, lane);
   const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;  // the lane's 16-bit half of each dword
   const uint16_t *awb = &aw[0][b];
   for (int ck = 0; ck < nck; ++ck) {
@@ -480,6 +489,80 @@ __device__ __forceinline__ void scan_tile(Tile<NQ, RS> &t, const ScanArgs &a, co
       load_chunk(dn, nxt, ta, sub8);
     }
     compute_chunk<NQ, RS, CH>(t, d, cur, sh, awb, ck * CH, i, sel);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) d[k] = dn[k];
+    cur = nxt;
+  }
+}
+
+// Scans the two adjacent wave-tiles of blocks beta0 .. beta0 + 31 (beta0 a
+// multiple of 32, within one superblock: sub a multiple of 32) into tA and tB,
+// for stores in mapped host memory: each load instruction reads one unit of
+// both tiles, 256 contiguous bytes, which zero-copy reads over PCIe serve at
+// the link's rate (128-byte reads run at about 70 % of it).  Lanes 4k, 4k + 1
+// load block k of tile A, lanes 4k + 2, 4k + 3 block k of tile B (8 bytes
+// each); a DPP swap of lane pairs then gives every lane its dword of both.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <int CH>
+__device__ __forceinline__ void load_chunk_pair(u32x2 (&d)[CH], const ChunkDesc<CH> &cd, __amdgpu_buffer_rsrc_t pr,
+                                                uint32_t poff, uint32_t sub8) {
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(pr, poff, (cd.w[k] & 0xFFFFu) * sub8, 0);
+    d[k] = u32x2{v[0], v[1]};
+  }
+}
+
+template <int CH>
+__device__ __forceinline__ void split_pair(const u32x2 (&d)[CH], uint32_t (&dA)[CH], uint32_t (&dB)[CH], int i) {
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const uint32_t px = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[k][0], 0x4E, 0xF, 0xF, false);  // lane i ^ 2
+    const uint32_t py = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[k][1], 0x4E, 0xF, 0xF, false);
+    dA[k] = i < 2 ? d[k][0] : py;  // dword i >> 1 of tile A's block
+    dB[k] = i < 2 ? px : d[k][1];  // dword i >> 1 of tile B's block
+  }
+}
+
+template <int NQ, int CH>
+__device__ __forceinline__ void scan_tile_pair(Tile<NQ, 1> &tA, Tile<NQ, 1> &tB, const ScanArgs &a,
+                                               const Shared<NQ> &sh, uint16_t (*awA)[kWB], uint16_t (*awB)[kWB],
+                                               int64_t bh, int64_t beta0, int U, int nact, int lane) {
+  const int b = lane >> 2, i = lane & 3;
+  const uint32_t sub = (uint32_t)a.sub, sb0 = (uint32_t)beta0 / sub, off0 = (uint32_t)beta0 - sb0 * sub;
+  const uint32_t *pb = a.planes + ((bh * a.nsb + sb0) * a.D * 4) * a.sub * 2;
+  const uint16_t *sbp = a.scales + ((bh * a.nsb + sb0) * a.D) * a.sub;
+  const __amdgpu_buffer_rsrc_t pr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(pb), (short)0, 0x7FFFFFFF, kBufFlags);
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(sbp), (short)0, 0x7FFFFFFF, kBufFlags);
+  const uint32_t poff = (off0 + (uint32_t)b + (i >= 2 ? (uint32_t)kWB : 0u)) * 8u;
+  const uint32_t sub8 = (uint32_t)(a.sub * 8), sub2 = (uint32_t)(a.sub * 2);
+  const int nck = (U + CH - 1) / CH;
+  u32x2 d[CH], dn[CH];
+  ChunkDesc<CH> cur, nxt;
+  if (nck > 0) {
+    read_descs(cur, sh.desc, 0);
+    load_chunk_pair(d, cur, pr, poff, sub8);
+  }
+#pragma unroll
+  for (int hq = 0; hq < NQ; ++hq)
+#pragma unroll
+    for (int k = 0; k < kR; ++k) tA.acc[hq][k] = tB.acc[hq][k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  scale_pass<NQ, 1>(tA, sh, awA, sr, (off0 + (uint32_t)b) * 2u, sub2, nact, lane);
+  scale_pass<NQ, 1>(tB, sh, awB, sr, (off0 + kWB + (uint32_t)b) * 2u, sub2, nact, lane);
+  const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;  // the lane's 16-bit half of each dword
+  const uint16_t *awbA = &awA[0][b], *awbB = &awB[0][b];
+  for (int ck = 0; ck < nck; ++ck) {
+    if (ck + 1 < nck) {
+      read_descs(nxt, sh.desc, (ck + 1) * CH);
+      load_chunk_pair(dn, nxt, pr, poff, sub8);
+    }
+    uint32_t dA[CH], dB[CH];
+    split_pair(d, dA, dB, i);
+    compute_chunk<NQ, 1, CH>(tA, dA, cur, sh, awbA, ck * CH, i, sel);
+    compute_chunk<NQ, 1, CH>(tB, dB, cur, sh, awbB, ck * CH, i, sel);
 #pragma unroll
     for (int k = 0; k < CH; ++k) d[k] = dn[k];
     cur = nxt;
@@ -624,9 +707,12 @@ __device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t
 // that misled T_hi), rescans the row with T_lo into the regions under the
 // second count array -- slowly, with its four waves alone, but only for such
 // rows.  Nothing waits on another workgroup.
-template <int NQ, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 1 && MODE != kEmitSample ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
+// PAIR (stores in mapped host memory, sub a multiple of 32): the first pass
+// scans pairs of adjacent wave-tiles with 256-byte loads (scan_tile_pair).
+template <int NQ, int MODE, bool PAIR = false>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 1 && MODE != kEmitSample && !PAIR ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
   __shared__ Shared<NQ> sh;
+  __shared__ uint16_t awB[PAIR ? kWaves : 1][kMaxD][kWB];  // tile B's scale buffers
   __shared__ uint32_t s_tot[8], s_wt[kWaves][8];
   __shared__ uint32_t s_last;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -691,6 +777,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 
         Ls = kWaves;
       }
       uint32_t *rcp = fb ? em.sel.rc2 : em.sel.rc1;
+      if constexpr (PAIR) {
+        if (!fb) {
+          // pairs of tiles (2 P, 2 P + 1); then the padding regions' zero counts
+          const int64_t npair = (a.nwt + 1) / 2;
+          for (int64_t P = L0; P < npair; P += Ls) {
+            const int64_t LA = 2 * P, LB = LA + 1;
+            const int64_t beta0 = (a.wt0 + LA) * kWB;
+            if (beta0 >= a.blk_end || beta0 + 2 * kWB <= a.blk0) continue;  // uniform per wave
+            set_priority_by_tiles_left((npair - 1 - P) / Ls);
+            Tile<NQ, 1> tB;
+            tB.r0 = 0;
+            scan_tile_pair<NQ, kChunk>(t, tB, a, sh, aw, awB[wave], bh, beta0, U, nact, lane);
+            if constexpr (MODE == kEmitScores) {
+              emit_scores<NQ>(em, t, sh, a, bh, beta0, lane);
+              if (LB < a.nwt) emit_scores<NQ>(em, tB, sh, a, bh, beta0 + kWB, lane);
+            }
+            if constexpr (MODE == kEmitFilter) {
+              emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, fb, skipm, tot);
+              if (LB < a.nwt) emit_filter<NQ>(em, tB, sh, a, bh, beta0 + kWB, lane, fb, skipm, tot);
+            }
+            wave_lds_sync();  // the wave's scale buffers are rewritten by its next pair
+          }
+          if constexpr (kCand)
+            for (int64_t L = a.nwt + L0; L < nlist; L += Ls)
+              if (lane < a.G) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
+          continue;
+        }
+      }
       for (int64_t L = L0; L < nlist; L += Ls) {
         if (kCand && L >= a.nwt) {
           if (lane < a.G && !((skipm >> lane) & 1u)) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
@@ -711,7 +825,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 
 // --------------------------------------------------------------------- launch
 constexpr int64_t kTargetWaves = 4096;  // waves of a full launch (4 per SIMD on 256 CUs)
 
-template <int MODE>
+template <int MODE, bool PAIR = false>
 int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, hipStream_t st) {
   if (nwt <= 0) return FATHOM_OK;
   ScanArgs a = a0;
@@ -719,17 +833,36 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, hip
   int64_t wgs = cdiv(nwt, kWaves);
   if (MODE == kEmitSample) {
     wgs = nwt;  // one tile per workgroup
+  } else if (PAIR) {
+    // pairs of tiles; two waves per SIMD fill the chip (the pair variant's registers)
+    const int64_t npair = (nwt + 1) / 2, per = cdiv(npair * BH, kTargetWaves / 2);
+    wgs = cdiv(cdiv(npair, per), kWaves);
   } else {
     // enough waves to fill the chip, each taking a whole number of tiles
     const int64_t per = cdiv(nwt * BH, kTargetWaves);
     wgs = cdiv(cdiv(nwt, per), kWaves);
   }
   const dim3 grid((unsigned)wgs, (unsigned)BH);
-  if (a.G <= 4)
+  if constexpr (PAIR)
+    scan_wave_kernel<1, MODE, true><<<grid, kThreads, 0, st>>>(a, em);  // G <= 4 (pair_scan)
+  else if (a.G <= 4)
     scan_wave_kernel<1, MODE><<<grid, kThreads, 0, st>>>(a, em);
   else
     scan_wave_kernel<2, MODE><<<grid, kThreads, 0, st>>>(a, em);
   return launch_status("scan_wave_kernel");
+}
+
+// Planes in mapped host memory (read zero-copy over PCIe) in superblocks of a
+// multiple of 32 blocks: the paired-tile first pass applies.
+bool pair_scan(const ScanArgs &a) {
+  // one query-row tile: two row tiles of the pair would spill
+  if (a.G > 4 || a.sub % (2 * kWB) != 0 || a.wt0 != 0 || a.wt_stride != 1) return false;
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, a.planes) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return attr.type == hipMemoryTypeHost;
 }
 
 int check_scan(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
@@ -795,6 +928,7 @@ extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t
   a.wt0 = blk0 / kWB;
   Emit em{};
   em.out = out;
+  if (pair_scan(a)) return launch_scan<kEmitScores, true>(a, cdiv(blk_end, kWB) - a.wt0, BH, em, (hipStream_t)stream);
   return launch_scan<kEmitScores>(a, cdiv(blk_end, kWB) - a.wt0, BH, em, (hipStream_t)stream);
 }
 
@@ -871,7 +1005,7 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
     // T_hi may exceed a row's kk-th largest key (r_hi < kk): the candidate pass
     // then checks every row and rescans those with fewer than kk candidates
     em.fallback_check = r_hi < kk ? 1 : 0;
-    rc = launch_scan<kEmitFilter>(a, nwt, BH, em, st);
+    rc = pair_scan(a) ? launch_scan<kEmitFilter, true>(a, nwt, BH, em, st) : launch_scan<kEmitFilter>(a, nwt, BH, em, st);
     if (rc) return rc;
   }
   return (stages & FATHOM_STAGE_FINALIZE) ? launch_finalize(rows, m, k, sink, local, em.sel, idx, st) : FATHOM_OK;

@@ -569,6 +569,71 @@ def test_scan_topk_fused_host_resident():
         off.free_host(hp2)
 
 
+@pytest.mark.parametrize("cfg,n,sub,G", [(2, 50000, 32, None), (2, 65536, 64, None), (3, 33000, 32, None),
+                                         (3, 100000, 64, None), (2, 40000, "whole", None), (1, 50000, 32, None),
+                                         (2, 50000, 32, 8)])
+def test_scan_host_resident_paired_tiles(cfg, n, sub, G):
+    """Host-mapped stores with superblocks of a multiple of 32 blocks take the
+    paired-tile first pass (256-byte reads; G <= 4 only): scores and the fused
+    top-k equal the HBM store's bit for bit, for odd and even tile counts (the
+    odd count's last pair has no second tile) and for G = 8, which keeps the
+    single-tile pass."""
+    print(f"[paired-host] cfg={cfg} n={n} sub={sub} G={G}", flush=True)
+    s = math.ceil(n / 64) if sub == "whole" else sub
+    x, st, plan = _scan_case(cfg, n, 2, sub=s)
+    q = x["q"].to(DEV)
+    if G is not None:
+        q = torch.randn(2, G, q.shape[-1], generator=torch.Generator().manual_seed(3)).to(DEV)
+    k = 512 if n > 32768 else 128
+    ref_s = st.scan(q, plan).clone()
+    ref_i = st.scan_topk(q, plan, k)
+    _, pl_dev, hp1 = off.host_mapped(st.planes_k)
+    _, sc_dev, hp2 = off.host_mapped(st.scales_k)
+    try:
+        st.planes32, st.scales_k = pl_dev, sc_dev
+        got_s = st.scan(q, plan)
+        got_i = st.scan_topk(q, plan, k)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got_s, ref_s, rtol=0, atol=0)
+        torch.testing.assert_close(got_i, ref_i, rtol=0, atol=0)
+    finally:
+        off.free_host(hp1)
+        off.free_host(hp2)
+
+
+def test_scan_topk_fallback_pass_host_paired():
+    """The fallback pass (single tiles) after a paired first pass: a falling
+    row in a host-mapped store of 64-block superblocks."""
+    BH, d, n = 2, 128, 90000
+    K = torch.zeros(BH, n, d)
+    K[:, :, 0] = torch.linspace(1, -1, n)[None] * 3.0
+    K[:, :, 1] = torch.randn(BH, n, generator=torch.Generator().manual_seed(5)) * 0.01
+    bp.SUB = 64
+    try:
+        st = bp.PlaneStore(K.to(DEV))
+    finally:
+        bp.SUB = 16
+    q = torch.zeros(BH, 4, d)
+    q[:, :, 0] = 1.0
+    q[:, 1::2, 1] = 1.0
+    g = torch.ones(BH, d)
+    g[:, 0] = 1000.0
+    g[:, 1] = 10.0
+    plan = bp.make_plan(g.to(DEV), 6.0)
+    q = q.to(DEV)
+    ref = bp.sink_local_topk(st.scan(q, plan), 512)
+    _, pl_dev, hp1 = off.host_mapped(st.planes_k)
+    _, sc_dev, hp2 = off.host_mapped(st.scales_k)
+    try:
+        st.planes32, st.scales_k = pl_dev, sc_dev
+        got = st.scan_topk(q, plan, 512)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    finally:
+        off.free_host(hp1)
+        off.free_host(hp2)
+
+
 @pytest.mark.parametrize("direction,n", [(1.0, 90000), (-1.0, 90000), (1.0, 300000)])
 def test_scan_topk_fallback_pass(direction, n):
     """Fused path with scores falling (or rising) along the sequence: a falling
