@@ -55,6 +55,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--stages-only", action="store_true", help="scan + top-k only (for profiling runs)")
+    ap.add_argument("--host-scan-only", action="store_true",
+                    help="only the fused scan + top-k over the host-mapped store, --steps calls after --warmup "
+                         "(for rocprofv3 --pmc runs of the zero-copy scan); raises if its indices differ from "
+                         "the HBM store's")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the run, launch a plain fp32 device copy kernel of this many MiB 3 times "
                          "(the known-size kernel that scales rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
@@ -507,6 +511,61 @@ def cpu_baseline(W):
             "config1": {"all_threads": c1_all, "single_thread": c1_one}}
 
 
+def calib_copy(torch, dev, mib):
+    """torch's elementwise copy kernel, 3 launches that each read and write mib
+    MiB: the known-size kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE."""
+    if mib <= 0:
+        return
+    src = torch.ones(mib << 18, device=dev, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    log(f"[bench] calibration copy: 3 x {mib} MiB read + written")
+
+
+def host_scan_only(torch, bp, off, x, store, steps, warmup):
+    """The zero-copy fused scan + top-k alone, over a HOST_SUB-superblock store
+    in mapped pinned host memory: the command profiled for the bytes the scan
+    pulls over PCIe (FETCH_SIZE) against bytes_planes."""
+    plan = bp.make_plan(x["g"], x["budget"])
+    args = (x["q"], plan, x["k"], x["sink"], x["local"])
+    ref = store.scan_topk(*args)
+    bp.SUB = HOST_SUB
+    try:
+        hsrc = bp.PlaneStore(x["K"], keep_code=False)
+    finally:
+        bp.SUB = 16
+    hps = []
+    try:
+        _, pl_dev, h = off.host_mapped(hsrc.planes_k)
+        hps.append(h)
+        _, sc_dev, h = off.host_mapped(hsrc.scales_k)
+        hps.append(h)
+        hstore = bp.PlaneStore.__new__(bp.PlaneStore)
+        hstore.BH, hstore.n, hstore.nsb, hstore.sub = hsrc.BH, hsrc.n, hsrc.nsb, hsrc.sub
+        hstore.planes32, hstore.scales_k = pl_dev, sc_dev
+        del hsrc
+        for _ in range(warmup):
+            idx = hstore.scan_topk(*args)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            idx = hstore.scan_topk(*args)
+        e1.record()
+        torch.cuda.synchronize()
+        if not bool(torch.equal(idx, ref)):
+            raise RuntimeError("host-resident (zero-copy) index sets differ from the HBM path's")
+        ms = e0.elapsed_time(e1) / steps
+        by = bp.bytes_planes(plan["t"], x["n"])
+        log(f"[bench] host-scan-only: {steps} fused calls, {ms:.4f} ms each, bytes_planes {by}, "
+            f"{by / (ms * 1e-3) / 1e9:.1f} GB/s")
+    finally:
+        for h in hps:
+            off.free_host(h)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -529,6 +588,10 @@ def main():
     log(f"[bench] inputs + store built in {time.perf_counter() - t0:.1f} s: {W.CONFIGS[a.config]['name']}"
         f" n={x['n']}")
 
+    if a.host_scan_only:
+        host_scan_only(torch, bp, off, x, store, a.steps, a.warmup)
+        calib_copy(torch, dev, a.calib_copy_mib)
+        return
     hbm = run_regime(torch, bp, off, x, store, x["K"], V, a.steps, a.warmup, a.stages_only)
     st = hbm["stage_ms"]
     n, BH = x["n"], x["BH"]
@@ -631,14 +694,7 @@ def main():
             for h in hps:
                 off.free_host(h)
 
-    if a.calib_copy_mib > 0:
-        # torch's elementwise copy kernel: reads and writes calib_copy_mib MiB per launch
-        src = torch.ones(a.calib_copy_mib << 18, device=dev, dtype=torch.float32)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.mul(src, 1.0, out=dst)
-        torch.cuda.synchronize()
-        log(f"[bench] calibration copy: 3 x {a.calib_copy_mib} MiB read + written")
+    calib_copy(torch, dev, a.calib_copy_mib)
 
     ktab = None
     if not a.no_decode and not a.stages_only and a.n is None:
