@@ -25,6 +25,8 @@ PROTOTYPES = {
     "fathom_to_superblocks": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "fathom_dequant_planes": (_i32, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "fathom_make_plan": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fathom_make_plan_uniform": (_i32, [_vp, ctypes.c_float, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                        _vp, _vp]),
     "fathom_scan_planes": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp, _vp]),
     "fathom_pack_chan4": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),

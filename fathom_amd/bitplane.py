@@ -199,9 +199,6 @@ def make_plan(g, budget, bmax=4, iters=30):
     _need_gpu(g)
     BH, d = g.shape
     dev = g.device
-    if not torch.is_tensor(budget):
-        budget = torch.full((BH,), float(budget), device=dev)
-    budget = budget.to(device=dev, dtype=torch.float32).expand(BH).contiguous()
     gf = g.contiguous().float()
     t = torch.empty(BH, d, dtype=torch.int8, device=dev)
     pairs = torch.empty(BH, d * bmax, dtype=torch.int32, device=dev)
@@ -210,8 +207,12 @@ def make_plan(g, budget, bmax=4, iters=30):
     nact = torch.empty(BH, dtype=torch.int32, device=dev)
     cls = torch.empty(BH, bmax, d, dtype=torch.int32, device=dev)
     clsn = torch.empty(BH, bmax, dtype=torch.int32, device=dev)
-    _lib.call("fathom_make_plan", _ptr(gf), _ptr(budget), BH, d, int(bmax), int(iters), _ptr(t), _ptr(pairs),
-              _ptr(npairs), _ptr(act), _ptr(nact), _ptr(cls), _ptr(clsn), _stream(dev))
+    outs = (_ptr(t), _ptr(pairs), _ptr(npairs), _ptr(act), _ptr(nact), _ptr(cls), _ptr(clsn), _stream(dev))
+    if torch.is_tensor(budget):
+        budget = budget.to(device=dev, dtype=torch.float32).expand(BH).contiguous()
+        _lib.call("fathom_make_plan", _ptr(gf), _ptr(budget), BH, d, int(bmax), int(iters), *outs)
+    else:  # one float for every row: a kernel argument
+        _lib.call("fathom_make_plan_uniform", _ptr(gf), float(budget), BH, d, int(bmax), int(iters), *outs)
     return {"t": t, "pairs": pairs, "npairs": npairs, "act": act, "nact": nact, "cls": cls, "clsn": clsn}
 
 

@@ -44,9 +44,23 @@ __device__ float flog2(float x) {
   return (float)r;
 }
 
+// Exact sum of the 64 lanes' integers, in every lane: DPP row sums (quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the four row sums
+// read out and added -- a dependent chain of four DPP adds, where bit-sliced
+// ballots take a VALU-to-SALU round per bit.
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+  v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
+}
+
 template <int CPL>
-__global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, const float *__restrict__ budget, int D,
-                                                  int bmax, int iters, int8_t *__restrict__ t_out,
+__global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, const float *__restrict__ budget,
+                                                  float budget_value, int D, int bmax, int iters,
+                                                  int8_t *__restrict__ t_out,
                                                   int32_t *__restrict__ pairs, int32_t *__restrict__ npairs,
                                                   int32_t *__restrict__ act, int32_t *__restrict__ nact,
                                                   int32_t *__restrict__ cls, int32_t *__restrict__ clsn) {
@@ -64,15 +78,18 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
   // depths are integers in [0, bmax]: a lane's sum is below 2^6, the row's
   // (an exact integer) equals the float sum in any order
   constexpr int kSumBits = CPL <= 1 ? 4 : CPL <= 2 ? 5 : 6;
-  const float Br = budget[bh];
-  float lo = -60.0f, hi = 60.0f;
-  for (int it = 0; it < iters; ++it) {
-    const float mid = (lo + hi) * 0.5f;
+  const float Br = budget ? budget[bh] : budget_value;
+  // the row's depth total at water line mid exceeds the budget
+  auto over = [&](float mid) {
     int s = 0;
 #pragma unroll
     for (int k = 0; k < CPL; ++k) s += (int)fminf(fmaxf(rintf((lg[k] - mid) * 0.5f), 0.0f), bm);
-    const float tot = (float)wave_sum_small<kSumBits>(s);
-    if (tot > Br) lo = mid; else hi = mid;
+    return (float)wave_sum_dpp(s) > Br;
+  };
+  float lo = -60.0f, hi = 60.0f;
+  for (int it = 0; it < iters; ++it) {
+    const float mid = (lo + hi) * 0.5f;
+    if (over(mid)) lo = mid; else hi = mid;
   }
   int t[CPL];
   int cnt_act = 0, cnt_pairs = 0;
@@ -153,10 +170,12 @@ __global__ __launch_bounds__(64) void channel_list_kernel(const uint8_t *__restr
 
 using namespace fathom;
 
-extern "C" int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D, int bmax, int iters,
-                                int8_t *t, int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls,
-                                int32_t *clsn, void *stream) {
-  if (!g || !budget || !t || !pairs || !npairs || !act || !nact || !cls || !clsn)
+namespace fathom {
+namespace {
+int make_plan_run(const float *g, const float *budget, float budget_value, int64_t BH, int64_t D, int bmax, int iters,
+                  int8_t *t, int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls, int32_t *clsn,
+                  void *stream) {
+  if (!g || !t || !pairs || !npairs || !act || !nact || !cls || !clsn)
     return fail(FATHOM_ERR_INVALID, "make_plan: null pointer");
   if (BH < 1 || BH > 0x7FFFFFFF) return fail(FATHOM_ERR_INVALID, "make_plan: BH=%lld unsupported", (long long)BH);
   if (D < 1 || D > 256) return fail(FATHOM_ERR_INVALID, "make_plan: D=%lld outside [1, 256]", (long long)D);
@@ -164,13 +183,29 @@ extern "C" int fathom_make_plan(const float *g, const float *budget, int64_t BH,
   if (iters < 0 || iters > 200) return fail(FATHOM_ERR_INVALID, "make_plan: iters=%d outside [0, 200]", iters);
   hipStream_t st = (hipStream_t)stream;
   const int d = (int)D;
+  const float bv = budget_value;
   if (D <= 64)
-    plan_kernel<1><<<(unsigned)BH, 64, 0, st>>>(g, budget, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
+    plan_kernel<1><<<(unsigned)BH, 64, 0, st>>>(g, budget, bv, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
   else if (D <= 128)
-    plan_kernel<2><<<(unsigned)BH, 64, 0, st>>>(g, budget, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
+    plan_kernel<2><<<(unsigned)BH, 64, 0, st>>>(g, budget, bv, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
   else
-    plan_kernel<4><<<(unsigned)BH, 64, 0, st>>>(g, budget, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
+    plan_kernel<4><<<(unsigned)BH, 64, 0, st>>>(g, budget, bv, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
   return launch_status("plan_kernel");
+}
+}  // namespace
+}  // namespace fathom
+
+extern "C" int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D, int bmax, int iters,
+                                int8_t *t, int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls,
+                                int32_t *clsn, void *stream) {
+  if (!budget) return fail(FATHOM_ERR_INVALID, "make_plan: null pointer");
+  return make_plan_run(g, budget, 0.0f, BH, D, bmax, iters, t, pairs, npairs, act, nact, cls, clsn, stream);
+}
+
+extern "C" int fathom_make_plan_uniform(const float *g, float budget, int64_t BH, int64_t D, int bmax, int iters,
+                                        int8_t *t, int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact,
+                                        int32_t *cls, int32_t *clsn, void *stream) {
+  return make_plan_run(g, nullptr, budget, BH, D, bmax, iters, t, pairs, npairs, act, nact, cls, clsn, stream);
 }
 
 extern "C" int fathom_channel_list(const uint8_t *active, int64_t BH, int64_t D, int32_t *act, int32_t *nact,

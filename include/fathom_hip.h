@@ -98,6 +98,16 @@ int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D,
                      void *stream);
 
 /*
+ * make_plan with one budget for every row (kernels/bitplane.py:83-116 called
+ * with a float budget, as scripts/B_kernel_bench.py:74 does): the value is a
+ * kernel argument, so no device copy of it is made per call.  Outputs and
+ * limits as fathom_make_plan.
+ */
+int fathom_make_plan_uniform(const float *g, float budget, int64_t BH, int64_t D, int bmax, int iters, int8_t *t,
+                             int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls,
+                             int32_t *clsn, void *stream);
+
+/*
  * PlaneStore.scan (kernels/bitplane.py:319-338, scan_planes_cls_kernel :275-307):
  * out[bh, g, tok] = sum_j q[bh, g, j] * value_{t_j}(tok, j) over the channels of
  * the plan's depth classes 1..min(bmax, 4), for the 64-token blocks [blk0, blk1)

@@ -51,6 +51,8 @@ def test_workspace_queries_and_argument_errors_without_gpu():
     assert rc == _lib.ERR_INVALID and b"null" in L.fathom_last_error()
     with pytest.raises(ValueError):
         _lib.check(rc, "fathom_make_plan")
+    rc = L.fathom_make_plan_uniform(None, 48.0, 1, 128, 4, 30, None, None, None, None, None, None, None, None)
+    assert rc == _lib.ERR_INVALID and b"null" in L.fathom_last_error()
 
 
 def test_python_api_rejects_host_tensors():

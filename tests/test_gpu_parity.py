@@ -127,12 +127,20 @@ def test_make_plan_torch_is_the_plan_depths():
 
 
 def test_make_plan_scalar_budget_and_iters():
+    """The scalar-budget entry point (fathom_make_plan_uniform) and every
+    bisection count modulo the kernel's three-step rounds (30, 29, 28, ...):
+    the oracle's one-step bisection bit for bit, and the tensor-budget call."""
     rng = np.random.default_rng(9)
     g = np.exp(rng.standard_normal((8, 128)) * 2).astype(np.float32)
-    for it in (30, 10, 0):
-        ref = O.make_plan(g, 48.0, iters=it)
-        got = bp.make_plan(torch.from_numpy(g).to(DEV), 48.0, iters=it)
-        np.testing.assert_array_equal(got["t"].cpu().numpy(), ref["t"])
+    gd = torch.from_numpy(g).to(DEV)
+    for budget in (48.0, 47.5, 0.3, 700.0):
+        for it in (30, 29, 28, 10, 2, 1, 0):
+            ref = O.make_plan(g, budget, iters=it)
+            got = bp.make_plan(gd, budget, iters=it)
+            tens = bp.make_plan(gd, torch.full((8,), budget, device=DEV), iters=it)
+            for key in ("t", "pairs", "npairs", "act", "nact", "cls", "clsn"):
+                np.testing.assert_array_equal(got[key].cpu().numpy(), ref[key], err_msg=f"{key} {budget} {it}")
+                assert torch.equal(got[key], tens[key])
 
 
 def test_make_plan_worked_example():
@@ -634,16 +642,17 @@ def test_scan_topk_fallback_pass_host_paired():
         off.free_host(hp2)
 
 
-@pytest.mark.parametrize("direction,n", [(1.0, 90000), (-1.0, 90000), (1.0, 300000)])
-def test_scan_topk_fallback_pass(direction, n):
+@pytest.mark.parametrize("direction,n,BH", [(1.0, 90000, 2), (-1.0, 90000, 2), (1.0, 300000, 2), (-1.0, 200000, 8)])
+def test_scan_topk_fallback_pass(direction, n, BH):
     """Fused path with scores falling (or rising) along the sequence: a falling
     row has its top kk inside the first sampled tile, so the tight threshold
     falls short and the fallback scan runs; the result equals the unfused one.
     The scores are coarse (few distinct values), so the fallback pass's
     candidates at the longer length outgrow one workgroup's LDS and are
-    selected from the regions in place."""
-    print(f"[fused-fallback] direction={direction} n={n}", flush=True)
-    BH, d = 2, 128
+    selected from the regions in place.  BH = 8 at n = 200000: 392
+    candidate-pass workgroups over eight rows."""
+    print(f"[fused-fallback] direction={direction} n={n} BH={BH}", flush=True)
+    d = 128
     K = torch.zeros(BH, n, d)
     K[:, :, 0] = torch.linspace(1, -1, n)[None] * 3.0 * direction
     K[:, :, 1] = torch.randn(BH, n) * 0.01
