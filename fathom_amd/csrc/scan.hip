@@ -55,6 +55,7 @@ namespace {
 constexpr int kWB = 16;                // token blocks per wave-tile: one MFMA product each
 constexpr int kWTok = kWB * kBlk;      // tokens per wave-tile
 constexpr int kR = 16;                 // tokens per lane (16 i + r)
+static_assert(kR == kGroupTok, "a lane's tokens are one group of the group maxima");
 constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxD = 128;             // the reference's head dimension (kernels/bitplane.py:313)
@@ -71,7 +72,7 @@ struct h2x2 {
   h2 a, b;
 };
 
-enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2 };
+enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2, kEmitScoresMax = 3 };
 
 struct ScanArgs {
   const float *q;          // [BH, G, D]
@@ -89,6 +90,7 @@ struct ScanArgs {
 
 struct Emit {
   float *out;        // scores [BH, G, n]
+  uint32_t *gmax;    // kEmitScoresMax: [BH * G, ceil(n / 16)] each 16-token group's largest masked key
   uint32_t *samp;    // sampled keys [BH * G, samp_cap]: list entry L at L * kWTok
   int64_t samp_cap;
   TopkSel sel;       // thresholds + candidate regions
@@ -578,7 +580,28 @@ __device__ __forceinline__ float threshold_value(uint32_t thr) {
 }
 
 // Scores [BH, G, n]: the lane's 16 tokens of a head are 64 contiguous bytes.
-template <int NQ>
+// Largest key of the lane's 16 scores, sink/local-masked (-inf), past n
+// excluded: a max over the floats (which passes NaN over) and a NaN test of
+// pairs, then one key -- the maximum of the 16 keys.
+__device__ __forceinline__ uint32_t group_max_key(const float (&s)[kR], int64_t tok0, int64_t n, int64_t sink,
+                                                  int64_t lstart, bool plain) {
+  float v[kR];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const int64_t tok = tok0 + r;
+    v[r] = plain || (tok < n && tok >= sink && tok < lstart) ? s[r] : -INFINITY;
+  }
+  float mx = -INFINITY;
+  bool nan = false;
+#pragma unroll
+  for (int r = 0; r < kR; r += 2) {
+    mx = fmaxf(mx, fmaxf(v[r], v[r + 1]));
+    nan |= __builtin_isunordered(v[r], v[r + 1]);
+  }
+  return nan ? 0xFFFFFFFFu : score_key(mx);
+}
+
+template <int NQ, bool GMAX = false>
 __device__ __forceinline__ void emit_scores(const Emit &em, const Tile<NQ, 1> &t, const Shared<NQ> &sh, const ScanArgs &a,
                                             int64_t bh, int64_t beta0, int lane) {
   const int b = lane >> 2, i = lane & 3;
@@ -586,6 +609,8 @@ __device__ __forceinline__ void emit_scores(const Emit &em, const Tile<NQ, 1> &t
   if (beta < a.blk0 || beta >= a.blk_end) return;
   const int64_t tok0 = beta * kBlk + 16 * i;
   const bool whole = tok0 + kR <= a.n && (a.n & 3) == 0;
+  const bool plain = tok0 + kR <= a.n && tok0 >= em.sink && tok0 + kR <= em.lstart;
+  const int64_t ngrp = (a.n + kR - 1) / kR;
 #pragma unroll
   for (int h = 0; h < 4 * NQ; ++h) {
     if (h >= a.G) break;
@@ -594,6 +619,8 @@ __device__ __forceinline__ void emit_scores(const Emit &em, const Tile<NQ, 1> &t
     head_factors(f, t, sh, h);
 #pragma unroll
     for (int r = 0; r < kR; ++r) s[r] = tile_score<NQ, 1>(t, f, r, h);
+    if (GMAX && tok0 < a.n)
+      em.gmax[(bh * a.G + h) * ngrp + beta * 4 + i] = group_max_key(s, tok0, a.n, em.sink, em.lstart, plain);
     if (whole) {
 #pragma unroll
       for (int r = 0; r < kR; r += 4) *reinterpret_cast<float4 *>(dst + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
@@ -710,7 +737,8 @@ __device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t
 // PAIR (stores in mapped host memory, sub a multiple of 32): the first pass
 // scans pairs of adjacent wave-tiles with 256-byte loads (scan_tile_pair).
 template <int NQ, int MODE, bool PAIR = false>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 1 && MODE != kEmitSample && !PAIR ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
+    NQ == 1 && MODE != kEmitSample && MODE != kEmitScoresMax && !PAIR ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
   __shared__ Shared<NQ> sh;
   __shared__ uint16_t awB[PAIR ? kWaves : 1][kMaxD][kWB];  // tile B's scale buffers
   __shared__ uint32_t s_tot[8], s_wt[kWaves][8];
@@ -789,9 +817,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 
             Tile<NQ, 1> tB;
             tB.r0 = 0;
             scan_tile_pair<NQ, kChunk>(t, tB, a, sh, aw, awB[wave], bh, beta0, U, nact, lane);
-            if constexpr (MODE == kEmitScores) {
-              emit_scores<NQ>(em, t, sh, a, bh, beta0, lane);
-              if (LB < a.nwt) emit_scores<NQ>(em, tB, sh, a, bh, beta0 + kWB, lane);
+            if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax) {
+              emit_scores<NQ, MODE == kEmitScoresMax>(em, t, sh, a, bh, beta0, lane);
+              if (LB < a.nwt) emit_scores<NQ, MODE == kEmitScoresMax>(em, tB, sh, a, bh, beta0 + kWB, lane);
             }
             if constexpr (MODE == kEmitFilter) {
               emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, fb, skipm, tot);
@@ -814,7 +842,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 
         if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
         set_priority_by_tiles_left((nlist - 1 - L) / Ls);
         scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
-        if constexpr (MODE == kEmitScores) emit_scores<NQ>(em, t, sh, a, bh, beta0, lane);
+        if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax)
+          emit_scores<NQ, MODE == kEmitScoresMax>(em, t, sh, a, bh, beta0, lane);
         if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, fb, skipm, tot);
         wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
       }
@@ -937,7 +966,7 @@ namespace fathom {
 // scores ([rows, n] fp32) for one row-select launch; longer rows the sampled
 // keys and the candidate regions.
 size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k) {
-  if (n <= kRowSelectMax) return ws_align((size_t)rows * (size_t)n * 4);
+  if (n <= kRowSelectMax) return ws_align((size_t)rows * (size_t)n * 4) + ws_align((size_t)rows * cdiv(n, kGroupTok) * 4);
   return topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
 }  // namespace fathom
@@ -974,15 +1003,21 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   a.wt0 = 0;
   const int64_t nwt = cdiv(nblk, kWB);
   if (n <= kRowSelectMax) {
-    // short rows: the scores in the workspace (the candidate stage), then the
-    // whole rows selected in one launch (the finalize stage)
+    // short rows: the scores and their 16-token group maxima in the workspace
+    // (the candidate stage), then the rows selected in one launch from the
+    // groups that can hold a top-kk key (the finalize stage)
     Emit es{};
     es.out = static_cast<float *>(workspace);
+    es.gmax = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + ws_align((size_t)rows * (size_t)n * 4));
+    es.sink = sink;
+    es.lstart = (m - local) > 0 ? (m - local) : 0;
     if (stages & FATHOM_STAGE_CANDIDATES) {
-      rc = launch_scan<kEmitScores>(a, nwt, BH, es, st);
+      rc = pair_scan(a) ? launch_scan<kEmitScoresMax, true>(a, nwt, BH, es, st)
+                        : launch_scan<kEmitScoresMax>(a, nwt, BH, es, st);
       if (rc) return rc;
     }
-    return (stages & FATHOM_STAGE_FINALIZE) ? launch_rowselect(es.out, rows, n, m, k, sink, local, idx, st) : FATHOM_OK;
+    return (stages & FATHOM_STAGE_FINALIZE) ? launch_rowselect_gmax(es.out, es.gmax, rows, n, m, k, sink, local, idx, st)
+                                            : FATHOM_OK;
   }
   Emit em{};
   int64_t S = 1;

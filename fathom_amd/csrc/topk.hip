@@ -797,6 +797,223 @@ __global__ __launch_bounds__(kFinThreads) void rowselect_kernel(const float *__r
   select_sorted(ArraySrc{ss, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl + 2 * kMaxK, cl, sh, s_cnt, false);
 }
 
+// Wave-wide minimum and maximum of 32-bit values (in every lane): DPP row
+// reductions, then the four rows' results read out.
+template <int CTL>
+__device__ __forceinline__ void minmax_dpp(uint32_t &mn, uint32_t &mx) {
+  mn = min(mn, (uint32_t)__builtin_amdgcn_mov_dpp((int)mn, CTL, 0xF, 0xF, false));
+  mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, CTL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void wave_minmax_u32(uint32_t &mn, uint32_t &mx) {
+  minmax_dpp<0xB1>(mn, mx);   // quad_perm [1,0,3,2]
+  minmax_dpp<0x4E>(mn, mx);   // quad_perm [2,3,0,1]
+  minmax_dpp<0x141>(mn, mx);  // row_half_mirror
+  minmax_dpp<0x140>(mn, mx);  // row_mirror
+  mn = min(min((uint32_t)__builtin_amdgcn_readlane((int)mn, 0), (uint32_t)__builtin_amdgcn_readlane((int)mn, 16)),
+           min((uint32_t)__builtin_amdgcn_readlane((int)mn, 32), (uint32_t)__builtin_amdgcn_readlane((int)mn, 48)));
+  mx = max(max((uint32_t)__builtin_amdgcn_readlane((int)mx, 0), (uint32_t)__builtin_amdgcn_readlane((int)mx, 16)),
+           max((uint32_t)__builtin_amdgcn_readlane((int)mx, 32), (uint32_t)__builtin_amdgcn_readlane((int)mx, 48)));
+}
+
+// Histogram round of kth_bound: the values v with (v - base) >> sh_in == bin_in
+// (all when sh_in < 0) counted into 2048 bins of (v - base) >> sft; sets
+// sh.hsel to the bin holding the need-th largest of them and sh.need to the
+// count of those above it.
+template <int PER>
+__device__ __forceinline__ void bound_round(const uint32_t (&v)[PER], int cnt, uint32_t need, uint32_t base, int sft,
+                                            int sh_in, uint32_t bin_in, RangeShared &sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (tid + u * kFinThreads < cnt && v[u] >= base && (sh_in < 0 || ((v[u] - base) >> sh_in) == bin_in))
+      atomicAdd(&sh.hist[(v[u] - base) >> sft], 1u);
+  __syncthreads();
+  // running counts from the top bin down: thread t holds bins 2047 - 2t, 2046 - 2t
+  const uint32_t c0 = sh.hist[kBins - 1 - 2 * tid], c1 = sh.hist[kBins - 2 - 2 * tid], c = c0 + c1;
+  const uint32_t wi = wave_incl_scan_u32(c);
+  if (lane == kWave - 1) sh.wsum[wave] = wi;
+  __syncthreads();
+  uint32_t above = wi - c;
+  for (int w = 0; w < wave; ++w) above += sh.wsum[w];
+  if (above < need && above + c0 >= need) {
+    sh.hsel = (uint32_t)(kBins - 1 - 2 * tid);
+    sh.need = above;
+  }
+  if (above + c0 < need && above + c >= need) {
+    sh.hsel = (uint32_t)(kBins - 2 - 2 * tid);
+    sh.need = above + c0;
+  }
+  sh.hist[tid] = 0u;  // for the next round
+  sh.hist[tid + kFinThreads] = 0u;
+  __syncthreads();
+}
+
+// A lower bound of the need-th largest of the cnt values v (thread t holds
+// values t + 1024 u; need <= cnt): a 2048-bin histogram over [min, max], then
+// one over the bin that holds the need-th largest; the lower edge of the
+// second round's bin.  At least need values reach it, and it lies within
+// (max - min) / 2^22 of the need-th largest.
+template <int PER>
+__device__ __forceinline__ uint32_t kth_bound(const uint32_t (&v)[PER], int cnt, uint32_t need, RangeShared &sh) {
+  static_assert(kBins == 2 * kFinThreads, "two bins per thread");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
+  uint32_t mn = ~0u, mx = 0u;
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (tid + u * kFinThreads < cnt) {
+      mn = min(mn, v[u]);
+      mx = max(mx, v[u]);
+    }
+  wave_minmax_u32(mn, mx);
+  if (lane == 0) {
+    sh.wmin[wave] = mn;
+    sh.wmax[wave] = mx;
+  }
+  sh.hist[tid] = 0u;
+  sh.hist[tid + kFinThreads] = 0u;
+  __syncthreads();
+  uint32_t lo = ~0u, hi = 0u;
+  for (int w = 0; w < nw; ++w) {
+    lo = min(lo, (uint32_t)sh.wmin[w]);
+    hi = max(hi, (uint32_t)sh.wmax[w]);
+  }
+  const uint32_t R = hi - lo;
+  const int bl = R ? 32 - __clz((int)R) : 0;
+  const int sft = bl > 11 ? bl - 11 : 0;  // (v - lo) >> sft < 2048
+  bound_round<PER>(v, cnt, need, lo, sft, -1, 0u, sh);
+  const uint32_t b = sh.hsel, base = lo + (b << sft);
+  if (sft == 0) return base;  // one value per bin: base is the need-th largest
+  const int sft2 = sft > 11 ? sft - 11 : 0;
+  const uint32_t need2 = need - sh.need;
+  __syncthreads();  // every thread has read sh.hsel and sh.need
+  bound_round<PER>(v, cnt, need2, base, sft2, sft, 0u, sh);
+  return base + (sh.hsel << sft2);
+}
+
+// Exact top kk of short score rows whose 16-token group maxima the scan
+// wrote beside them (gmax [rows, ceil(n / 16)]: the largest masked key of each
+// group).  T, a lower bound of the kk-th largest group maximum, bounds the
+// row's kk-th largest key from below (kk groups each hold a key >= T), and
+// every key >= T lies in a group whose maximum is >= T: only those groups'
+// scores are read, and their keys >= T are the candidates (a little over kk
+// for spread scores).  Up to 2048 candidates are ranked by one sort; more are
+// selected first; rows whose candidates outgrow the LDS list (ties around T)
+// are selected from the whole row.
+__global__ __launch_bounds__(kFinThreads) void rowselect_gmax_kernel(const float *__restrict__ scores,
+                                                                     const uint32_t *__restrict__ gmax, int64_t n,
+                                                                     int64_t m, int64_t k, int64_t sink, int64_t local,
+                                                                     int64_t *__restrict__ idx) {
+  constexpr int kGroups = (int)(kRowSelectMax / kGroupTok);
+  constexpr int kPer = kGroups / kFinThreads;
+  __shared__ uint64_t cl[kCandLds];
+  __shared__ uint64_t ss[kMaxK];
+  __shared__ RangeShared sh;
+  __shared__ uint16_t glist[kGroups];
+  __shared__ uint32_t s_cnt;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
+  const int64_t row = blockIdx.x;
+  const float *rs = scores + row * n;
+  const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
+  const int64_t kk = k - sink - local;
+  const int ngrp = (int)cdiv(n, kGroupTok);
+  int64_t *out = idx + row * k;
+  uint32_t gm[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int g = tid + u * kFinThreads;
+    gm[u] = g < ngrp ? gmax[row * ngrp + g] : 0u;
+  }
+  const uint32_t T = ngrp > kk ? kth_bound<kPer>(gm, ngrp, (uint32_t)kk, sh) : 0u;
+  // the groups reaching T, listed in order
+  uint32_t ngr = 0u;
+  {
+    uint32_t c = 0u;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) c += (tid + u * kFinThreads < ngrp && gm[u] >= T) ? 1u : 0u;
+    const uint32_t wi = wave_incl_scan_u32(c);
+    if (lane == kWave - 1) sh.wsum[wave] = wi;
+    __syncthreads();
+    uint32_t off = wi - c;
+    for (int w = 0; w < nw; ++w) {
+      const uint32_t ws = sh.wsum[w];
+      off += w < wave ? ws : 0u;
+      ngr += ws;
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int g = tid + u * kFinThreads;
+      if (g < ngrp && gm[u] >= T) glist[off++] = (uint16_t)g;
+    }
+    __syncthreads();
+  }
+  // their keys >= T, one group per thread, placed by a workgroup prefix sum
+  uint32_t cnt = 0u;
+  for (uint32_t e0 = 0; e0 < ngr; e0 += kFinThreads) {  // uniform
+    const uint32_t e = e0 + tid;
+    const int64_t t0 = e < ngr ? (int64_t)glist[e] * kGroupTok : n;
+    float v[kGroupTok];
+    if (t0 + kGroupTok <= n && (n & 3) == 0) {
+#pragma unroll
+      for (int r = 0; r < kGroupTok; r += 4) {
+        const float4 f = *reinterpret_cast<const float4 *>(rs + t0 + r);
+        v[r] = f.x;
+        v[r + 1] = f.y;
+        v[r + 2] = f.z;
+        v[r + 3] = f.w;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kGroupTok; ++r) v[r] = t0 + r < n ? rs[t0 + r] : 0.0f;
+    }
+    uint32_t key[kGroupTok], c = 0u;
+#pragma unroll
+    for (int r = 0; r < kGroupTok; ++r) {
+      const int64_t i = t0 + r;
+      key[r] = (i < sink || i >= lstart) ? kKeyNegInf : score_key(v[r]);
+      c += (i < n && key[r] >= T) ? 1u : 0u;
+    }
+    const uint32_t wi = wave_incl_scan_u32(c);
+    if (lane == kWave - 1) sh.wsum[wave] = wi;
+    __syncthreads();
+    uint32_t off = cnt + wi - c;
+    for (int w = 0; w < nw; ++w) {
+      const uint32_t ws = sh.wsum[w];
+      off += w < wave ? ws : 0u;
+      cnt += ws;
+    }
+#pragma unroll
+    for (int r = 0; r < kGroupTok; ++r) {
+      const int64_t i = t0 + r;
+      if (i < n && key[r] >= T) {
+        if (off < (uint32_t)kCandLds) cl[off] = k64_of(key[r], i);
+        ++off;
+      }
+    }
+    __syncthreads();  // sh.wsum is rewritten by the next step
+  }
+  if (cnt > (uint32_t)kCandLds) {  // uniform: ties around T
+    const auto src = index_src([&](int64_t i) { return k64_of(masked_key(rs, i, sink, lstart), i); }, n);
+    select_sorted(src, n, kk, m, sink, local, out, cl, ss, sh, s_cnt, true);
+    return;
+  }
+  if (cnt > (uint32_t)(2 * kFinThreads)) {
+    select_sorted(ArraySrc{cl, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
+    return;
+  }
+  // at most 2048 candidates: one sort ranks them, the first kk are written
+  uint64_t v2[2];
+  v2[0] = (uint32_t)tid < cnt ? cl[tid] : 0ull;  // zero: padding (below every K64)
+  v2[1] = (uint32_t)(tid + kFinThreads) < cnt ? cl[tid + kFinThreads] : 0ull;
+  __syncthreads();  // cl is the sort scratch from here
+  int nlim = kWave;
+  while (nlim < (int)cnt) nlim <<= 1;
+  const int got = (int64_t)cnt < kk ? (int)cnt : (int)kk;
+  block_rank_desc<2>(v2, cl, cl + 2 * kFinThreads, nlim, [&](int rank, uint64_t x) {
+    if (rank < got) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x);
+  });
+  write_fixed(out, got, kk, m, sink, local);
+}
+
 __global__ __launch_bounds__(256) void fixed_only_kernel(int64_t rows, int64_t m, int64_t k, int64_t sink,
                                                          int64_t local, int64_t *__restrict__ idx) {
   const int64_t total = rows * k;
@@ -877,6 +1094,12 @@ int launch_rowselect(const float *scores, int64_t rows, int64_t n, int64_t m, in
                      int64_t *idx, hipStream_t st) {
   rowselect_kernel<<<(unsigned)rows, kFinThreads, 0, st>>>(scores, n, m, k, sink, local, idx);
   return launch_status("rowselect_kernel");
+}
+
+int launch_rowselect_gmax(const float *scores, const uint32_t *gmax, int64_t rows, int64_t n, int64_t m, int64_t k,
+                          int64_t sink, int64_t local, int64_t *idx, hipStream_t st) {
+  rowselect_gmax_kernel<<<(unsigned)rows, kFinThreads, 0, st>>>(scores, gmax, n, m, k, sink, local, idx);
+  return launch_status("rowselect_gmax_kernel");
 }
 
 int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st) {

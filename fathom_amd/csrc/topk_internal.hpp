@@ -42,6 +42,10 @@ constexpr int64_t kAlpha = 4;  // expected first-pass candidates per row, in uni
 // fused scan + top-k keeps the chain (its first pass writes no scores).
 constexpr int64_t kRowSelectMax = 32768;
 
+// Tokens per group of the group maxima that the fused scan's short-row pass
+// writes beside its scores (one lane's 16 tokens of a block).
+constexpr int64_t kGroupTok = 16;
+
 // Candidate counters of a row, one per 256 bytes: every workgroup of a pass
 // adds to its row's counter, and atomics to one cache line serialise.
 constexpr int64_t kCntStride = 64;
@@ -123,6 +127,10 @@ int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t lo
 // Exact top kk of whole score rows [rows, n] (n <= kRowSelectMax).
 int launch_rowselect(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
                      int64_t *idx, hipStream_t st);
+// The same from the rows' 16-token group maxima (gmax [rows, ceil(n / 16)]
+// largest masked keys): only the groups that can hold a top-kk key are read.
+int launch_rowselect_gmax(const float *scores, const uint32_t *gmax, int64_t rows, int64_t n, int64_t m, int64_t k,
+                          int64_t sink, int64_t local, int64_t *idx, hipStream_t st);
 // kk == 0: only the sink and local positions are written.
 int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st);
 // Shape checks shared by the top-k entry points (FATHOM_OK or an error status).

@@ -546,7 +546,8 @@ def test_config2_full_size_invariants():
 
 # ----------------------------------------------------------------------------- fused scan + top-k
 @pytest.mark.parametrize("cfg,n,BH,k,sub", [(1, 16384, None, 128, None), (2, 40000, 2, 512, None),
-                                            (4, 30000, 2, 2048, None), (2, 5000, 3, 300, 7), (2, 700, 1, 60, None)])
+                                            (4, 30000, 2, 2048, None), (2, 5000, 3, 300, 7), (2, 700, 1, 60, None),
+                                            (2, 4097, 2, 512, None), (3, 32768, 2, 512, None), (2, 30001, 1, 2048, None)])
 def test_scan_topk_fused_equals_unfused(cfg, n, BH, k, sub):
     print(f"[fused] cfg={cfg} n={n} BH={BH} k={k} sub={sub}", flush=True)
     x, st, plan = _scan_case(cfg, n, BH, sub)
@@ -727,12 +728,13 @@ def test_scan_topk_graph_replays():
         torch.testing.assert_close(eager, ref, rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("n", [70000, 16000])
+@pytest.mark.parametrize("n", [70000, 16000, 32768])
 def test_scan_topk_all_ties(n):
     """Every score equal (all-zero keys): every element reaches the threshold,
     so a row has n candidates -- more than one workgroup's LDS holds at n =
-    70000, when the selection reads the candidate regions in place.  Ties go
-    to the lowest index."""
+    70000, when the selection reads the candidate regions in place, and at
+    n = 32768, when the short-row selection from group maxima takes the whole
+    row.  Ties go to the lowest index."""
     print(f"[fused-ties] n={n}", flush=True)
     BH, d = 2, 128
     st = bp.PlaneStore(torch.zeros(BH, n, d, device=DEV))
@@ -745,10 +747,13 @@ def test_scan_topk_all_ties(n):
     np.testing.assert_array_equal(got.cpu().numpy(), expect)
 
 
-def test_scan_topk_adversarial_order():
+@pytest.mark.parametrize("n", [60000, 30000])
+def test_scan_topk_adversarial_order(n):
     """Scores rising along the sequence: the sampled threshold admits far more
-    candidates than usual; the result stays exact."""
-    BH, n, d = 1, 60000, 128
+    candidates than usual (n = 60000), and on a short row the top-kk keys lie
+    in the last groups, all of whose maxima reach T (n = 30000); the result
+    stays exact."""
+    BH, d = 1, 128
     K = torch.zeros(BH, n, d)
     K[0, :, 0] = torch.linspace(-1, 1, n) * 3.0
     K[0, :, 1] = torch.randn(n) * 0.01
