@@ -243,12 +243,12 @@ __device__ __forceinline__ float wave_max_f(float v) {
 }
 
 // LDS of an attention workgroup of NW waves (16 tokens per wave).
-template <int G, int NW = kAttnWaves>
+template <int G, int NW = kAttnWaves, int NC = 1>
 struct AttnShared {
   float q[G][kAttnD];            // the row's query heads
-  uint64_t kaddr[16 * NW];       // K and V row addresses of the workgroup's tokens (0: zero row)
-  uint64_t vaddr[16 * NW];
-  uint4 cnt[16 * NW];            // per-head selection counts (0 past the row's distinct tokens)
+  uint64_t kaddr[16 * NW * NC];  // K and V row addresses of the workgroup's tokens (0: zero row), NC groups
+  uint64_t vaddr[16 * NW * NC];
+  uint4 cnt[16 * NW * NC];       // per-head selection counts (0 past the row's distinct tokens)
   float wm[NW][G], wl[NW][G];
   float o[NW][G][kAttnD];        // the waves' weighted V sums
 };
@@ -297,20 +297,37 @@ typedef const __attribute__((address_space(1))) u32x4 *gptr4;
 // in sh.wm, sh.wl and sh.o (complete after the caller's next barrier).  Rows
 // without data (address 0) score 0 and add nothing to V; qa: any 256 readable
 // bytes, read in their place.
-template <int G, int NW = kAttnWaves>
-__device__ __forceinline__ void attn_tokens(AttnShared<G, NW> &sh, uint64_t qa, float scale) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rg = lane >> 4, ds = lane & 15;
+// The lane's K and V row pieces of one group of 16 NW tokens (the group at
+// token t0 of the address arrays), loads only.
+struct AttnRows {
   u32x4 kv[4], vv[4];
   bool has[4];
+};
+
+template <int G, int NW, int NC>
+__device__ __forceinline__ void attn_load(const AttnShared<G, NW, NC> &sh, int t0, uint64_t qa, AttnRows &r) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = lane >> 4, ds = lane & 15;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int t = 16 * wave + 4 * j + rg;
+    const int t = t0 + 16 * wave + 4 * j + rg;
     const uint64_t ka = sh.kaddr[t], va = sh.vaddr[t];
-    has[j] = ka != 0ull;
-    kv[j] = reinterpret_cast<gptr4>(ka ? ka : qa)[ds];
-    vv[j] = reinterpret_cast<gptr4>(va ? va : qa)[ds];
+    r.has[j] = ka != 0ull;
+    r.kv[j] = reinterpret_cast<gptr4>(ka ? ka : qa)[ds];
+    r.vv[j] = reinterpret_cast<gptr4>(va ? va : qa)[ds];
   }
+}
+
+template <int G, int NW = kAttnWaves>
+__device__ __forceinline__ void attn_tokens(AttnShared<G, NW> &sh, uint64_t qa, float scale);
+
+template <int G, int NW, int NC>
+__device__ __forceinline__ void attn_compute(AttnShared<G, NW, NC> &sh, int t0, const AttnRows &r, float scale) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = lane >> 4, ds = lane & 15;
+  const u32x4(&kv)[4] = r.kv;
+  const u32x4(&vv)[4] = r.vv;
+  const bool(&has)[4] = r.has;
   // ---- scores
   float s[4][G];
 #pragma unroll
@@ -333,7 +350,7 @@ __device__ __forceinline__ void attn_tokens(AttnShared<G, NW> &sh, uint64_t qa, 
   float c[4][G];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint4 cn = sh.cnt[16 * wave + 4 * j + rg];
+    const uint4 cn = sh.cnt[t0 + 16 * wave + 4 * j + rg];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       c[j][g] = (float)head_count(cn, g);
@@ -387,6 +404,13 @@ __device__ __forceinline__ void attn_tokens(AttnShared<G, NW> &sh, uint64_t qa, 
     const float lw = across_rows<false>(l[g]);
     if (lane == 0) sh.wl[wave][g] = lw;
   }
+}
+
+template <int G, int NW>
+__device__ __forceinline__ void attn_tokens(AttnShared<G, NW> &sh, uint64_t qa, float scale) {
+  AttnRows r;
+  attn_load(sh, 0, qa, r);
+  attn_compute(sh, 0, r, scale);
 }
 
 // Partial attention of one workgroup's kAttnTok distinct tokens of the union
@@ -447,15 +471,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(const float 
 // g's k selected positions 16 kHeadWaves at a time, each with a count of one
 // (a row selected twice counts twice), folds every group into a running (M,
 // sum, weighted V) with the usual rescaling, and writes out[bh, g] itself --
-// one launch, no partial triples.
+// one launch, no partial triples.  Positions are placed kHeadGroups groups at
+// a time, and all of their K/V rows are requested before the first group is
+// computed, so the groups' load latencies overlap.
 constexpr int kHeadWaves = 16;
 constexpr int kHeadTok = 16 * kHeadWaves;
+constexpr int kHeadGroups = 2;
 
 __global__ __launch_bounds__(kHeadWaves * kWave) void attn_head_kernel(const float *__restrict__ q,
                                                                        const int64_t *__restrict__ idx, int64_t G,
                                                                        int64_t k, RowSrc rs, float scale,
                                                                        float *__restrict__ out) {
-  __shared__ AttnShared<1, kHeadWaves> sh;
+  __shared__ AttnShared<1, kHeadWaves, kHeadGroups> sh;
   __shared__ float runO[kAttnD];
   __shared__ float runM, runL;
   const int tid = threadIdx.x;
@@ -470,8 +497,9 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attn_head_kernel(const flo
     runM = -INFINITY;
     runL = 0.0f;
   }
-  for (int64_t c0 = 0; c0 < k; c0 += kHeadTok) {
-    if (tid < kHeadTok) {
+  static_assert(kHeadGroups * kHeadTok <= kHeadWaves * kWave, "a thread per position placed");
+  for (int64_t c0 = 0; c0 < k; c0 += kHeadGroups * kHeadTok) {
+    if (tid < kHeadGroups * kHeadTok) {
       const int64_t j = c0 + tid;
       uint4 cn = make_uint4(0u, 0u, 0u, 0u);
       uint64_t ka = 0ull, va = 0ull;
@@ -489,29 +517,38 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attn_head_kernel(const flo
       sh.cnt[tid] = cn;
     }
     __syncthreads();
-    attn_tokens<1, kHeadWaves>(sh, reinterpret_cast<uint64_t>(qg), scale);
-    __syncthreads();
-    // fold the group into the running triple (every thread reads runM first)
-    float mc = -INFINITY;
+    const int ng = (int)min((int64_t)kHeadGroups, cdiv(k - c0, (int64_t)kHeadTok));  // uniform
+    AttnRows r[kHeadGroups];
 #pragma unroll
-    for (int v = 0; v < kHeadWaves; ++v) mc = fmaxf(mc, sh.wm[v][0]);
-    const float Mo = runM, Mn = fmaxf(Mo, mc);
-    const float eo = Mo == -INFINITY ? 0.0f : expf(Mo - Mn), ec = mc == -INFINITY ? 0.0f : expf(mc - Mn);
-    if (tid < kAttnD) {
-      float oc = 0.0f;
+    for (int gi = 0; gi < kHeadGroups; ++gi)
+      if (gi < ng) attn_load(sh, gi * kHeadTok, reinterpret_cast<uint64_t>(qg), r[gi]);
 #pragma unroll
-      for (int v = 0; v < kHeadWaves; ++v) oc += sh.o[v][0][tid];
-      runO[tid] = runO[tid] * eo + oc * ec;
+    for (int gi = 0; gi < kHeadGroups; ++gi) {
+      if (gi >= ng) break;
+      attn_compute(sh, gi * kHeadTok, r[gi], scale);
+      __syncthreads();
+      // fold the group into the running triple (every thread reads runM first)
+      float mc = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < kHeadWaves; ++v) mc = fmaxf(mc, sh.wm[v][0]);
+      const float Mo = runM, Mn = fmaxf(Mo, mc);
+      const float eo = Mo == -INFINITY ? 0.0f : expf(Mo - Mn), ec = mc == -INFINITY ? 0.0f : expf(mc - Mn);
+      if (tid < kAttnD) {
+        float oc = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kHeadWaves; ++v) oc += sh.o[v][0][tid];
+        runO[tid] = runO[tid] * eo + oc * ec;
+      }
+      __syncthreads();  // every thread has read runM
+      if (tid == 0) {
+        float lc = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kHeadWaves; ++v) lc += sh.wl[v][0];
+        runL = runL * eo + lc * ec;
+        runM = Mn;
+      }
+      __syncthreads();  // sh is rewritten by the next group
     }
-    __syncthreads();  // every thread has read runM
-    if (tid == 0) {
-      float lc = 0.0f;
-#pragma unroll
-      for (int v = 0; v < kHeadWaves; ++v) lc += sh.wl[v][0];
-      runL = runL * eo + lc * ec;
-      runM = Mn;
-    }
-    __syncthreads();  // sh is rewritten by the next group
   }
   if (tid < kAttnD) out[(bh * G + g) * kAttnD + tid] = runO[tid] / runL;
 }
