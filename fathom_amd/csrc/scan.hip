@@ -42,10 +42,12 @@
 // wave-tile: the listed channels' scales of the 16 blocks are loaded into the
 // wave's LDS (the four lanes of a block split the channels and reduce the
 // block's largest scale and the constant C for every head with quad DPP
-// sums), rescaled by 2^-s_b; then the plane dwords are loaded 16 units at a
-// time (the next 16 in flight while the current ones are computed), one
-// dword per lane and unit: 64 lanes read the unit's 16 blocks as one 128-byte
-// run of a superblock store.
+// sums), rescaled by 2^-s_b; then the plane dwords are loaded 8 units at a
+// time (the next 8 in flight while the current ones are computed), one dword
+// per lane and unit: 64 lanes read the unit's 16 blocks as one 128-byte run
+// of a superblock store.  Stores in mapped host memory with superblocks of a
+// multiple of 32 blocks are read two adjacent wave-tiles per instruction (256
+// contiguous bytes, scan_tile_pair).
 #include "topk_internal.hpp"
 #include "scan_internal.hpp"
 
