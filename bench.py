@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode step")
     ap.add_argument("--stages-only", action="store_true", help="scan + top-k only (for profiling runs)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only config 5's 36-layer decode step (for rocprofv3 kernel traces of its stages)")
     ap.add_argument("--host-scan-only", action="store_true",
                     help="only the fused scan + top-k over the host-mapped store, --steps calls after --warmup "
                          "(for rocprofv3 --pmc runs of the zero-copy scan); raises if its indices differ from "
@@ -580,6 +582,10 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if a.decode_only:
+        decode = run_decode_step(torch, bp, off, W, dev, max(3, a.steps // 2), 2)
+        log(f"[bench] decode step (config 5): {json.dumps(decode)}")
+        return
     t0 = time.perf_counter()
     x = W.config_inputs(a.config, device=dev, n=a.n)
     V = W.synth_values(x["BH"], x["n"], device=dev)
