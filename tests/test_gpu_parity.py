@@ -246,10 +246,12 @@ def _topk_case(rows, k, sink, local, m=None):
 @pytest.mark.parametrize("n,k,sink,local", [(1000, 128, 4, 64), (16384, 128, 4, 64), (131072, 512, 4, 32),
                                             (100000, 2048, 4, 32), (3000, 2048, 4, 32), (600, 40, 0, 0),
                                             (32768, 512, 4, 32), (32769, 512, 4, 32), (32768, 2048, 0, 0),
-                                            (65536, 1024, 0, 0)])
+                                            (65536, 1024, 0, 0), (600000, 40, 4, 32), (1000000, 64, 4, 32)])
 def test_topk_random_bitexact(n, k, sink, local):
     """Rows up to 32768 take the one-kernel row selection, longer rows the
-    sample / select / filter / finalize chain; both must equal the oracle."""
+    sample / select / filter / finalize chain; both must equal the oracle.
+    Small k on long rows (kk = 4 of 600000, 28 of 10^6) needs the sample's
+    tile stride rounded up, or the sample would outgrow its 65536 keys."""
     print(f"[topk] n={n} k={k}", flush=True)
     rng = np.random.default_rng(n + k)
     rows = rng.standard_normal((2, 3, n)).astype(np.float32)
@@ -556,9 +558,21 @@ def test_scan_topk_fused_equals_unfused(cfg, n, BH, k, sub):
     ref = bp.sink_local_topk(st.scan(q, plan), k, sink, local)
     got = st.scan_topk(q, plan, k, sink, local)
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
-    m = n + 3
+    m = n + 3  # the local window partly past the scanned row
     ref = bp.sink_local_topk(st.scan(q, plan), k, sink, local, m=m)
     got = st.scan_topk(q, plan, k, sink, local, m=m)
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("n,k", [(600000, 40), (1000000, 64)])
+def test_scan_topk_fused_small_k_long_rows(n, k):
+    """The fused call with kk = k - 36 small against n (4 of 600000, 28 of
+    10^6): the sample stride rounds up, the call equals scan + top-k."""
+    print(f"[fused-small-k] n={n} k={k}", flush=True)
+    x, st, plan = _scan_case(2, n, 1)
+    q = x["q"].to(DEV)
+    ref = bp.sink_local_topk(st.scan(q, plan), k, 4, 32)
+    got = st.scan_topk(q, plan, k, 4, 32)
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
 
 
@@ -580,7 +594,7 @@ def test_scan_topk_fused_host_resident():
 
 @pytest.mark.parametrize("cfg,n,sub,G", [(2, 50000, 32, None), (2, 65536, 64, None), (3, 33000, 32, None),
                                          (3, 100000, 64, None), (2, 40000, "whole", None), (1, 50000, 32, None),
-                                         (2, 50000, 32, 8)])
+                                         (2, 50000, 32, 8), (2, 20000, 64, None), (3, 4097, 32, None)])
 def test_scan_host_resident_paired_tiles(cfg, n, sub, G):
     """Host-mapped stores with superblocks of a multiple of 32 blocks take the
     paired-tile first pass (256-byte reads; G <= 4 only): scores and the fused
