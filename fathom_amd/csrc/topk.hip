@@ -229,6 +229,7 @@ __device__ __forceinline__ IndexSrc<Get> index_src(Get get, int64_t cnt) {
 // batch's counts load while the current one is read); lane e of a step reads
 // the batch's e-th value, found by a binary search over the lanes' exclusive
 // prefix sums of the counts.
+static_assert(kRegTok < (1 << 11), "region counts fit the 11-bit wave sums of RegionSrc");
 struct RegionSrc {
   const uint32_t *rc;
   const uint64_t *cand;
@@ -242,8 +243,8 @@ struct RegionSrc {
     while (r0 < nreg) {  // uniform per wave
       const int64_t r1 = r0 + step;
       const uint32_t cn = r1 + lane < nreg ? min(rc[r1 + lane], (uint32_t)kRegTok) : 0u;
-      const uint32_t pre = (uint32_t)wave_excl_scan_small<10>((int)c, lane);  // counts <= 512
-      const uint32_t tot = (uint32_t)wave_sum_small<10>((int)c);
+      const uint32_t pre = (uint32_t)wave_excl_scan_small<11>((int)c, lane);  // counts <= kRegTok = 1024
+      const uint32_t tot = (uint32_t)wave_sum_small<11>((int)c);
       for (uint32_t e0 = 0; e0 < tot; e0 += kWave) {
         const uint32_t e = e0 + lane;
         int j = 0;  // the last lane whose prefix is <= e: its region holds value e
@@ -391,7 +392,10 @@ __device__ __forceinline__ uint64_t range_select(const Src &src, int64_t cnt, ui
     sh.thr = a;
   }
   __syncthreads();
-  for (;;) {
+  // each round narrows the range of distinct 64-bit values by at least 11
+  // bits, so six rounds end it; the bound keeps a source that yields fewer
+  // values than cnt from looping
+  for (int round = 0; round < 8; ++round) {
     const uint64_t lo = sh.lo, hi = sh.hi;
     const uint32_t nd = sh.need;
     const uint64_t R = hi - lo;

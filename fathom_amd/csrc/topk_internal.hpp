@@ -65,14 +65,15 @@ struct TopkSel {
   __host__ __device__ uint32_t *cnt2(int64_t row) const { return cand2_cnt + row * kCntStride; }
 };
 
-// Sample stride in tiles of `tile` tokens: about 16384 sampled tokens per row,
-// more where the sample must hold 2 kk keys or where about 16 sampled keys
-// must reach the first-pass threshold (kAlpha * kk * sample / n >= 16), at
-// most kMaxSample keys.  The stride rounds up, so the sample never exceeds
-// that many tiles.
+// Sample stride in tiles of `tile` tokens: about 16384 sampled tokens per row
+// (8192 for the fused scan's wave-tiles: a launch of half the workgroups for
+// its latency-bound sample pass), more where the sample must hold 2 kk keys
+// or where about 16 sampled keys must reach the first-pass threshold (kAlpha *
+// kk * sample / n >= 16), at most kMaxSample keys.  The stride rounds up, so
+// the sample never exceeds that many tiles.
 inline int64_t topk_tile_stride(int64_t n, int64_t kk, int64_t tile) {
   const int64_t ntiles = cdiv(n, tile);
-  int64_t want = cdiv(8 * kTileTok, tile);
+  int64_t want = tile == kRegTok ? 8 : cdiv(8 * kTileTok, tile);
   if (kk > 0) {
     const int64_t a = cdiv(2 * kk, tile), b = cdiv(16 * n, kAlpha * kk * tile);
     want = a > want ? a : want;
