@@ -63,9 +63,8 @@ constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxD = 128;             // the reference's head dimension (kernels/bitplane.py:313)
 constexpr int kMaxUnits = 4 * kMaxD;   // (channel, plane) units of a plan
 constexpr int kChunk = 8;              // units per load chunk
-constexpr int kChunkSample = 32;       // units per load chunk of the sample pass
 static_assert(kWTok == kRegTok, "a candidate region is one wave-tile");
-static_assert(kMaxUnits % kChunkSample == 0 && kChunkSample % kChunk == 0, "unit tables pad to whole chunks");
+static_assert(kMaxUnits % kChunk == 0, "unit tables pad to whole chunks");
 
 typedef __fp16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -228,7 +227,7 @@ __device__ __forceinline__ int plan_tables(Shared<NQ> &sh, const ScanArgs &a, in
     for (int p = 0; p <= c; ++p) sh.desc[ub + p] = (uint32_t)(j * 4 + p) | ((uint32_t)e << 16);
   }
   // zero-weight padding units (plane word 0) up to a whole chunk of every pass
-  const int upad = (u + kChunkSample - 1) / kChunkSample * kChunkSample;
+  const int upad = (u + kChunk - 1) / kChunk * kChunk;
   for (int v = u + tid; v < upad; v += kThreads) {
     sh.desc[v] = 0u;
 #pragma unroll
@@ -310,8 +309,9 @@ __device__ __forceinline__ float residual(h2 h, float w) {
 }
 
 // One chunk of units: per group of four units the weights (f16 hi/lo) and the
-// token steps of B and the MFMAs.
-template <int NQ, int RS, int CH>
+// token steps of B and the MFMAs.  FIRST: the tile's first chunk, whose first
+// MFMA of every accumulator adds to zero (no separate clearing).
+template <int NQ, int RS, int CH, bool FIRST = false>
 __device__ __forceinline__ void compute_chunk(Tile<NQ, RS> &t, const uint32_t (&d)[CH], const ChunkDesc<CH> &cd,
                                               const Shared<NQ> &sh, const uint16_t *awb, int u0, int i, uint32_t sel) {
 #pragma unroll
@@ -353,8 +353,9 @@ __device__ __forceinline__ void compute_chunk(Tile<NQ, RS> &t, const uint32_t (&
           }
 #pragma unroll
           for (int hq = 0; hq < NQ; ++hq) {
-            t.acc[hq][r] = __builtin_amdgcn_mfma_f32_4x4x4f16(Ah[hq], B0, t.acc[hq][r], 0, 0, 0);
-            t.acc[hq][r + 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(Ah[hq], B1, t.acc[hq][r + 1], 0, 0, 0);
+            t.acc[hq][r] = __builtin_amdgcn_mfma_f32_4x4x4f16(Ah[hq], B0, FIRST && g == 0 ? f4{} : t.acc[hq][r], 0, 0, 0);
+            t.acc[hq][r + 1] =
+                __builtin_amdgcn_mfma_f32_4x4x4f16(Ah[hq], B1, FIRST && g == 0 ? f4{} : t.acc[hq][r + 1], 0, 0, 0);
           }
 #pragma unroll
           for (int hq = 0; hq < NQ; ++hq) {
@@ -375,7 +376,8 @@ __device__ __forceinline__ void compute_chunk(Tile<NQ, RS> &t, const uint32_t (&
         h4 B;
         __builtin_memcpy(&B, bb, sizeof(B));
 #pragma unroll
-        for (int hq = 0; hq < NQ; ++hq) t.acc[hq][k] = __builtin_amdgcn_mfma_f32_4x4x4f16(Ah[hq], B, t.acc[hq][k], 0, 0, 0);
+        for (int hq = 0; hq < NQ; ++hq)
+          t.acc[hq][k] = __builtin_amdgcn_mfma_f32_4x4x4f16(Ah[hq], B, FIRST && g == 0 ? f4{} : t.acc[hq][k], 0, 0, 0);
 #pragma unroll
         for (int hq = 0; hq < NQ; ++hq) t.acc[hq][k] = __builtin_amdgcn_mfma_f32_4x4x4f16(Al[hq], B, t.acc[hq][k], 0, 0, 0);
       }
@@ -480,14 +482,26 @@ __device__ __forceinline__ void scan_tile(Tile<NQ, RS> &t, const ScanArgs &a, co
     read_descs(cur, sh.desc, 0);
     load_chunk(d, cur, ta, sub8);
   }
-#pragma unroll
-  for (int hq = 0; hq < NQ; ++hq)
-#pragma unroll
-    for (int k = 0; k < Tile<NQ, RS>::NR; ++k) t.acc[hq][k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   scale_pass<NQ, RS>(t, sh, aw, ta.sr, ta.soff, sub2, nact, lane);
   const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;  // the lane's 16-bit half of each dword
   const uint16_t *awb = &aw[0][b];
-  for (int ck = 0; ck < nck; ++ck) {
+  if (nck == 0) {
+#pragma unroll
+    for (int hq = 0; hq < NQ; ++hq)
+#pragma unroll
+      for (int k = 0; k < Tile<NQ, RS>::NR; ++k) t.acc[hq][k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    return;
+  }
+  // chunk 0 starts the accumulators
+  if (nck > 1) {
+    read_descs(nxt, sh.desc, CH);
+    load_chunk(dn, nxt, ta, sub8);
+  }
+  compute_chunk<NQ, RS, CH, true>(t, d, cur, sh, awb, 0, i, sel);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) d[k] = dn[k];
+  cur = nxt;
+  for (int ck = 1; ck < nck; ++ck) {
     if (ck + 1 < nck) {
       read_descs(nxt, sh.desc, (ck + 1) * CH);
       load_chunk(dn, nxt, ta, sub8);
@@ -668,13 +682,16 @@ __device__ __forceinline__ void emit_sample(const Emit &em, const Tile<NQ, RS> &
 // that ulp and the rounding of thr - C, so no passing token fails the
 // prefilter (NaN passes both).  Only steps where some lane passes it compute
 // scores and keys.
-// f = 2^fe exactly, so dividing by it is an exact ldexp (when f is a normal
-// power of two; otherwise every token takes the exact path).
-__device__ __forceinline__ float acc_threshold(float thr, float C, float f, int fe) {
-  if (!(f > 0.0f) || !(f < INFINITY) || !(fabsf(C) < INFINITY) || fe < -126 || fe > 127)
-    return __int_as_float(0x7FC00000);  // NaN: all pass
+// f_w = 2^fe_w exactly, fe_w = fe0 - e_w, so dividing by it is an exact ldexp
+// of the one numerator X = (thr - C) - margin when every f_w is a normal power
+// of two (e_w spans [-13, 1]); otherwise T is NaN and every token of the tile
+// takes the exact path.
+__device__ __forceinline__ void acc_thresholds(float (&T)[4], float thr, float C, int fe0) {
   const float margin = (fabsf(thr) + fabsf(C)) * 0x1p-20f + 0x1p-126f;
-  return ldexpf((thr - C) - margin, -fe);
+  const bool ok = fabsf(C) < INFINITY && fe0 - bit_exp(3) >= -126 && fe0 - bit_exp(0) <= 127;
+  const float X = ok ? (thr - C) - margin : __int_as_float(0x7FC00000);  // NaN: all pass
+#pragma unroll
+  for (int w = 0; w < 4; ++w) T[w] = ldexpf(X, bit_exp(w) - fe0);
 }
 
 template <int NQ>
@@ -696,18 +713,22 @@ __device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t
     if ((skipm >> h) & 1u) continue;
     const int64_t row = bh * a.G + h;
     const float thr_f = threshold_value(ld_uniform(thr + row));
-    float f[4], T[4];
-    head_factors(f, t, sh, h);
+    const int fe0 = sh.sig[h] + t.sx;
+    float T[4];
+    if (plain) {
+      acc_thresholds(T, thr_f, t.cst[h], fe0);
+    } else {
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
-      T[w] = plain ? acc_threshold(thr_f, t.cst[h], f[w], sh.sig[h] + t.sx - bit_exp(w)) : __int_as_float(0x7FC00000);
+      for (int w = 0; w < 4; ++w) T[w] = __int_as_float(0x7FC00000);
+    }
     uint64_t *dst = em.sel.cand + row * em.sel.cand_cap + t0;
     uint32_t off = 0u;
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
       if (__ballot(!(t.acc[h >> 2][r][h & 3] < T[r & 3])) == 0ull) continue;  // uniform
       const int64_t tok = tok0 + r;
-      const float v = tile_score<NQ, 1>(t, f, r, h);
+      // the score as tile_score forms it: acc * 2^(sigma + s_b - e_r) + C
+      const float v = fmaf(t.acc[h >> 2][r][h & 3], ldexpf(1.0f, fe0 - bit_exp(r)), t.cst[h]);
       bool valid = true;
       float vm = v;
       if (!plain) {
@@ -725,17 +746,42 @@ __device__ __forceinline__ void emit_filter(const Emit &em, const Tile<NQ, 1> &t
   }
 }
 
+// The tile loop of the one-tile modes: list entries L0, L0 + Ls, ... < nlist.
+// FB: the candidate pass's fallback rescan (T_lo, second count array; heads in
+// skipm emit nothing).
+template <int NQ, int MODE, bool FB>
+__device__ __forceinline__ void tile_pass(Tile<NQ, 1> &t, const ScanArgs &a, const Emit &em, const Shared<NQ> &sh,
+                                          uint16_t (*aw)[kWB], int64_t bh, int U, int nact, int lane, int64_t L0,
+                                          int64_t Ls, int64_t nlist, uint32_t skipm, uint32_t (&tot)[4 * NQ]) {
+  constexpr bool kCand = MODE == kEmitFilter;
+  uint32_t *rcp = FB ? em.sel.rc2 : em.sel.rc1;
+  for (int64_t L = L0; L < nlist; L += Ls) {
+    if (kCand && L >= a.nwt) {
+      if (lane < a.G && !((skipm >> lane) & 1u)) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
+      continue;
+    }
+    const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
+    if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
+    set_priority_by_tiles_left((nlist - 1 - L) / Ls);
+    scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
+    if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax)
+      emit_scores<NQ, MODE == kEmitScoresMax>(em, t, sh, a, bh, beta0, lane);
+    if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, FB, skipm, tot);
+    wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
+  }
+}
+
 // --------------------------------------------------------------------- kernel
 // Grid (workgroups, BH); the waves of the grid's row take the list entries L
 // in a grid-stride loop.  The candidate pass ends with the fallback check.
-// Every cross-workgroup value goes through returning atomics, which resolve
-// at one coherence point (no fence, no cache writeback): a workgroup adds its
-// per-head candidate totals to the row's counters, waits for them, then counts
-// itself done on the row's completion counter; the workgroup that counts last
-// reads the totals back and, for heads with fewer than kk candidates (a sample
-// that misled T_hi), rescans the row with T_lo into the regions under the
-// second count array -- slowly, with its four waves alone, but only for such
-// rows.  Nothing waits on another workgroup.
+// The only cross-workgroup values are per-head 64-bit counters, each updated
+// by one returning atomic per workgroup that carries both the workgroup's
+// candidate count and its completion (a single coherence point: no fence, no
+// cache writeback).  The workgroup that completes a head's count holds the
+// head's total; for a head with fewer than kk candidates (a sample that misled
+// T_hi) it rescans the row with T_lo into the regions under the second count
+// array -- slowly, with its four waves alone, but only for such heads.
+// Nothing waits on another workgroup.
 // PAIR (stores in mapped host memory, sub a multiple of 32): the first pass
 // scans pairs of adjacent wave-tiles with 256-byte loads (scan_tile_pair).
 template <int NQ, int MODE, bool PAIR = false>
@@ -743,8 +789,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
     NQ == 1 && MODE != kEmitSample && MODE != kEmitScoresMax && !PAIR ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
   __shared__ Shared<NQ> sh;
   __shared__ uint16_t awB[PAIR ? kWaves : 1][kMaxD][kWB];  // tile B's scale buffers
-  __shared__ uint32_t s_tot[8], s_wt[kWaves][8];
-  __shared__ uint32_t s_last;
+  __shared__ uint32_t s_wt[kWaves][8], s_need[8];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
@@ -753,14 +798,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
   uint16_t(*aw)[kWB] = sh.a[wave];
   if constexpr (MODE == kEmitSample) {
     // the sample pass is latency-bound (a few tiles per row): the four waves
-    // of a workgroup share each tile, one token-step class each, with larger
-    // load chunks
+    // of a workgroup share each tile, one token-step class each
     Tile<NQ, 4> t;
     t.r0 = wave;
     for (int64_t L = blockIdx.x; L < a.nwt; L += gridDim.x) {
       const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
       if (beta0 >= a.blk_end) continue;  // uniform per workgroup
-      scan_tile<NQ, 4, kChunkSample>(t, a, sh, aw, bh, beta0, U, nact, lane);
+      scan_tile<NQ, 4, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
       emit_sample(em, t, sh, a, bh, beta0, L, lane);
       wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
     }
@@ -770,85 +814,68 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
     // the candidate pass also writes the (zero) counts of the padding regions past the row
     constexpr bool kCand = MODE == kEmitFilter;
     const int64_t nlist = kCand && em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
-    int64_t L0 = (int64_t)blockIdx.x * kWaves + wave, Ls = (int64_t)gridDim.x * kWaves;
-    uint32_t skipm = 0u;
-    bool fb = false;
+    const int64_t L0 = (int64_t)blockIdx.x * kWaves + wave, Ls = (int64_t)gridDim.x * kWaves;
     uint32_t tot[4 * NQ];
 #pragma unroll
     for (int h = 0; h < 4 * NQ; ++h) tot[h] = 0u;
-#pragma nounroll
-    for (int pass = 0; pass < (kCand ? 2 : 1); ++pass) {
-      if (pass == 1) {  // the fallback check (candidate pass only)
-        if (!em.fallback_check) return;  // uniform
-        if (lane == 0)
-#pragma unroll
-          for (int h = 0; h < 4 * NQ; ++h) s_wt[wave][h] = tot[h];
-        __syncthreads();
-        if (tid < a.G) {
-          const uint32_t add = s_wt[0][tid] + s_wt[1][tid] + s_wt[2][tid] + s_wt[3][tid];
-          const uint32_t was = atomicAdd(em.sel.cnt1(bh * a.G + tid), add);
-          asm volatile("" ::"v"(was));  // completed before the barrier, so before the done count
-        }
-        __syncthreads();
-        if (tid == 0) s_last = atomicAdd(em.sel.cnt2(bh * a.G), 1u) == gridDim.x - 1 ? 1u : 0u;
-        __syncthreads();
-        if (!s_last) return;  // uniform
-        // every other workgroup of the row has added its totals and counted
-        // itself done: take the totals and leave both counters at zero, so a
-        // candidate pass run again on its own (the stage entry point) starts
-        // from the state the selection kernel leaves
-        if (tid < a.G) s_tot[tid] = atomicExch(em.sel.cnt1(bh * a.G + tid), 0u);
-        if (tid == 0) atomicExch(em.sel.cnt2(bh * a.G), 0u);
-        __syncthreads();
-        for (int g = 0; g < a.G; ++g) skipm |= (s_tot[g] >= em.sel.kk ? 1u : 0u) << g;
-        if (skipm == (1u << a.G) - 1u) return;  // uniform: the common case
-        fb = true;
-        L0 = wave;
-        Ls = kWaves;
-      }
-      uint32_t *rcp = fb ? em.sel.rc2 : em.sel.rc1;
-      if constexpr (PAIR) {
-        if (!fb) {
-          // pairs of tiles (2 P, 2 P + 1); then the padding regions' zero counts
-          const int64_t npair = (a.nwt + 1) / 2;
-          for (int64_t P = L0; P < npair; P += Ls) {
-            const int64_t LA = 2 * P, LB = LA + 1;
-            const int64_t beta0 = (a.wt0 + LA) * kWB;
-            if (beta0 >= a.blk_end || beta0 + 2 * kWB <= a.blk0) continue;  // uniform per wave
-            set_priority_by_tiles_left((npair - 1 - P) / Ls);
-            Tile<NQ, 1> tB;
-            tB.r0 = 0;
-            scan_tile_pair<NQ, kChunk>(t, tB, a, sh, aw, awB[wave], bh, beta0, U, nact, lane);
-            if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax) {
-              emit_scores<NQ, MODE == kEmitScoresMax>(em, t, sh, a, bh, beta0, lane);
-              if (LB < a.nwt) emit_scores<NQ, MODE == kEmitScoresMax>(em, tB, sh, a, bh, beta0 + kWB, lane);
-            }
-            if constexpr (MODE == kEmitFilter) {
-              emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, fb, skipm, tot);
-              if (LB < a.nwt) emit_filter<NQ>(em, tB, sh, a, bh, beta0 + kWB, lane, fb, skipm, tot);
-            }
-            wave_lds_sync();  // the wave's scale buffers are rewritten by its next pair
-          }
-          if constexpr (kCand)
-            for (int64_t L = a.nwt + L0; L < nlist; L += Ls)
-              if (lane < a.G) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
-          continue;
-        }
-      }
-      for (int64_t L = L0; L < nlist; L += Ls) {
-        if (kCand && L >= a.nwt) {
-          if (lane < a.G && !((skipm >> lane) & 1u)) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
-          continue;
-        }
-        const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
-        if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
-        set_priority_by_tiles_left((nlist - 1 - L) / Ls);
-        scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
-        if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax)
+    if constexpr (PAIR) {
+      // pairs of tiles (2 P, 2 P + 1); then the padding regions' zero counts
+      const int64_t npair = (a.nwt + 1) / 2;
+      for (int64_t P = L0; P < npair; P += Ls) {
+        const int64_t LA = 2 * P, LB = LA + 1;
+        const int64_t beta0 = (a.wt0 + LA) * kWB;
+        if (beta0 >= a.blk_end || beta0 + 2 * kWB <= a.blk0) continue;  // uniform per wave
+        set_priority_by_tiles_left((npair - 1 - P) / Ls);
+        Tile<NQ, 1> tB;
+        tB.r0 = 0;
+        scan_tile_pair<NQ, kChunk>(t, tB, a, sh, aw, awB[wave], bh, beta0, U, nact, lane);
+        if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax) {
           emit_scores<NQ, MODE == kEmitScoresMax>(em, t, sh, a, bh, beta0, lane);
-        if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, fb, skipm, tot);
-        wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
+          if (LB < a.nwt) emit_scores<NQ, MODE == kEmitScoresMax>(em, tB, sh, a, bh, beta0 + kWB, lane);
+        }
+        if constexpr (MODE == kEmitFilter) {
+          emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, false, 0u, tot);
+          if (LB < a.nwt) emit_filter<NQ>(em, tB, sh, a, bh, beta0 + kWB, lane, false, 0u, tot);
+        }
+        wave_lds_sync();  // the wave's scale buffers are rewritten by its next pair
       }
+      if constexpr (kCand)
+        for (int64_t L = a.nwt + L0; L < nlist; L += Ls)
+          if (lane < a.G) em.sel.rc1[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
+    } else {
+      tile_pass<NQ, MODE, false>(t, a, em, sh, aw, bh, U, nact, lane, L0, Ls, nlist, 0u, tot);
+    }
+    if constexpr (kCand) {
+      // the fallback check: one 64-bit atomic per head and workgroup, (1 << 32)
+      // | the workgroup's candidates of the head.  The workgroup whose add
+      // completes the done count holds the head's final total: it leaves the
+      // counter at zero (the state the selection kernel leaves, so a candidate
+      // pass run again on its own starts from it) and, if the head has fewer
+      // than kk candidates, rescans the row for that head with T_lo.  The
+      // rescan is a second instance of the tile loop, so the first pass's
+      // registers are allocated for the first pass alone.
+      if (!em.fallback_check) return;  // uniform
+      if (lane == 0)
+#pragma unroll
+        for (int h = 0; h < 4 * NQ; ++h) s_wt[wave][h] = tot[h];
+      __syncthreads();
+      if (tid < a.G) {
+        const uint32_t add = s_wt[0][tid] + s_wt[1][tid] + s_wt[2][tid] + s_wt[3][tid];
+        uint64_t *ctr = reinterpret_cast<uint64_t *>(em.sel.cnt1(bh * a.G + tid));
+        const uint64_t was = atomicAdd(ctr, (1ull << 32) | (uint64_t)add);
+        bool need = false;
+        if ((uint32_t)(was >> 32) == gridDim.x - 1u) {
+          need = (uint32_t)was + add < em.sel.kk;
+          atomicExch(ctr, 0ull);
+        }
+        s_need[tid] = need ? 1u : 0u;
+      }
+      __syncthreads();
+      uint32_t nm = 0u;
+      for (int g = 0; g < a.G; ++g) nm |= s_need[g] << g;
+      if (nm == 0u) return;  // uniform: the common case
+      tile_pass<NQ, MODE, true>(t, a, em, sh, aw, bh, U, nact, lane, wave, kWaves, nlist, ~nm & ((1u << a.G) - 1u),
+                                tot);
     }
   }
 }

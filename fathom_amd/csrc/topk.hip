@@ -555,7 +555,9 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
   if (threadIdx.x == 0) {
     s.thr[row] = t_hi;
     s.thr_lo[row] = t_lo;
-    *s.cnt1(row) = 0u;
+    // both halves of the fused candidate pass's 64-bit (done, count) counter
+    s.cnt1(row)[0] = 0u;
+    s.cnt1(row)[1] = 0u;
     *s.cnt2(row) = 0u;
   }
 }

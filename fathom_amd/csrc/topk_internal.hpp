@@ -53,7 +53,8 @@ constexpr int64_t kCntStride = 64;
 struct TopkSel {
   uint32_t *thr;        // [rows] first-pass threshold key T_hi
   uint32_t *thr_lo;     // [rows] safe threshold key T_lo
-  uint32_t *cand_cnt;   // [rows * kCntStride] candidates of the first pass
+  uint32_t *cand_cnt;   // [rows * kCntStride] candidates of the first pass (the fused
+                        // candidate pass: a 64-bit (waves done << 32 | candidates) counter)
   uint32_t *cand2_cnt;  // [rows * kCntStride] candidates of the fallback pass
   uint64_t *cand;       // [rows, cand_cap] K64 candidates (of the pass in effect)
   int64_t cand_cap;
