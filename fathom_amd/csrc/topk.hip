@@ -15,6 +15,7 @@
 // above a threshold -- still spread over many bins (few atomic collisions),
 // and a 64-bit K64 needs at most six rounds.
 #include "topk_internal.hpp"
+#include "scan_core.hpp"
 
 namespace fathom {
 namespace {
@@ -555,9 +556,7 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
   if (threadIdx.x == 0) {
     s.thr[row] = t_hi;
     s.thr_lo[row] = t_lo;
-    // both halves of the fused candidate pass's 64-bit (done, count) counter
-    s.cnt1(row)[0] = 0u;
-    s.cnt1(row)[1] = 0u;
+    *s.cnt1(row) = 0u;
     *s.cnt2(row) = 0u;
   }
 }
@@ -669,11 +668,9 @@ __device__ __forceinline__ void select_sorted(const Src &src, int64_t cnt, int64
   write_fixed(out, got, kk, m, sink, local);
 }
 
-// Exact top kk of a row's candidates: those of the first pass, or, where it
-// found fewer than kk, those of the fallback pass (which ran for exactly such
-// rows).  List layout: counts in the row counters.  Region layout: the first
-// pass's regions are copied to LDS while they are counted; a row with more
-// than kCandLds candidates is selected from its regions in place.
+// Exact top kk of a row's candidates (list layout): those of the first pass,
+// or, where it found fewer than kk, those of the fallback pass (which ran for
+// exactly such rows); counts in the row counters.
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_t k, int64_t sink, int64_t local,
                                                                TopkSel s, int64_t *__restrict__ idx) {
   __shared__ uint64_t cl[kCandLds];
@@ -684,23 +681,73 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
   const int64_t kk = k - sink - local;
   const uint64_t *gc = s.cand + row * s.cand_cap;
   int64_t *out = idx + row * k;
-  if (s.rc1) {
-    uint32_t *pre = reinterpret_cast<uint32_t *>(ss);  // free until the survivors are collected
-    RegionSrc src{s.rc1 + row * s.nreg, gc, s.nreg};
-    uint32_t cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
-    if (cnt < s.kk) {
-      src.rc = s.rc2 + row * s.nreg;
-      cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
-    }
-    if (cnt <= (uint32_t)kCandLds)
-      select_sorted(ArraySrc{cl, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
-    else
-      select_sorted(src, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
-    return;
-  }
   const uint32_t c1 = *s.cnt1(row);
   const int64_t cnt = min((int64_t)(c1 >= s.kk ? c1 : *s.cnt2(row)), s.cand_cap);
   select_sorted(ArraySrc{gc, cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, true);
+}
+
+// The fallback of the fused scan + top-k, run by the finalize workgroup of a
+// row whose candidate pass found fewer than kk candidates: the row (head h of
+// bh) is rescanned with T_lo into the regions under the second count array by
+// the workgroup's first four waves, with the scan's plan tables in tsh (LDS
+// that the caller frees for it).  The rescan computes the scores of the
+// candidate pass bit for bit (the same tile arithmetic).
+template <int NQ>
+__device__ __forceinline__ void rescan_row(const sc::ScanArgs &a, const sc::Emit &em, int64_t bh, int h,
+                                           sc::Shared<NQ> &tsh) {
+  int nact = 0;
+  const int U = sc::plan_tables<NQ>(tsh, a, bh, nact);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (wave < sc::kWaves) {
+    sc::Tile<NQ, 1> t;
+    t.r0 = 0;
+    uint32_t tot[4 * NQ];
+#pragma unroll
+    for (int g = 0; g < 4 * NQ; ++g) tot[g] = 0u;
+    const int64_t nlist = em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
+    const uint32_t skipm = ((1u << a.G) - 1u) & ~(1u << h);
+    sc::tile_pass<NQ, sc::kEmitFilter, true>(t, a, em, tsh, tsh.a[wave], bh, U, nact, lane, wave, sc::kWaves, nlist,
+                                             skipm, tot);
+    __builtin_amdgcn_s_setprio(0);
+  }
+  // the rescan's region counts and candidates are read back by other waves of
+  // the workgroup, and their old values may sit in the CU's L1: write back and
+  // invalidate before the barrier
+  __threadfence();
+  __syncthreads();
+}
+
+// Exact top kk of a row of the fused scan + top-k from its candidate regions
+// (row = bh * G + h), copied to LDS while they are counted; a row with more
+// than kCandLds candidates is selected from its regions in place.  A row with
+// fewer than kk first-pass candidates is rescanned first (rescan_row).
+template <int NQ>
+__global__ __launch_bounds__(kFinThreads) void finalize_fused_kernel(int64_t m, int64_t k, int64_t sink, int64_t local,
+                                                                     sc::ScanArgs a, sc::Emit em,
+                                                                     int64_t *__restrict__ idx) {
+  __shared__ uint64_t cl[kCandLds];
+  __shared__ uint64_t ss[kMaxK];
+  __shared__ RangeShared sh;
+  __shared__ uint32_t s_cnt;
+  static_assert(sizeof(sc::Shared<NQ>) <= sizeof(cl), "the rescan's plan tables fit the candidate buffer");
+  const TopkSel &s = em.sel;
+  const int64_t row = blockIdx.x;
+  const int64_t kk = k - sink - local;
+  const uint64_t *gc = s.cand + row * s.cand_cap;
+  int64_t *out = idx + row * k;
+  uint32_t *pre = reinterpret_cast<uint32_t *>(ss);  // free until the survivors are collected
+  RegionSrc src{s.rc1 + row * s.nreg, gc, s.nreg};
+  uint32_t cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
+  if (cnt < s.kk) {  // uniform
+    __syncthreads();  // cl holds the plan tables from here
+    rescan_row<NQ>(a, em, row / a.G, (int)(row % a.G), *reinterpret_cast<sc::Shared<NQ> *>(cl));
+    src.rc = s.rc2 + row * s.nreg;
+    cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
+  }
+  if (cnt <= (uint32_t)kCandLds)
+    select_sorted(ArraySrc{cl, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
+  else
+    select_sorted(src, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
 }
 
 // Exact top kk of a whole score row (rows up to kRowSelectMax): every element
@@ -1094,6 +1141,15 @@ int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t lo
                     hipStream_t st) {
   finalize_kernel<<<(unsigned)rows, kFinThreads, 0, st>>>(m, k, sink, local, s, idx);
   return launch_status("finalize_kernel");
+}
+
+int launch_finalize_fused(const sc::ScanArgs &a, const sc::Emit &em, int64_t rows, int64_t m, int64_t k, int64_t sink,
+                          int64_t local, int64_t *idx, hipStream_t st) {
+  if (a.G <= 4)
+    finalize_fused_kernel<1><<<(unsigned)rows, kFinThreads, 0, st>>>(m, k, sink, local, a, em, idx);
+  else
+    finalize_fused_kernel<2><<<(unsigned)rows, kFinThreads, 0, st>>>(m, k, sink, local, a, em, idx);
+  return launch_status("finalize_fused_kernel");
 }
 
 int launch_rowselect(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,

@@ -12,7 +12,8 @@
 //             hold the whole top kk;
 //   fallback  rows with fewer than kk candidates (a sample that was not
 //             representative) are filtered again with T_lo, into the same
-//             buffer under a second count; other rows skip the pass;
+//             buffer under a second count; other rows skip the pass (the
+//             fused scan's finalize workgroup rescans such a row itself);
 //   finalize  one workgroup per row selects the exact kk largest candidates by
 //             K64 = key << 32 | (0xFFFFFFFF - index) and writes them sorted.
 // Exactness never depends on the sample: a poor sample only costs a fallback
@@ -53,8 +54,7 @@ constexpr int64_t kCntStride = 64;
 struct TopkSel {
   uint32_t *thr;        // [rows] first-pass threshold key T_hi
   uint32_t *thr_lo;     // [rows] safe threshold key T_lo
-  uint32_t *cand_cnt;   // [rows * kCntStride] candidates of the first pass (the fused
-                        // candidate pass: a 64-bit (waves done << 32 | candidates) counter)
+  uint32_t *cand_cnt;   // [rows * kCntStride] candidates of the first pass
   uint32_t *cand2_cnt;  // [rows * kCntStride] candidates of the fallback pass
   uint64_t *cand;       // [rows, cand_cap] K64 candidates (of the pass in effect)
   int64_t cand_cap;

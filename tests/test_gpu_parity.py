@@ -657,22 +657,23 @@ def test_scan_topk_fallback_pass_host_paired():
         off.free_host(hp2)
 
 
-@pytest.mark.parametrize("direction,n,BH", [(1.0, 90000, 2), (-1.0, 90000, 2), (1.0, 300000, 2), (-1.0, 200000, 8)])
-def test_scan_topk_fallback_pass(direction, n, BH):
+@pytest.mark.parametrize("direction,n,BH,G", [(1.0, 90000, 2, 4), (-1.0, 90000, 2, 4), (1.0, 300000, 2, 4),
+                                               (-1.0, 200000, 8, 4), (-1.0, 90000, 2, 8), (-1.0, 40000, 1, 3)])
+def test_scan_topk_fallback_pass(direction, n, BH, G):
     """Fused path with scores falling (or rising) along the sequence: a falling
     row has its top kk inside the first sampled tile, so the tight threshold
-    falls short and the fallback scan runs; the result equals the unfused one.
-    The scores are coarse (few distinct values), so the fallback pass's
-    candidates at the longer length outgrow one workgroup's LDS and are
-    selected from the regions in place.  BH = 8 at n = 200000: 392
-    candidate-pass workgroups over eight rows."""
-    print(f"[fused-fallback] direction={direction} n={n} BH={BH}", flush=True)
+    falls short and the row's finalize workgroup rescans it with T_lo; the
+    result equals the unfused one.  The scores are coarse (few distinct
+    values), so the rescan's candidates at the longer length outgrow one
+    workgroup's LDS and are selected from the regions in place.  BH = 8 at
+    n = 200000: eight rows of rescans; G = 8: the two-tile-row rescan."""
+    print(f"[fused-fallback] direction={direction} n={n} BH={BH} G={G}", flush=True)
     d = 128
     K = torch.zeros(BH, n, d)
     K[:, :, 0] = torch.linspace(1, -1, n)[None] * 3.0 * direction
     K[:, :, 1] = torch.randn(BH, n) * 0.01
     st = bp.PlaneStore(K.to(DEV))
-    q = torch.zeros(BH, 4, d)
+    q = torch.zeros(BH, G, d)
     q[:, :, 0] = 1.0
     q[:, 1::2, 1] = 1.0
     g = torch.ones(BH, d)
@@ -689,8 +690,8 @@ def test_scan_topk_stages_repeat(fallback):
     """The stage entry point: the stages run one by one on one workspace, and the
     candidate pass run again on its own over the state the last full call left
     (the way bench.py times it), give the fused call's indices -- also for rows
-    whose tight threshold falls short, where the candidate pass's own fallback
-    check must see this pass's totals, not the sum over repeats."""
+    whose tight threshold falls short, which the finalize stage rescans each
+    time it runs."""
     print(f"[fused-stages] fallback={fallback}", flush=True)
     if fallback:
         BH, d, n = 2, 128, 90000
