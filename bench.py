@@ -11,7 +11,8 @@ the same steps; the unfused pair must select the same indices.
 
 `value` counts scanned token*heads per second of scan + top-k with the index
 resident in HBM (n * BH / t_scan_topk, t_scan_topk the GPU time of one fused
-call: 20 calls captured in one HIP graph, checked equal to the eager call).
+call: 20 calls captured in one HIP graph, replayed for 30 ms before 10 timed
+replays, checked equal to the eager call).
 The roofline object is for the dominant kernel of that call, the candidate
 pass (scan_wave_kernel<1, 2>), run on its own through the stage entry point
 (20 launches in one HIP graph, events on the launching stream; algorithmic
@@ -292,10 +293,11 @@ def run_decode_step(torch, bp, off, W, dev, steps, warmup):
             "scan_topk_GBps": scan_bytes / (ms["scan_topk"] * 1e-3) / 1e9}
 
 
-def _graph_run(torch, fn, reps=20):
+def _graph_run(torch, fn, reps=20, warm_ms=30.0, timed=10):
     """GPU time of one fn() call: reps calls captured in one HIP graph, replayed
-    3 times after a warm-up, events around the replays.  Returns (ms, the last
-    call's output after the replays)."""
+    back to back for at least warm_ms first (the clocks settle under load),
+    then `timed` replays between events.  Returns (ms, the last call's output
+    after the replays)."""
     for _ in range(2):
         fn()
     torch.cuda.synchronize()
@@ -305,13 +307,18 @@ def _graph_run(torch, fn, reps=20):
             r = fn()
     gph.replay()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(4):
+            gph.replay()
+        torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(3):
+    for _ in range(timed):
         gph.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / (3 * reps), r
+    return e0.elapsed_time(e1) / (timed * reps), r
 
 
 def _graph_ms(torch, fn, reps=20):
@@ -345,7 +352,7 @@ def run_kernel_table(torch, bp, W, dev):
     del ps, cs, x
     torch.cuda.empty_cache()
     return {"shape": "n=131072, BH=32 (batch 4 x 8 KV heads), G=4, synthetic config-2 keys",
-            "timing": "HIP graph of 20 launches, 3 replays", "scans": rows,
+            "timing": "HIP graph of 20 launches, 10 replays after 30 ms of warm-up replays", "scans": rows,
             "reference_A100": "paper/tables/tab_kernel.tex:6-10 at 128k: Fathom 48 0.415 ms (102 GB/s); "
                               "16-ch / 32-ch / full 4-bit nibble scans 218 / 245 / 282 GB/s"}
 
@@ -379,7 +386,7 @@ def run_config4(torch, bp, W, dev):
                                         "scanned_tokens_per_s": n * x["BH"] / (ms_st * 1e-3)}
     del stores, x
     torch.cuda.empty_cache()
-    return {"workload": W.CONFIGS[4]["name"], "k": 2048, "timing": "HIP graph of 10 launches, 3 replays",
+    return {"workload": W.CONFIGS[4]["name"], "k": 2048, "timing": "HIP graph of 10 launches, 10 replays after 30 ms of warm-up replays",
             "runs": res}
 
 
@@ -734,13 +741,13 @@ def main():
                    "bits_per_token": round(hbm["bits_per_token"], 3), "parallelism": "single GPU"},
         "stage_ms": {k: round(v, 4) for k, v in st.items()},
         "scan_topk_ms": scan_topk_ms,
-        "scan_topk_timing": "20 fused calls captured in one HIP graph, 3 replays (eager per-stage time: stage_ms)",
+        "scan_topk_timing": "20 fused calls captured in one HIP graph, 10 replays after 30 ms of warm-up replays (eager per-stage time: stage_ms)",
         "unfused_scan_plus_topk_ms": st["scan"] + st["topk"],
         "roofline": {"bound": "hbm", "kernel": CAND_KERNEL + " (candidate pass of the fused scan + top-k)",
                      "achieved": achieved, "launch_ms": cand_ms, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": hbm["scan_bytes"],
-                     "timing": "stage entry point, candidate pass alone, 20 launches in one HIP graph, 3 replays",
+                     "timing": "stage entry point, candidate pass alone, 20 launches in one HIP graph, 10 replays after 30 ms of warm-up replays",
                      "issue_ceiling": issue_ceiling(hbm["scan_bytes"], BH * -(-n // 64), achieved),
                      "whole_call": {"ms": scan_topk_ms, "GBps": hbm["scan_bytes"] / (scan_topk_ms * 1e-3) / 1e9,
                                     "frac": hbm["scan_bytes"] / (scan_topk_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,

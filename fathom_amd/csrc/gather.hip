@@ -42,7 +42,6 @@ constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kAttnTok = 16 * kAttnWaves;          // distinct tokens per workgroup (16 per wave)
 constexpr int kPartStride = kAttnD + 2;            // (max, sum, weighted V[128])
-constexpr int kMaxSplit = kMaxGK / kAttnTok;       // workgroups per row at most
 
 template <typename V>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const char *__restrict__ src, int64_t cap,

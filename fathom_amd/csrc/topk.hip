@@ -471,97 +471,6 @@ __device__ __forceinline__ uint32_t masked_key(const float *row, int64_t i, int6
   return (i < sink || i >= lstart) ? kKeyNegInf : score_key(row[i]);
 }
 
-// Thresholds of a row from its sampled keys: each thread keeps its M largest
-// keys (2 kk <= 1024 M); T_lo is the kk-th largest of those M * 1024 values
-// (for M = 1: of the maxima of P >= kk groups of them).
-// They are kk elements of the sample >= T_lo, so T_lo <= the sample's kk-th
-// largest <= the row's: every element of the row's top kk has key >= T_lo.
-// T_hi is the r_hi-th largest of the same values (r_hi <= kk, so T_hi >= T_lo).
-template <int M>
-__device__ void sample_bound(const uint32_t (&v)[kSelPer], uint32_t kk, uint32_t r_hi, uint64_t *vals,
-                             RangeShared &sh, uint32_t &t_lo, uint32_t &t_hi) {
-  uint32_t top[M];
-#pragma unroll
-  for (int i = 0; i < M; ++i) top[i] = 0u;
-#pragma unroll
-  for (int u = 0; u < kSelPer; ++u) {
-    uint32_t x = v[u];
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-      const uint32_t hi = max(top[i], x);
-      x = min(top[i], x);
-      top[i] = hi;
-    }
-  }
-  // the M * 1024 candidates as distinct nonzero values key << 32 | slot; the
-  // keys of the kk-th and r_hi-th largest are the thresholds
-  uint64_t w[M];
-#pragma unroll
-  for (int i = 0; i < M; ++i) w[i] = ((uint64_t)top[i] << 32) | (uint32_t)(threadIdx.x + 1024 * i + 1);
-  if constexpr (M > 1) {  // 2048+ values: histogram range selection
-#pragma unroll
-    for (int i = 0; i < M; ++i) vals[threadIdx.x + kSelThreads * i] = w[i];
-    __syncthreads();
-    const ArraySrc src{vals, (int64_t)M * kSelThreads};
-    const uint64_t lo = range_select(src, src.cnt, kk, sh);
-    const uint64_t hi = r_hi < kk ? range_select(src, src.cnt, r_hi, sh) : lo;
-    t_lo = (uint32_t)(lo >> 32);
-    t_hi = (uint32_t)(hi >> 32);
-  } else {
-    // P = the smallest power of two >= max(kk, 64) values: the maxima of P
-    // disjoint groups of sampled keys (thread s < P combines the 1024 / P
-    // threads s, s + P, ...), ranked by one sort of P values.  They are
-    // distinct sample elements, so the kk-th largest is a valid T_lo.
-    int P = kWave;
-    while (P < (int)kk) P <<= 1;
-    uint32_t *mx = sh.hist;  // 1024 words, free here
-    mx[threadIdx.x] = top[0];
-    __syncthreads();
-    uint32_t g = 0u;
-    if ((int)threadIdx.x < P)
-      for (int j = threadIdx.x; j < kSelThreads; j += P) g = max(g, mx[j]);
-    const uint64_t wg[1] = {((uint64_t)g << 32) | (uint32_t)(threadIdx.x + 1)};
-    block_rank_desc<1>(wg, vals, vals + kSelThreads, P, [&](int rank, uint64_t x) {
-      if (rank == (int)kk - 1) sh.lo = x;
-      if (rank == (int)r_hi - 1) sh.hi = x;
-    });
-    __syncthreads();
-    t_lo = (uint32_t)(sh.lo >> 32);
-    t_hi = r_hi < kk ? (uint32_t)(sh.hi >> 32) : t_lo;
-  }
-}
-
-__global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t *__restrict__ samp,
-                                                                  int64_t samp_cap, uint32_t kk, uint32_t r_hi,
-                                                                  TopkSel s) {
-  __shared__ uint64_t vals[4 * kSelThreads];
-  __shared__ RangeShared sh;
-  const int64_t row = blockIdx.x;
-  const uint32_t *src = samp + row * samp_cap;
-  uint32_t v[kSelPer];
-#pragma unroll
-  for (int u = 0; u < kSelPer; ++u) {
-    const int64_t i = threadIdx.x + (int64_t)u * kSelThreads;
-    v[u] = i < samp_cap ? src[i] : 0u;
-  }
-  uint32_t t_lo = 0u, t_hi = 0u;  // fewer samples than kk: every element is a candidate
-  if (samp_cap >= (int64_t)kk) {
-    if (2 * kk <= kSelThreads)
-      sample_bound<1>(v, kk, r_hi, vals, sh, t_lo, t_hi);
-    else if (kk <= kSelThreads)
-      sample_bound<2>(v, kk, r_hi, vals, sh, t_lo, t_hi);
-    else
-      sample_bound<4>(v, kk, r_hi, vals, sh, t_lo, t_hi);
-  }
-  if (threadIdx.x == 0) {
-    s.thr[row] = t_hi;
-    s.thr_lo[row] = t_lo;
-    *s.cnt1(row) = 0u;
-    *s.cnt2(row) = 0u;
-  }
-}
-
-// Sampled keys of score rows: tile ti of the sample is tile ti * S of the row.
 __global__ __launch_bounds__(256) void sample_scores_kernel(const float *__restrict__ scores, int64_t n, int64_t S,
                                                             int64_t sink, int64_t lstart, uint32_t *__restrict__ samp,
                                                             int64_t samp_cap) {
@@ -943,6 +852,134 @@ __device__ __forceinline__ uint32_t kth_bound(const uint32_t (&v)[PER], int cnt,
   return base + (sh.hsel << sft2);
 }
 
+// Histogram scan of a round of two_bounds: bins counted from the top; for
+// each of the two ranks, the bin that holds it and the count above that bin.
+__device__ __forceinline__ void two_bins(const uint32_t *hist, uint32_t na, uint32_t nb, RangeShared &sh,
+                                         uint32_t (&sel)[2], uint32_t (&above_sel)[2], uint32_t *s_sel) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t c0 = hist[kBins - 1 - 2 * tid], c1 = hist[kBins - 2 - 2 * tid], c = c0 + c1;
+  const uint32_t wi = wave_incl_scan_u32(c);
+  if (lane == kWave - 1) sh.wsum[wave] = wi;
+  __syncthreads();
+  uint32_t above = wi - c;
+  for (int w = 0; w < wave; ++w) above += sh.wsum[w];
+  const uint32_t need[2] = {na, nb};
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (above < need[r] && above + c0 >= need[r]) {
+      s_sel[2 * r] = (uint32_t)(kBins - 1 - 2 * tid);
+      s_sel[2 * r + 1] = above;
+    }
+    if (above + c0 < need[r] && above + c >= need[r]) {
+      s_sel[2 * r] = (uint32_t)(kBins - 2 - 2 * tid);
+      s_sel[2 * r + 1] = above + c0;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    sel[r] = s_sel[2 * r];
+    above_sel[r] = s_sel[2 * r + 1];
+  }
+}
+
+// Lower bounds of the na-th and the nb-th largest of the cnt values v (thread
+// t holds values t + 1024 u; nb, na <= cnt) in two histogram rounds shared by
+// both ranks: 2048 bins over [min, max], then 2048 bins over each rank's bin
+// (the second histogram in hist2).  Each bound is the lower edge of the final
+// bin that holds its rank: at least that many values reach it, and it lies
+// within (max - min) / 2^22 of the value of that rank.
+template <int PER>
+__device__ __forceinline__ void two_bounds(const uint32_t (&v)[PER], int cnt, uint32_t na, uint32_t nb,
+                                           RangeShared &sh, uint32_t *hist2, uint32_t *s_sel, uint32_t &ta,
+                                           uint32_t &tb) {
+  static_assert(kBins == 2 * kFinThreads, "two bins per thread");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
+  uint32_t mn = ~0u, mx = 0u;
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (tid + u * kFinThreads < cnt) {
+      mn = min(mn, v[u]);
+      mx = max(mx, v[u]);
+    }
+  wave_minmax_u32(mn, mx);
+  if (lane == 0) {
+    sh.wmin[wave] = mn;
+    sh.wmax[wave] = mx;
+  }
+  sh.hist[tid] = sh.hist[tid + kFinThreads] = 0u;
+  hist2[tid] = hist2[tid + kFinThreads] = 0u;
+  __syncthreads();
+  uint32_t lo = ~0u, hi = 0u;
+  for (int w = 0; w < nw; ++w) {
+    lo = min(lo, (uint32_t)sh.wmin[w]);
+    hi = max(hi, (uint32_t)sh.wmax[w]);
+  }
+  const uint32_t R = hi - lo;
+  const int bl = R ? 32 - __clz((int)R) : 0;
+  const int sft = bl > 11 ? bl - 11 : 0;  // (v - lo) >> sft < 2048
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (tid + u * kFinThreads < cnt) atomicAdd(&sh.hist[(v[u] - lo) >> sft], 1u);
+  __syncthreads();
+  uint32_t sel[2], above[2];
+  two_bins(sh.hist, na, nb, sh, sel, above, s_sel);
+  const uint32_t base_a = lo + (sel[0] << sft), base_b = lo + (sel[1] << sft);
+  if (sft == 0) {  // one value per bin: the bins' values are the ranks' values
+    ta = base_a;
+    tb = base_b;
+    return;
+  }
+  const int sft2 = sft > 11 ? sft - 11 : 0;
+  sh.hist[tid] = sh.hist[tid + kFinThreads] = 0u;  // every thread has read both histograms (two_bins' barriers)
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (tid + u * kFinThreads < cnt) {
+      const uint32_t b = (v[u] - lo) >> sft;
+      if (b == sel[0]) atomicAdd(&sh.hist[(v[u] - base_a) >> sft2], 1u);
+      if (b == sel[1]) atomicAdd(&hist2[(v[u] - base_b) >> sft2], 1u);
+    }
+  __syncthreads();
+  uint32_t sa[2], aa[2], sb[2], ab[2];
+  two_bins(sh.hist, na - above[0], na - above[0], sh, sa, aa, s_sel);
+  two_bins(hist2, nb - above[1], nb - above[1], sh, sb, ab, s_sel);
+  ta = base_a + (sa[0] << sft2);
+  tb = base_b + (sb[0] << sft2);
+}
+
+// Thresholds of a row from its sampled keys (the row's samp_cap keys, PER per
+// thread): T_lo a lower bound of the sample's kk-th largest key, T_hi one of
+// its r_hi-th largest (r_hi <= kk, so T_hi >= T_lo up to the bounds' bins).
+// The sample is a subset of the row, so T_lo never exceeds the row's kk-th
+// largest: every element of the row's top kk has key >= T_lo.  Also clears
+// the row's candidate counters.
+template <int PER>
+__global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t *__restrict__ samp,
+                                                                  int64_t samp_cap, uint32_t kk, uint32_t r_hi,
+                                                                  TopkSel s) {
+  static_assert(kSelThreads == kFinThreads, "the bounds use the finalize block size");
+  __shared__ RangeShared sh;
+  __shared__ uint32_t hist2[kBins];
+  __shared__ uint32_t s_sel[4];
+  const int64_t row = blockIdx.x;
+  const uint32_t *src = samp + row * samp_cap;
+  uint32_t v[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int64_t i = threadIdx.x + (int64_t)u * kSelThreads;
+    v[u] = i < samp_cap ? src[i] : 0u;
+  }
+  uint32_t t_lo = 0u, t_hi = 0u;  // fewer samples than kk: every element is a candidate
+  if (samp_cap >= (int64_t)kk) two_bounds<PER>(v, (int)samp_cap, kk, r_hi < kk ? r_hi : kk, sh, hist2, s_sel, t_lo, t_hi);
+  if (threadIdx.x == 0) {
+    s.thr[row] = r_hi < kk ? t_hi : t_lo;
+    s.thr_lo[row] = t_lo;
+    *s.cnt1(row) = 0u;
+    *s.cnt2(row) = 0u;
+  }
+}
+
 // Exact top kk of short score rows whose 16-token group maxima the scan
 // wrote beside them (gmax [rows, ceil(n / 16)]: the largest masked key of each
 // group).  T, a lower bound of the kk-th largest group maximum, bounds the
@@ -1116,7 +1153,16 @@ size_t topk_layout(int64_t rows, int64_t n, int64_t k, bool regions, char *base,
 int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, int64_t r_hi, TopkSel s,
                        hipStream_t st) {
   if (samp_cap > kMaxSample) return fail(FATHOM_ERR_INVALID, "select: %lld sampled keys exceed %lld", (long long)samp_cap, (long long)kMaxSample);
-  select_keys_kernel<<<(unsigned)rows, kSelThreads, 0, st>>>(samp, samp_cap, (uint32_t)kk, (uint32_t)r_hi, s);
+  const unsigned g = (unsigned)rows;
+  const uint32_t ukk = (uint32_t)kk, urh = (uint32_t)r_hi;
+  if (samp_cap <= 8 * kSelThreads)
+    select_keys_kernel<8><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+  else if (samp_cap <= 16 * kSelThreads)
+    select_keys_kernel<16><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+  else if (samp_cap <= 32 * kSelThreads)
+    select_keys_kernel<32><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+  else
+    select_keys_kernel<kSelPer><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
   return launch_status("select_keys_kernel");
 }
 
