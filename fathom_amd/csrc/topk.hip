@@ -190,6 +190,87 @@ __device__ __forceinline__ void block_rank_desc(const uint64_t (&v)[E], uint64_t
   }
 }
 
+// Descending ranks of the cnt valid values of E * 1024 (thread t holding slots
+// t + 1024 e; the valid ones are the slots below cnt, all distinct) by a
+// counting sort: 2048 bins of (v - min) >> s over the values' range, each
+// value's place in its bin from a returning LDS atomic, the bins' offsets by a
+// prefix sum from the top bin down, then every value's rank = the values in
+// higher bins + the greater values of its own bin (a few, read from the
+// values placed in bin order).  Values crowd a bin only where their range is
+// dominated by a few outliers: then (more than kCrowd in one bin) the ranks
+// come from block_rank_desc over the first nlim slots instead.  put(rank, v)
+// is called for every valid value.  scratch: LDS of 4096 values.
+constexpr uint32_t kCrowd = 48;
+template <int E, typename Put>
+__device__ __forceinline__ void bin_rank_desc(const uint64_t (&v)[E], int cnt, uint64_t *scratch, RangeShared &sh,
+                                              int nlim, Put put) {
+  static_assert(kBins == 2 * kFinThreads, "two bins per thread");
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = kFinThreads >> 6;
+  uint64_t *placed = scratch;                                           // [2048] values in bin order
+  uint32_t *hist = reinterpret_cast<uint32_t *>(scratch + kBins);       // [2048] values per bin
+  uint32_t *above = hist + kBins;                                       // [2048] values in higher bins
+  uint64_t mn = ~0ull, mx = 0ull;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (t + 1024 * e < cnt) {
+      mn = v[e] < mn ? v[e] : mn;
+      mx = v[e] > mx ? v[e] : mx;
+    }
+  wave_minmax_u64(mn, mx);
+  if (lane == 0) {
+    sh.wmin[wave] = mn;
+    sh.wmax[wave] = mx;
+  }
+  hist[t] = hist[t + kFinThreads] = 0u;
+  if (t == 0) sh.fcnt = 0u;
+  __syncthreads();
+  uint64_t lo = ~0ull, hi = 0ull;
+  for (int w = 0; w < nw; ++w) {
+    lo = sh.wmin[w] < lo ? sh.wmin[w] : lo;
+    hi = sh.wmax[w] > hi ? sh.wmax[w] : hi;
+  }
+  const uint64_t R = cnt > 0 ? hi - lo : 0ull;
+  const int bl = R ? 64 - __clzll((long long)R) : 0;
+  const int sft = bl > 11 ? bl - 11 : 0;  // (v - lo) >> sft < 2048
+  uint32_t bin[E], slot[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (t + 1024 * e < cnt) {
+      bin[e] = (uint32_t)((v[e] - lo) >> sft);
+      slot[e] = atomicAdd(&hist[bin[e]], 1u);
+    }
+  __syncthreads();
+  // values in higher bins: thread t holds bins 2047 - 2t, 2046 - 2t
+  const uint32_t c0 = hist[kBins - 1 - 2 * t], c1 = hist[kBins - 2 - 2 * t], c = c0 + c1;
+  const uint32_t wi = wave_incl_scan_u32(c);
+  if (lane == kWave - 1) sh.wsum[wave] = wi;
+  if (c0 > kCrowd || c1 > kCrowd) sh.fcnt = 1u;  // any thread: the same value
+  __syncthreads();
+  if (sh.fcnt) {  // uniform
+    block_rank_desc<E>(v, scratch, scratch + 2 * kFinThreads, nlim, [&](int rank, uint64_t x) {
+      if (rank < cnt) put(rank, x);
+    });
+    return;
+  }
+  uint32_t ab = wi - c;
+  for (int w = 0; w < wave; ++w) ab += sh.wsum[w];
+  above[kBins - 1 - 2 * t] = ab;
+  above[kBins - 2 - 2 * t] = ab + c0;
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (t + 1024 * e < cnt) placed[above[bin[e]] + slot[e]] = v[e];
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (t + 1024 * e < cnt) {
+      const uint32_t base = above[bin[e]], n = hist[bin[e]];
+      uint32_t rank = base;
+      for (uint32_t j = 0; j < n; ++j) rank += placed[base + j] > v[e] ? 1u : 0u;
+      put((int)rank, v[e]);
+    }
+}
+
 // Value sources of the selections.  for_each(f) calls f(ok, v) for every value
 // v of the set, each thread of the workgroup for its share, in loops that are
 // uniform over the workgroup (all threads call it; f runs with every lane
@@ -570,8 +651,8 @@ __device__ __forceinline__ void select_sorted(const Src &src, int64_t cnt, int64
   int nlim = kWave;
   while (nlim < nv) nlim <<= 1;  // the survivors fill the first nv <= 2048 slots
   const int got = nv < (int)kk ? nv : (int)kk;
-  // the padding ranks at or after nv: only the survivors are written
-  block_rank_desc<2>(v2, cl, cl + 2 * kFinThreads, nlim, [&](int rank, uint64_t x) {
+  // only the survivors are ranked and written
+  bin_rank_desc<2>(v2, nv, cl, sh, nlim, [&](int rank, uint64_t x) {
     if (rank < got) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x);
   });
   write_fixed(out, got, kk, m, sink, local);
@@ -1098,7 +1179,7 @@ __global__ __launch_bounds__(kFinThreads) void rowselect_gmax_kernel(const float
   int nlim = kWave;
   while (nlim < (int)cnt) nlim <<= 1;
   const int got = (int64_t)cnt < kk ? (int)cnt : (int)kk;
-  block_rank_desc<2>(v2, cl, cl + 2 * kFinThreads, nlim, [&](int rank, uint64_t x) {
+  bin_rank_desc<2>(v2, (int)cnt, cl, sh, nlim, [&](int rank, uint64_t x) {
     if (rank < got) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x);
   });
   write_fixed(out, got, kk, m, sink, local);
