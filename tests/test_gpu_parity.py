@@ -297,6 +297,20 @@ def test_topk_ties_nan_inf_negzero():
     _topk_case(rows, 100, 3, 5, m=n + 2)
 
 
+@pytest.mark.parametrize("n,k", [(20000, 512), (100000, 512), (100000, 2048)])
+def test_topk_final_ranking_spread_and_crowded(n, k):
+    """The final ranking of the selected values counts them into 2048 bins over
+    their range: spread values (row 0) take the counting sort; a far outlier
+    per row squeezes the rest into few bins (rows 1-2: +1e30, +inf), which
+    takes the block rank sort instead.  Both orders equal the oracle's."""
+    print(f"[topk-rank] n={n} k={k}", flush=True)
+    rng = np.random.default_rng(n + 3 * k)
+    rows = rng.standard_normal((3, n)).astype(np.float32)
+    rows[1, n // 3] = 1e30
+    rows[2, n // 2] = np.inf
+    _topk_case(rows, k, 4, 32)
+
+
 def test_topk_huge_tie_bucket_slow_path():
     """All scores inside one first-level bucket (> 8192 candidates)."""
     rng = np.random.default_rng(2)
