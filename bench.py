@@ -686,6 +686,8 @@ def main():
                           "roofline_pcie": {"peak": PCIE_PEAK_GBPS,
                                             "frac_step": ci_bytes / (ci_tot * 1e-3) / 1e9 / PCIE_PEAK_GBPS},
                           "index_sets_equal_hbm": bool(torch.equal(ci["idx"], hbm["idx"]))}
+            if not (torch.equal(ci["idx"], hbm["idx"]) and torch.equal(ci["pipelined_idx"], hbm["idx"])):
+                raise RuntimeError("copy-index (whole or pipelined) index sets differ from the HBM path's")
             ps = ci["pipelined_stage_ms"]
             p_tot = sum(ps.values())
             copy_index["pipelined_4_chunks"] = {
