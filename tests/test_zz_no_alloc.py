@@ -65,6 +65,29 @@ def test_noalloc_equals_workspace_entry_on_shrinking_calls():
     assert torch.cuda.mem_get_info()[0] == free0
 
 
+def test_noalloc_fallback_rescan():
+    """A falling row (its top kk in the first sampled tile: the sample's
+    threshold misleads and the row's finalize workgroup rescans it) on the
+    static array equals the workspace entry point."""
+    print("[noalloc] fallback rescan", flush=True)
+    BH, d, n = 2, 128, 90_000
+    K = torch.zeros(BH, n, d)
+    K[:, :, 0] = torch.linspace(3, -3, n)[None]
+    K[:, :, 1] = torch.randn(BH, n, generator=torch.Generator().manual_seed(11)) * 0.01
+    st = bp.PlaneStore(K.to(DEV))
+    q = torch.zeros(BH, 4, d)
+    q[:, :, 0] = 1.0
+    q[:, 1::2, 1] = 1.0
+    g = torch.ones(BH, d)
+    g[:, 0], g[:, 1] = 1000.0, 10.0
+    q, plan = q.to(DEV), bp.make_plan(g.to(DEV), 6.0)
+    ref = st.scan_topk(q, plan, 512, 4, 32)
+    idx = torch.full_like(ref, -1)
+    _noalloc(st, plan, q, 512, 4, 32, n, idx)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(idx, ref, rtol=0, atol=0)
+
+
 def test_noalloc_refuses_shapes_past_the_array():
     L = _lib.lib()
     need = L.fathom_scan_topk_workspace_bytes(8, 4, 1 << 20, 512, 4, 32)
