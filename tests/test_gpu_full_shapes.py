@@ -13,13 +13,16 @@ Per case: the plan bit for bit; the fused scan + top-k == sink_local_topk(scan)
 tiles per row and of the blocks of up to 512 selected tokens per row within
 1e-3 of oracle.scan_planes over those blocks (the quantiser works per 64-token
 block, so quantising the gathered blocks gives the full store's codes and
-scales).
+scales); exact attention over the selected rows (union and per-position
+reads) within 1e-4 relative + 2e-5 absolute of the float64 oracle, with the
+union's distinct-row counts equal.
 """
 import numpy as np
 import pytest
 import torch
 
 from fathom_amd import bitplane as bp
+from fathom_amd import offload as off
 from fathom_amd import workloads as W
 from oracle import fathom_oracle as O
 
@@ -85,3 +88,22 @@ def test_full_shape_scores_on_tiles_and_selected_tokens(full):
         err = np.abs(got - ref)
         bad = err > 1e-3 * np.abs(ref) + floor
         assert not bad.any(), f"row {r}: {int(bad.sum())} of {bad.size} scores off; max err {err.max():.3e}"
+
+
+def test_full_shape_attention_matches_oracle(full):
+    print(f"[full-shape] config {full['cfg']}: attention vs oracle", flush=True)
+    x, idx = full["x"], full["idx"]
+    n = x["n"]
+    V = W.synth_values(x["BH"], n, device=DEV)
+    q = x["q"].float().contiguous()
+    ref, rnu = O.gather_attention(q.cpu().numpy(), idx.cpu().numpy(), n, x["K"].float().cpu().numpy(),
+                                  V.float().cpu().numpy())
+    for unique in (True, False):
+        out, nu = off.gather_attention(q, idx, n, x["K"], V, n, unique=unique)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref)
+        bad = err > 1e-4 * np.abs(ref) + 2e-5
+        assert not bad.any(), f"unique={unique}: {int(bad.sum())} outputs off; max err {err.max():.3e}"
+        if unique:
+            np.testing.assert_array_equal(nu.cpu().numpy(), rnu)
