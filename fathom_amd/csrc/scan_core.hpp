@@ -617,9 +617,63 @@ __device__ __forceinline__ uint32_t group_max_key(const float (&s)[kR], int64_t 
   return nan ? 0xFFFFFFFFu : score_key(mx);
 }
 
-template <int NQ, bool GMAX = false>
+// Scores of a wave-tile wholly inside its row and block range: lane l holds
+// tokens 16 l .. 16 l + 15 of each head (the MFMA layout), so a store
+// instruction straight from the registers would write four 16-byte pieces 64
+// bytes apart per lane quad.  Instead each head's 4 KB goes through the wave's
+// scale buffer (free once the tile's chunks are computed): float4 f (tokens
+// 4f .. 4f + 3) in slot f ^ ((f >> 4) & 3), which spreads the sixteen lanes of
+// each LDS phase over distinct banks both ways; then each store instruction
+// writes 1 KB of consecutive tokens, with the non-temporal hint (the scores are
+// read once, by the next kernel or the caller).
+template <int NQ, bool GMAX>
+__device__ __forceinline__ void emit_scores_staged(const Emit &em, const Tile<NQ, 1> &t, const Shared<NQ> &sh,
+                                                   const ScanArgs &a, int64_t bh, int64_t beta0, int lane, void *stage) {
+  const int b = lane >> 2, i = lane & 3;
+  const int64_t beta = beta0 + b;
+  const int64_t tok0 = beta * kBlk + 16 * i;
+  const bool plain = tok0 >= em.sink && tok0 + kR <= em.lstart;
+  const int64_t ngrp = (a.n + kR - 1) / kR;
+  f4 *slots = reinterpret_cast<f4 *>(stage);
+#pragma unroll
+  for (int h = 0; h < 4 * NQ; ++h) {
+    if (h >= a.G) break;
+    float f[4], s[kR];
+    head_factors(f, t, sh, h);
+#pragma unroll
+    for (int r = 0; r < kR; ++r) s[r] = tile_score<NQ, 1>(t, f, r, h);
+    if (GMAX) em.gmax[(bh * a.G + h) * ngrp + beta * 4 + i] = group_max_key(s, tok0, a.n, em.sink, em.lstart, plain);
+    wave_lds_sync();  // the buffer's last readers (the chunks, or the previous head) are done
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int fi = 4 * lane + c;
+      slots[fi ^ ((fi >> 4) & 3)] = f4{s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]};
+    }
+    wave_lds_sync();
+    float *dst = em.out + (bh * a.G + h) * a.n + beta0 * kBlk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int fi = 64 * j + lane;
+      __builtin_nontemporal_store(slots[fi ^ ((fi >> 4) & 3)], reinterpret_cast<f4 *>(dst + 4 * fi));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // one head's values live at a time
+  }
+}
+
+// Scores [BH, G, n] of a wave-tile (and, GMAX, the 16-token group maxima
+// beside them).  STAGED (kernels with registers to spare for it): whole tiles
+// go out through stage, the wave's 4 KB LDS scale buffer, free at this point.
+template <int NQ, bool GMAX = false, bool STAGED = false>
 __device__ __forceinline__ void emit_scores(const Emit &em, const Tile<NQ, 1> &t, const Shared<NQ> &sh, const ScanArgs &a,
-                                            int64_t bh, int64_t beta0, int lane) {
+                                            int64_t bh, int64_t beta0, int lane, void *stage = nullptr) {
+  static_assert(sizeof(sh.a[0]) == kWTok * sizeof(float), "a wave's scale buffer holds one head of a wave-tile");
+  if constexpr (STAGED) {
+    if (beta0 >= a.blk0 && beta0 + kWB <= a.blk_end && (beta0 + kWB) * kBlk <= a.n && (a.n & 3) == 0 &&
+        ((uintptr_t)stage & 15) == 0) {  // uniform
+      emit_scores_staged<NQ, GMAX>(em, t, sh, a, bh, beta0, lane, stage);
+      return;
+    }
+  }
   const int b = lane >> 2, i = lane & 3;
   const int64_t beta = beta0 + b;
   if (beta < a.blk0 || beta >= a.blk_end) return;
@@ -765,7 +819,7 @@ __device__ __forceinline__ void tile_pass(Tile<NQ, 1> &t, const ScanArgs &a, con
     set_priority_by_tiles_left((nlist - 1 - L) / Ls);
     scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
     if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax)
-      emit_scores<NQ, MODE == kEmitScoresMax>(em, t, sh, a, bh, beta0, lane);
+      emit_scores<NQ, MODE == kEmitScoresMax, MODE == kEmitScoresMax && NQ == 1>(em, t, sh, a, bh, beta0, lane, aw);
     if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, FB, skipm, tot);
     wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
   }
