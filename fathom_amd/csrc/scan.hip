@@ -15,9 +15,11 @@ using namespace sc;
 // finalize workgroup (launch_finalize_fused).
 // PAIR (stores in mapped host memory, sub a multiple of 32): the first pass
 // scans pairs of adjacent wave-tiles with 256-byte loads (scan_tile_pair).
+// Registers: four waves per SIMD for the candidate pass (its few stores), two
+// where the scores go out through LDS (score modes) or pairs of tiles are held.
 template <int NQ, int MODE, bool PAIR = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
-    NQ == 1 && MODE != kEmitSample && MODE != kEmitScoresMax && !PAIR ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
+    NQ == 1 && MODE == kEmitFilter && !PAIR ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
   __shared__ Shared<NQ> sh;
   __shared__ uint16_t awB[PAIR ? kWaves : 1][kMaxD][kWB];  // tile B's scale buffers
   const int tid = threadIdx.x, lane = tid & 63;
