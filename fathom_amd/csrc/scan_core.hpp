@@ -819,7 +819,7 @@ __device__ __forceinline__ void tile_pass(Tile<NQ, 1> &t, const ScanArgs &a, con
     set_priority_by_tiles_left((nlist - 1 - L) / Ls);
     scan_tile<NQ, 1, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
     if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax)
-      emit_scores<NQ, MODE == kEmitScoresMax, NQ == 1>(em, t, sh, a, bh, beta0, lane, aw);
+      emit_scores<NQ, MODE == kEmitScoresMax, NQ == 1 || MODE == kEmitScores>(em, t, sh, a, bh, beta0, lane, aw);
     if constexpr (MODE == kEmitFilter) emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, FB, skipm, tot);
     wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
   }
