@@ -1,0 +1,95 @@
+"""End-to-end index-set parity at full size: the fused scan + top-k on the GPU
+against the oracle's own selection from float64 scores of every token
+(quantise_u4 + scan_planes on the CPU), the way the reference checks its
+kernels at the real shape (scripts/B_e2e_offload_v2.py:184-202) and compares
+top-k sets (scripts/topk_bench.py:9-16).  Differences are allowed only at the
+selection boundary, within twice the row's measured score error (criterion in
+tests/fullsize_oracle.py).
+
+Cases: config 2; config 3 (n = 2^20) from HBM and from mapped host memory in
+64-block superblocks (the paired-tile first pass of the host-resident
+regime); config 4 at budgets 40, 48 and 80 bits; config 5 at its first and
+last layer.
+"""
+import numpy as np
+import pytest
+import torch
+
+from fathom_amd import bitplane as bp
+from fathom_amd import offload as off
+from fathom_amd import workloads as W
+from fullsize_oracle import check_rows
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+CASES = [(2, 0, None), (4, 0, 40.0), (4, 0, 48.0), (4, 0, 80.0), (5, 0, None), (5, 35, None)]
+
+
+@pytest.mark.parametrize("cfg,layer,budget", CASES,
+                         ids=[f"c{c}-layer{l}-b{b}" for c, l, b in CASES])
+def test_fused_sets_vs_float64_oracle(cfg, layer, budget):
+    print(f"[e2e] config {cfg} layer {layer} budget {budget}", flush=True)
+    x = W.config_inputs(cfg, device=DEV, layer=layer)
+    if budget is not None:
+        x["budget"] = budget
+    st = bp.PlaneStore(x["K"], keep_code=False)
+    plan = bp.make_plan(x["g"], x["budget"])
+    idx = st.scan_topk(x["q"], plan, x["k"], x["sink"], x["local"])
+    scores = st.scan(x["q"], plan)
+    torch.cuda.synchronize()
+    del st
+    nd = check_rows(x["K"], x["q"], plan["t"], idx, scores, x["k"], x["sink"], x["local"], label=f"c{cfg}")
+    # the boundary differences are rare: far below one per selected list
+    assert nd <= x["BH"] * x["G"], nd
+
+
+@pytest.fixture(scope="module")
+def c3():
+    print("[e2e] config 3: building the 2^20-token store", flush=True)
+    x = W.config_inputs(3, device=DEV)
+    st = bp.PlaneStore(x["K"], keep_code=False)
+    plan = bp.make_plan(x["g"], x["budget"])
+    idx = st.scan_topk(x["q"], plan, x["k"], x["sink"], x["local"])
+    torch.cuda.synchronize()
+    yield {"x": x, "st": st, "plan": plan, "idx": idx}
+    del st
+    torch.cuda.empty_cache()
+
+
+def test_c3_fused_sets_vs_float64_oracle(c3):
+    x, st, plan, idx = c3["x"], c3["st"], c3["plan"], c3["idx"]
+    scores = st.scan(x["q"], plan)
+    torch.cuda.synchronize()
+    nd = check_rows(x["K"], x["q"], plan["t"], idx, scores, x["k"], x["sink"], x["local"], label="c3")
+    assert nd <= x["BH"] * x["G"], nd
+
+
+def test_c3_host_paired_tiles_equal_hbm(c3):
+    """The host-resident regime's first pass (two wave-tiles per 256-byte load,
+    64-block superblocks in mapped pinned memory) at full size selects the
+    HBM path's indices bit for bit."""
+    print("[e2e] config 3: 64-block superblocks in mapped host memory", flush=True)
+    x, plan = c3["x"], c3["plan"]
+    bp.SUB = 64
+    try:
+        hsrc = bp.PlaneStore(x["K"], keep_code=False)
+    finally:
+        bp.SUB = 16
+    assert hsrc.sub == 64
+    hps = []
+    try:
+        _, pl_dev, h = off.host_mapped(hsrc.planes_k)
+        hps.append(h)
+        _, sc_dev, h = off.host_mapped(hsrc.scales_k)
+        hps.append(h)
+        hst = bp.PlaneStore.__new__(bp.PlaneStore)
+        hst.BH, hst.n, hst.nsb, hst.sub = hsrc.BH, hsrc.n, hsrc.nsb, hsrc.sub
+        hst.planes32, hst.scales_k = pl_dev, sc_dev
+        del hsrc
+        got = hst.scan_topk(x["q"], plan, x["k"], x["sink"], x["local"])
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), c3["idx"].cpu().numpy())
+    finally:
+        for h in hps:
+            off.free_host(h)
