@@ -27,7 +27,7 @@ PROTOTYPES = {
     "fathom_make_plan": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "fathom_make_plan_uniform": (_i32, [_vp, ctypes.c_float, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                         _vp, _vp]),
-    "fathom_scan_planes": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+    "fathom_scan_planes": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp, _vp]),
     "fathom_pack_chan4": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "fathom_quantise_chan4": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _vp]),
@@ -35,11 +35,11 @@ PROTOTYPES = {
     "fathom_scan_chan4": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "fathom_klt_query": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "fathom_scan_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
-    "fathom_scan_topk": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+    "fathom_scan_topk": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _vp, _vp, _sz, _vp]),
-    "fathom_scan_topk_stages": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+    "fathom_scan_topk_stages": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _i64, _vp, _vp, _sz, _i32, _vp]),
-    "fathom_scan_topk_noalloc": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+    "fathom_scan_topk_noalloc": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                         _i64, _i64, _vp, _vp]),
     "fathom_topk_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "fathom_sink_local_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),

@@ -208,12 +208,23 @@ def make_plan(g, budget, bmax=4, iters=30):
     cls = torch.empty(BH, bmax, d, dtype=torch.int32, device=dev)
     clsn = torch.empty(BH, bmax, dtype=torch.int32, device=dev)
     outs = (_ptr(t), _ptr(pairs), _ptr(npairs), _ptr(act), _ptr(nact), _ptr(cls), _ptr(clsn), _stream(dev))
+    # a host-side bound on sum(t) (the bisection keeps it within the budget),
+    # known without a device sync for float budgets and host tensors; the scan
+    # uses it only to pick its register layout
+    units_max = 0
     if torch.is_tensor(budget):
+        if budget.device.type == "cpu" and budget.numel() > 0:
+            bmx = float(budget.float().max())
+            units_max = int(math.floor(bmx)) if math.isfinite(bmx) else 0
         budget = budget.to(device=dev, dtype=torch.float32).expand(BH).contiguous()
         _lib.call("fathom_make_plan", _ptr(gf), _ptr(budget), BH, d, int(bmax), int(iters), *outs)
     else:  # one float for every row: a kernel argument
-        _lib.call("fathom_make_plan_uniform", _ptr(gf), float(budget), BH, d, int(bmax), int(iters), *outs)
-    return {"t": t, "pairs": pairs, "npairs": npairs, "act": act, "nact": nact, "cls": cls, "clsn": clsn}
+        bf = float(budget)
+        units_max = int(math.floor(bf)) if math.isfinite(bf) else 0
+        _lib.call("fathom_make_plan_uniform", _ptr(gf), bf, BH, d, int(bmax), int(iters), *outs)
+    units_max = max(0, min(units_max, int(bmax) * d)) if units_max > 0 else 0
+    return {"t": t, "pairs": pairs, "npairs": npairs, "act": act, "nact": nact, "cls": cls, "clsn": clsn,
+            "units_max": units_max}
 
 
 def make_plan_torch(g, budget, bmax=4, iters=30):
@@ -223,6 +234,11 @@ def make_plan_torch(g, budget, bmax=4, iters=30):
 
 
 # ----------------------------------------------------------------------------- store + scan
+def _units_max(plan):
+    """The plan's host-side bound on sum(t) per row (0: unknown)."""
+    return int(plan.get("units_max", 0)) if isinstance(plan, dict) else 0
+
+
 def _plan_classes(plan, BH, d):
     """The plan's depth-class lists as the scan kernels read them: cls int32
     [BH, bmax, D] and clsn int32 [BH, bmax], contiguous, on the GPU."""
@@ -286,7 +302,7 @@ class PlaneStore:
         sub = int(getattr(self, "sub", SUB))
         qc = q.contiguous().float()
         cls, clsn = _plan_classes(plan, BH, d)
-        _lib.call("fathom_scan_planes", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1],
+        _lib.call("fathom_scan_planes", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1], _units_max(plan),
                   ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), self.n,
                   int(self.nsb), sub, b0, b1, _ptr(out), _stream(q.device))
         return out
@@ -310,7 +326,7 @@ class PlaneStore:
         nbytes = L.fathom_scan_topk_workspace_bytes(BH, G, n, int(k), int(sink), int(local))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         cls, clsn = _plan_classes(plan, BH, d)
-        _lib.call("fathom_scan_topk", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1],
+        _lib.call("fathom_scan_topk", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1], _units_max(plan),
                   ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), n,
                   int(self.nsb), sub, m, int(k), int(sink), int(local), _ptr(idx), _ptr(ws), nbytes,
                   _stream(q.device))
@@ -336,7 +352,7 @@ class PlaneStore:
         if ws.numel() < nbytes:
             raise ValueError(f"workspace of {ws.numel()} bytes, need {nbytes}")
         cls, clsn = _plan_classes(plan, BH, d)
-        _lib.call("fathom_scan_topk_stages", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1],
+        _lib.call("fathom_scan_topk_stages", _ptr(qc), BH, G, d, _ptr(cls), _ptr(clsn), cls.shape[1], _units_max(plan),
                   ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), n,
                   int(self.nsb), sub, m, int(k), int(sink), int(local), _ptr(idx), _ptr(ws), nbytes, int(stages),
                   _stream(q.device))

@@ -60,14 +60,18 @@ int scratch_on_current_device(void **out) {
 using namespace fathom;
 
 extern "C" int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
-                                        const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
-                                        int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink,
-                                        int64_t local, int64_t *idx, void *stream) {
+                                        const int32_t *clsn, int bmax, int64_t units_max, const void *planes_sb,
+                                        const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m,
+                                        int64_t k, int64_t sink, int64_t local, int64_t *idx, void *stream) {
   // the fused path's own shape limits, checked first so that the size below cannot overflow
   if (BH < 1 || BH > 65535 || G < 1 || G > 8)
     return fail(FATHOM_ERR_INVALID, "scan_topk_noalloc: BH=%lld G=%lld rejected", (long long)BH, (long long)G);
   int rc = check_topk_args(BH * G, n, m, k, sink, local, "scan_topk_noalloc");
   if (rc) return rc;
+  // k == sink + local: only the fixed positions are written, with no workspace
+  if (k - sink - local == 0)
+    return scan_topk_run(q, BH, G, D, cls, clsn, bmax, units_max, planes_sb, scales_sb, n, nsb, sub, m, k, sink,
+                         local, idx, nullptr, 0, FATHOM_STAGE_ALL, stream);
   const size_t need = scan_topk_ws(BH * G, n, k);
   if (need > kScratchBytes)
     return fail(FATHOM_ERR_WORKSPACE,
@@ -77,6 +81,6 @@ extern "C" int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, i
   void *ws = nullptr;
   rc = scratch_on_current_device(&ws);
   if (rc) return rc;
-  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx, ws,
-                       kScratchBytes, FATHOM_STAGE_ALL, stream);
+  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, units_max, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local,
+                       idx, ws, kScratchBytes, FATHOM_STAGE_ALL, stream);
 }

@@ -12,115 +12,62 @@ using namespace sc;
 // Grid (workgroups, BH); the waves of the grid's row take the list entries L
 // in a grid-stride loop.  Nothing waits on another wave: a candidate pass
 // that found fewer than kk candidates for a row is completed by the row's
-// finalize workgroup (launch_finalize_fused).
-// PAIR (stores in mapped host memory, sub a multiple of 32): the first pass
-// scans pairs of adjacent wave-tiles with 256-byte loads (scan_tile_pair).
-// Registers: four waves per SIMD for the candidate pass (its few stores), two
-// where the scores go out through LDS (score modes) or pairs of tiles are held.
-template <int NQ, int MODE, bool PAIR = false>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
-    NQ == 1 && MODE == kEmitFilter && !PAIR ? 4 : 2))) void scan_wave_kernel(ScanArgs a, Emit em) {
-  __shared__ Shared<NQ> sh;
-  __shared__ uint16_t awB[PAIR ? kWaves : 1][kMaxD][kWB];  // tile B's scale buffers
+// finalize workgroup (launch_finalize_fused).  The sample pass gives each of
+// its tiles four waves, one quarter of every block each.
+// ACC (1 or 4): step groups whose accumulators a plan of more than 64 units
+// keeps over its register groups (4: fewer reloads, more registers; the
+// scores are the same either way).
+template <int MODE, int ACC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ACC == 1 ? 3 : 2))) void scan_wave_kernel(
+    ScanArgs a, Emit em) {
+  __shared__ Shared sh;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
-  int nact = 0;
-  const int U = plan_tables<NQ>(sh, a, bh, nact);
-  uint16_t(*aw)[kWB] = sh.a[wave];
+  plan_tables(sh, a, bh);
   if constexpr (MODE == kEmitSample) {
-    // the sample pass is latency-bound (a few tiles per row): the four waves
-    // of a workgroup share each tile, one token-step class each
-    Tile<NQ, 4> t;
-    t.r0 = wave;
-    for (int64_t L = blockIdx.x; L < a.nwt; L += gridDim.x) {
-      const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
-      if (beta0 >= a.blk_end) continue;  // uniform per workgroup
-      scan_tile<NQ, 4, kChunk>(t, a, sh, aw, bh, beta0, U, nact, lane);
-      emit_sample(em, t, sh, a, bh, beta0, L, lane);
-      wave_lds_sync();  // the wave's scale buffer is rewritten by its next tile
-    }
+    // the sample pass is latency-bound (a few tiles per row): four waves per
+    // tile, one quarter each; two tiles per workgroup
+    const int qs = wave & 3;
+    tile_pass<kEmitSample, ACC, false>(a, em, sh, bh, lane, (int64_t)blockIdx.x * 2 + (wave >> 2),
+                                       (int64_t)gridDim.x * 2, a.nwt, qs, qs + 1, 0u);
   } else {
-    Tile<NQ, 1> t;
-    t.r0 = 0;
     // the candidate pass also writes the (zero) counts of the padding regions past the row
     constexpr bool kCand = MODE == kEmitFilter;
     const int64_t nlist = kCand && em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
     const int64_t L0 = (int64_t)blockIdx.x * kWaves + wave, Ls = (int64_t)gridDim.x * kWaves;
-    uint32_t tot[4 * NQ];
-#pragma unroll
-    for (int h = 0; h < 4 * NQ; ++h) tot[h] = 0u;
-    if constexpr (PAIR) {
-      // pairs of tiles (2 P, 2 P + 1); then the padding regions' zero counts
-      const int64_t npair = (a.nwt + 1) / 2;
-      for (int64_t P = L0; P < npair; P += Ls) {
-        const int64_t LA = 2 * P, LB = LA + 1;
-        const int64_t beta0 = (a.wt0 + LA) * kWB;
-        if (beta0 >= a.blk_end || beta0 + 2 * kWB <= a.blk0) continue;  // uniform per wave
-        set_priority_by_tiles_left((npair - 1 - P) / Ls);
-        Tile<NQ, 1> tB;
-        tB.r0 = 0;
-        scan_tile_pair<NQ, kChunk>(t, tB, a, sh, aw, awB[wave], bh, beta0, U, nact, lane);
-        if constexpr (MODE == kEmitScores || MODE == kEmitScoresMax) {
-          emit_scores<NQ, MODE == kEmitScoresMax>(em, t, sh, a, bh, beta0, lane);
-          if (LB < a.nwt) emit_scores<NQ, MODE == kEmitScoresMax>(em, tB, sh, a, bh, beta0 + kWB, lane);
-        }
-        if constexpr (MODE == kEmitFilter) {
-          emit_filter<NQ>(em, t, sh, a, bh, beta0, lane, false, 0u, tot);
-          if (LB < a.nwt) emit_filter<NQ>(em, tB, sh, a, bh, beta0 + kWB, lane, false, 0u, tot);
-        }
-        wave_lds_sync();  // the wave's scale buffers are rewritten by its next pair
-      }
-      if constexpr (kCand)
-        for (int64_t L = a.nwt + L0; L < nlist; L += Ls)
-          if (lane < a.G) em.sel.rc1[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
-    } else {
-      tile_pass<NQ, MODE, false>(t, a, em, sh, aw, bh, U, nact, lane, L0, Ls, nlist, 0u, tot);
-    }
+    tile_pass<MODE, ACC, false>(a, em, sh, bh, lane, L0, Ls, nlist, 0, kQS, 0u);
   }
 }
 
 // --------------------------------------------------------------------- launch
 constexpr int64_t kTargetWaves = 4096;  // waves of a full launch (4 per SIMD on 256 CUs)
 
-template <int MODE, bool PAIR = false>
-int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, hipStream_t st) {
+template <int MODE>
+int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int64_t units_max, hipStream_t st) {
   if (nwt <= 0) return FATHOM_OK;
   ScanArgs a = a0;
   a.nwt = nwt;
-  int64_t wgs = cdiv(nwt, kWaves);
+  int64_t wgs;
   if (MODE == kEmitSample) {
-    wgs = nwt;  // one tile per workgroup
-  } else if (PAIR) {
-    // pairs of tiles; two waves per SIMD fill the chip (the pair variant's registers)
-    const int64_t npair = (nwt + 1) / 2, per = cdiv(npair * BH, kTargetWaves / 2);
-    wgs = cdiv(cdiv(npair, per), kWaves);
+    wgs = cdiv(nwt, 2);  // four waves per tile
   } else {
     // enough waves to fill the chip, each taking a whole number of tiles
     const int64_t per = cdiv(nwt * BH, kTargetWaves);
     wgs = cdiv(cdiv(nwt, per), kWaves);
   }
   const dim3 grid((unsigned)wgs, (unsigned)BH);
-  if constexpr (PAIR)
-    scan_wave_kernel<1, MODE, true><<<grid, kThreads, 0, st>>>(a, em);  // G <= 4 (pair_scan)
-  else if (a.G <= 4)
-    scan_wave_kernel<1, MODE><<<grid, kThreads, 0, st>>>(a, em);
+  if (units_max > kGU)
+    scan_wave_kernel<MODE, 4><<<grid, kThreads, 0, st>>>(a, em);
   else
-    scan_wave_kernel<2, MODE><<<grid, kThreads, 0, st>>>(a, em);
+    scan_wave_kernel<MODE, 1><<<grid, kThreads, 0, st>>>(a, em);
   return launch_status("scan_wave_kernel");
 }
 
-// Planes in mapped host memory (read zero-copy over PCIe) in superblocks of a
-// multiple of 32 blocks: the paired-tile first pass applies.
-bool pair_scan(const ScanArgs &a) {
-  // one query-row tile: two row tiles of the pair would spill
-  if (a.G > 4 || a.sub % (2 * kWB) != 0 || a.wt0 != 0 || a.wt_stride != 1) return false;
-  hipPointerAttribute_t attr;
-  if (hipPointerGetAttributes(&attr, a.planes) != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  return attr.type == hipMemoryTypeHost;
+// The plan's units bound: the caller's, else every channel at full depth.
+int64_t units_bound(int64_t units_max, int64_t D, int bmax) {
+  const int64_t full = D * (bmax < 4 ? bmax : 4);
+  return units_max > 0 && units_max < full ? units_max : full;
 }
 
 int check_scan(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
@@ -169,7 +116,8 @@ ScanArgs make_args(const float *q, int64_t G, int64_t D, const int32_t *cls, con
 using namespace fathom;
 
 extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
-                                  const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
+                                  const int32_t *clsn, int bmax, int64_t units_max, const void *planes_sb,
+                                  const void *scales_sb,
                                   int64_t n, int64_t nsb, int64_t sub, int64_t blk0, int64_t blk1, float *out,
                                   void *stream) {
   int rc = check_scan(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, "scan_planes");
@@ -186,8 +134,8 @@ extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t
   a.wt0 = blk0 / kWB;
   Emit em{};
   em.out = out;
-  if (pair_scan(a)) return launch_scan<kEmitScores, true>(a, cdiv(blk_end, kWB) - a.wt0, BH, em, (hipStream_t)stream);
-  return launch_scan<kEmitScores>(a, cdiv(blk_end, kWB) - a.wt0, BH, em, (hipStream_t)stream);
+  return launch_scan<kEmitScores>(a, cdiv(blk_end, kWB) - a.wt0, BH, em, units_bound(units_max, D, bmax),
+                                  (hipStream_t)stream);
 }
 
 namespace fathom {
@@ -209,7 +157,7 @@ extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_
 
 namespace fathom {
 int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
-                  const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m,
+                  int64_t units_max, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m,
                   int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes,
                   int stages, void *stream) {
   int rc = check_scan(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, "scan_topk");
@@ -231,6 +179,7 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   a.blk_end = nblk;
   a.wt0 = 0;
   const int64_t nwt = cdiv(nblk, kWB);
+  const int64_t um = units_bound(units_max, D, bmax);
   if (n <= kRowSelectMax) {
     // short rows: the scores and their 16-token group maxima in the workspace
     // (the candidate stage), then the rows selected in one launch from the
@@ -241,8 +190,7 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
     es.sink = sink;
     es.lstart = (m - local) > 0 ? (m - local) : 0;
     if (stages & FATHOM_STAGE_CANDIDATES) {
-      rc = pair_scan(a) ? launch_scan<kEmitScoresMax, true>(a, nwt, BH, es, st)
-                        : launch_scan<kEmitScoresMax>(a, nwt, BH, es, st);
+      rc = launch_scan<kEmitScoresMax>(a, nwt, BH, es, um, st);
       if (rc) return rc;
     }
     return (stages & FATHOM_STAGE_FINALIZE) ? launch_rowselect_gmax(es.out, es.gmax, rows, n, m, k, sink, local, idx, st)
@@ -257,7 +205,7 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   em.lstart = (m - local) > 0 ? (m - local) : 0;
   if (stages & FATHOM_STAGE_SAMPLE) {
     a.wt_stride = S;
-    rc = launch_scan<kEmitSample>(a, topk_sample_tiles(n, S, kRegTok), BH, em, st);
+    rc = launch_scan<kEmitSample>(a, topk_sample_tiles(n, S, kRegTok), BH, em, um, st);
     if (rc) return rc;
   }
   if (stages & FATHOM_STAGE_SELECT) {
@@ -266,30 +214,31 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   }
   if (stages & FATHOM_STAGE_CANDIDATES) {
     a.wt_stride = 1;
-    rc = pair_scan(a) ? launch_scan<kEmitFilter, true>(a, nwt, BH, em, st) : launch_scan<kEmitFilter>(a, nwt, BH, em, st);
+    rc = launch_scan<kEmitFilter>(a, nwt, BH, em, um, st);
     if (rc) return rc;
   }
   // T_hi may exceed a row's kk-th largest key (r_hi < kk): the finalize
   // workgroup of a row with fewer than kk candidates rescans it with T_lo
   a.wt_stride = 1;
   a.nwt = nwt;
-  return (stages & FATHOM_STAGE_FINALIZE) ? launch_finalize_fused(a, em, rows, m, k, sink, local, idx, st) : FATHOM_OK;
+  return (stages & FATHOM_STAGE_FINALIZE) ? launch_finalize_fused(a, em, rows, m, k, sink, local, idx, st)
+                                          : FATHOM_OK;
 }
 }  // namespace fathom
 
 extern "C" int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
-                                const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
+                                const int32_t *clsn, int bmax, int64_t units_max, const void *planes_sb, const void *scales_sb,
                                 int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink,
                                 int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes, void *stream) {
-  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx,
+  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, units_max, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx,
                        workspace, workspace_bytes, FATHOM_STAGE_ALL, stream);
 }
 
 extern "C" int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
-                                       const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb,
+                                       const int32_t *clsn, int bmax, int64_t units_max, const void *planes_sb, const void *scales_sb,
                                        int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink,
                                        int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes,
                                        int stages, void *stream) {
-  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx,
+  return scan_topk_run(q, BH, G, D, cls, clsn, bmax, units_max, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx,
                        workspace, workspace_bytes, stages, stream);
 }

@@ -9,7 +9,7 @@ size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k);
 
 // The fused scan + top-k (stages: FATHOM_STAGE_* mask) on a caller-provided workspace.
 int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
-                  const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m,
+                  int64_t units_max, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m,
                   int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes,
                   int stages, void *stream);
 

@@ -679,25 +679,17 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
 // The fallback of the fused scan + top-k, run by the finalize workgroup of a
 // row whose candidate pass found fewer than kk candidates: the row (head h of
 // bh) is rescanned with T_lo into the regions under the second count array by
-// the workgroup's first four waves, with the scan's plan tables in tsh (LDS
-// that the caller frees for it).  The rescan computes the scores of the
-// candidate pass bit for bit (the same tile arithmetic).
-template <int NQ>
+// the workgroup's first waves, with the scan's plan tables in tsh (LDS that the
+// caller frees for it).  The rescan computes the scores of the candidate pass
+// bit for bit (the same chain of matrix instructions per token).
 __device__ __forceinline__ void rescan_row(const sc::ScanArgs &a, const sc::Emit &em, int64_t bh, int h,
-                                           sc::Shared<NQ> &tsh) {
-  int nact = 0;
-  const int U = sc::plan_tables<NQ>(tsh, a, bh, nact);
+                                           sc::Shared &tsh) {
+  sc::plan_tables(tsh, a, bh);
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (wave < sc::kWaves) {
-    sc::Tile<NQ, 1> t;
-    t.r0 = 0;
-    uint32_t tot[4 * NQ];
-#pragma unroll
-    for (int g = 0; g < 4 * NQ; ++g) tot[g] = 0u;
     const int64_t nlist = em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
     const uint32_t skipm = ((1u << a.G) - 1u) & ~(1u << h);
-    sc::tile_pass<NQ, sc::kEmitFilter, true>(t, a, em, tsh, tsh.a[wave], bh, U, nact, lane, wave, sc::kWaves, nlist,
-                                             skipm, tot);
+    sc::tile_pass<sc::kEmitFilter, 1, true>(a, em, tsh, bh, lane, wave, sc::kWaves, nlist, 0, sc::kQS, skipm);
     __builtin_amdgcn_s_setprio(0);
   }
   // the rescan's region counts and candidates are read back by other waves of
@@ -711,7 +703,6 @@ __device__ __forceinline__ void rescan_row(const sc::ScanArgs &a, const sc::Emit
 // (row = bh * G + h), copied to LDS while they are counted; a row with more
 // than kCandLds candidates is selected from its regions in place.  A row with
 // fewer than kk first-pass candidates is rescanned first (rescan_row).
-template <int NQ>
 __global__ __launch_bounds__(kFinThreads) void finalize_fused_kernel(int64_t m, int64_t k, int64_t sink, int64_t local,
                                                                      sc::ScanArgs a, sc::Emit em,
                                                                      int64_t *__restrict__ idx) {
@@ -719,7 +710,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_fused_kernel(int64_t m, 
   __shared__ uint64_t ss[kMaxK];
   __shared__ RangeShared sh;
   __shared__ uint32_t s_cnt;
-  static_assert(sizeof(sc::Shared<NQ>) <= sizeof(cl), "the rescan's plan tables fit the candidate buffer");
+  static_assert(sizeof(sc::Shared) <= sizeof(cl), "the rescan's plan tables fit the candidate buffer");
   const TopkSel &s = em.sel;
   const int64_t row = blockIdx.x;
   const int64_t kk = k - sink - local;
@@ -730,7 +721,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_fused_kernel(int64_t m, 
   uint32_t cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
   if (cnt < s.kk) {  // uniform
     __syncthreads();  // cl holds the plan tables from here
-    rescan_row<NQ>(a, em, row / a.G, (int)(row % a.G), *reinterpret_cast<sc::Shared<NQ> *>(cl));
+    rescan_row(a, em, row / a.G, (int)(row % a.G), *reinterpret_cast<sc::Shared *>(cl));
     src.rc = s.rc2 + row * s.nreg;
     cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
   }
@@ -1272,10 +1263,7 @@ int launch_finalize(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t lo
 
 int launch_finalize_fused(const sc::ScanArgs &a, const sc::Emit &em, int64_t rows, int64_t m, int64_t k, int64_t sink,
                           int64_t local, int64_t *idx, hipStream_t st) {
-  if (a.G <= 4)
-    finalize_fused_kernel<1><<<(unsigned)rows, kFinThreads, 0, st>>>(m, k, sink, local, a, em, idx);
-  else
-    finalize_fused_kernel<2><<<(unsigned)rows, kFinThreads, 0, st>>>(m, k, sink, local, a, em, idx);
+  finalize_fused_kernel<<<(unsigned)rows, kFinThreads, 0, st>>>(m, k, sink, local, a, em, idx);
   return launch_status("finalize_fused_kernel");
 }
 

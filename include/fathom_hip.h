@@ -115,12 +115,17 @@ int fathom_make_plan_uniform(const float *g, float budget, int64_t BH, int64_t D
  *   q         [BH, G, D] float32, 1 <= G <= 8, D <= 128 (the reference's D = 128,
  *             kernels/bitplane.py:313)
  *   cls, clsn from fathom_make_plan ([BH, bmax, D] and [BH, bmax] int32)
+ *   units_max an upper bound on the plan's (channel, plane) units of every row,
+ *             sum_j t_j (make_plan keeps it within the bit budget), or 0 when
+ *             none is known.  It only picks the kernel's register layout
+ *             (plans above 64 units keep more accumulators live); results are
+ *             the same for any value, a wrong bound included.
  *   planes_sb [BH, nsb, D, 4, sub] uint64, scales_sb [BH, nsb, D, sub] fp16
  *             (HBM, or mapped pinned host memory: the scan then reads over PCIe)
  *   out       [BH, G, n] float32
  */
 int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn,
-                       int bmax, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
+                       int bmax, int64_t units_max, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
                        int64_t blk0, int64_t blk1, float *out, void *stream);
 
 /*
@@ -172,7 +177,7 @@ int fathom_klt_query(const float *q, const float *Vt, const float *lam, int64_t 
  */
 size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t n, int64_t k, int64_t sink, int64_t local);
 int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn,
-                     int bmax, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
+                     int bmax, int64_t units_max, const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub,
                      int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace,
                      size_t workspace_bytes, void *stream);
 
@@ -193,7 +198,7 @@ int fathom_scan_topk(const float *q, int64_t BH, int64_t G, int64_t D, const int
 #define FATHOM_STAGE_FINALIZE 8
 #define FATHOM_STAGE_ALL 15
 int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
-                            const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb, int64_t n,
+                            const int32_t *clsn, int bmax, int64_t units_max, const void *planes_sb, const void *scales_sb, int64_t n,
                             int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
                             int64_t *idx, void *workspace, size_t workspace_bytes, int stages, void *stream);
 
@@ -211,7 +216,7 @@ int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, co
  */
 #define FATHOM_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,
-                             const int32_t *clsn, int bmax, const void *planes_sb, const void *scales_sb, int64_t n,
+                             const int32_t *clsn, int bmax, int64_t units_max, const void *planes_sb, const void *scales_sb, int64_t n,
                              int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
                              int64_t *idx, void *stream);
 

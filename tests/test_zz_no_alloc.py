@@ -30,7 +30,8 @@ def _noalloc(st, plan, q, k, sink, local, m, idx):
     BH, G, d = q.shape
     cls, clsn = bp._plan_classes(plan, BH, d)
     rc = _lib.lib().fathom_scan_topk_noalloc(
-        bp._ptr(q), BH, G, d, bp._ptr(cls), bp._ptr(clsn), cls.shape[1], ctypes.c_void_p(st.planes32.data_ptr()),
+        bp._ptr(q), BH, G, d, bp._ptr(cls), bp._ptr(clsn), cls.shape[1], bp._units_max(plan),
+        ctypes.c_void_p(st.planes32.data_ptr()),
         ctypes.c_void_p(st.scales_k.data_ptr()), st.n, int(st.nsb), int(getattr(st, "sub", bp.SUB)), m, k, sink, local, bp._ptr(idx),
         bp._stream(q.device))
     _lib.check(rc, "fathom_scan_topk_noalloc")
@@ -88,15 +89,59 @@ def test_noalloc_fallback_rescan():
     torch.testing.assert_close(idx, ref, rtol=0, atol=0)
 
 
+def test_noalloc_fixed_positions_only_on_long_rows():
+    """k == sink + local needs no workspace: accepted even where the selection's
+    workspace would not fit the static array (rows of 2^20 tokens)."""
+    print("[noalloc] k == sink + local at n = 2^20", flush=True)
+    BH, G, n = 8, 4, 1 << 20
+    assert _lib.lib().fathom_scan_topk_workspace_bytes(BH, G, n, 36, 4, 32) > SCRATCH
+    st, plan, q = _case(BH, G, n, seed=5)
+    ref = st.scan_topk(q, plan, 36, 4, 32)
+    idx = torch.full_like(ref, -1)
+    _noalloc(st, plan, q, 36, 4, 32, n, idx)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(idx, ref, rtol=0, atol=0)
+
+
+def test_noalloc_graph_replays_equal_eager():
+    """One eager call (the array's address is looked up on a device's first
+    call), then the call captured in a HIP graph and replayed with eager work
+    and synchronisations between replays: every replay equals the workspace
+    entry point."""
+    print("[noalloc] graph capture", flush=True)
+    st, plan, q = _case(2, 4, 100_000, seed=9)
+    ref = st.scan_topk(q, plan, 512, 4, 32)
+    idx = torch.full_like(ref, -1)
+    _noalloc(st, plan, q, 512, 4, 32, st.n, idx)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(idx, ref, rtol=0, atol=0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            _noalloc(st, plan, q, 512, 4, 32, st.n, idx)
+    torch.cuda.current_stream().wait_stream(s)
+    for r in range(3):
+        idx.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(idx, ref, rtol=0, atol=0)
+        other = st.scan_topk(q, plan, 256, 4, 32)  # eager work between replays
+        torch.cuda.synchronize()
+        assert other.shape[-1] == 256
+
+
 def test_noalloc_refuses_shapes_past_the_array():
     L = _lib.lib()
     need = L.fathom_scan_topk_workspace_bytes(8, 4, 1 << 20, 512, 4, 32)
     assert need > SCRATCH
     null = ctypes.c_void_p(0)
-    rc = L.fathom_scan_topk_noalloc(null, 8, 4, 128, null, null, 4, null, null, 1 << 20, (1 << 20) // 1024, 16,
+    rc = L.fathom_scan_topk_noalloc(null, 8, 4, 128, null, null, 4, 0, null, null, 1 << 20, (1 << 20) // 1024, 16,
                                     1 << 20, 512, 4, 32, null, null)
     assert rc == _lib.ERR_WORKSPACE
     assert b"static array holds" in L.fathom_last_error()
-    rc = L.fathom_scan_topk_noalloc(null, 8, 9, 128, null, null, 4, null, null, 4096, 4, 16, 4096, 64, 4, 32, null,
+    rc = L.fathom_scan_topk_noalloc(null, 8, 9, 128, null, null, 4, 0, null, null, 4096, 4, 16, 4096, 64, 4, 32, null,
                                     null)
     assert rc == _lib.ERR_INVALID
