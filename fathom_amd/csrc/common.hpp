@@ -57,10 +57,9 @@ __device__ __forceinline__ float load_elem<FATHOM_DT_BF16>(const void *p, int64_
 // Orderable key of a score: unsigned order == torch.topk value order
 // (NaN above +inf, -0.0 equal to +0.0).
 __device__ __forceinline__ uint32_t score_key(float s) {
-  if (s != s) return 0xFFFFFFFFu;
-  if (s == 0.0f) s = 0.0f;
-  uint32_t u = __float_as_uint(s);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  const uint32_t u = __float_as_uint(s + 0.0f);  // -0.0 + 0.0 = +0.0
+  const uint32_t k = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);  // negative: ~u; else u | sign
+  return s != s ? 0xFFFFFFFFu : k;
 }
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;  // score_key(-inf)
 

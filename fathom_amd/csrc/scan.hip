@@ -14,29 +14,30 @@ using namespace sc;
 // that found fewer than kk candidates for a row is completed by the row's
 // finalize workgroup (launch_finalize_fused).  The sample pass gives each of
 // its tiles four waves, one quarter of every block each.
-// ACC (1 or 4): step groups whose accumulators a plan of more than 64 units
-// keeps over its register groups (4: fewer reloads, more registers; the
-// scores are the same either way).
-template <int MODE, int ACC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ACC == 1 ? 3 : 2))) void scan_wave_kernel(
-    ScanArgs a, Emit em) {
+// NSMAX (1..4): the plan slices (16 units each) held in registers; ACC (1 or
+// 4): step groups whose accumulators a larger plan keeps over its register
+// groups (4: fewer reloads, more registers).  The scores are the same for any
+// choice; the launch picks them from the plan's units bound.
+template <int MODE, int NSMAX, int ACC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
+    ACC == 4 ? 2 : 4))) void scan_wave_kernel(ScanArgs a, Emit em) {
   __shared__ Shared sh;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
-  plan_tables(sh, a, bh);
+  plan_tables(sh, a, bh, NSMAX * kSlice);
   if constexpr (MODE == kEmitSample) {
     // the sample pass is latency-bound (a few tiles per row): four waves per
-    // tile, one quarter each; two tiles per workgroup
-    const int qs = wave & 3;
-    tile_pass<kEmitSample, ACC, false>(a, em, sh, bh, lane, (int64_t)blockIdx.x * 2 + (wave >> 2),
-                                       (int64_t)gridDim.x * 2, a.nwt, qs, qs + 1, 0u);
+    // tile, one quarter each
+    static_assert(kWaves == kQS, "a wave per quarter of a sample tile");
+    tile_pass<kEmitSample, ACC, false, NSMAX>(a, em, sh, bh, lane, (int64_t)blockIdx.x, (int64_t)gridDim.x, a.nwt,
+                                              wave, wave + 1, 0u);
   } else {
     // the candidate pass also writes the (zero) counts of the padding regions past the row
     constexpr bool kCand = MODE == kEmitFilter;
     const int64_t nlist = kCand && em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
     const int64_t L0 = (int64_t)blockIdx.x * kWaves + wave, Ls = (int64_t)gridDim.x * kWaves;
-    tile_pass<MODE, ACC, false>(a, em, sh, bh, lane, L0, Ls, nlist, 0, kQS, 0u);
+    tile_pass<MODE, ACC, false, NSMAX>(a, em, sh, bh, lane, L0, Ls, nlist, 0, kQS, 0u);
   }
 }
 
@@ -50,17 +51,22 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int
   a.nwt = nwt;
   int64_t wgs;
   if (MODE == kEmitSample) {
-    wgs = cdiv(nwt, 2);  // four waves per tile
+    wgs = nwt;  // four waves per tile
   } else {
     // enough waves to fill the chip, each taking a whole number of tiles
     const int64_t per = cdiv(nwt * BH, kTargetWaves);
     wgs = cdiv(cdiv(nwt, per), kWaves);
   }
   const dim3 grid((unsigned)wgs, (unsigned)BH);
-  if (units_max > kGU)
-    scan_wave_kernel<MODE, 4><<<grid, kThreads, 0, st>>>(a, em);
+  const int64_t nsl = cdiv(units_max, kSlice);
+  if (nsl > kGS)
+    scan_wave_kernel<MODE, kGS, 4><<<grid, kThreads, 0, st>>>(a, em);
+  else if (nsl == 4)
+    scan_wave_kernel<MODE, 4, 1><<<grid, kThreads, 0, st>>>(a, em);
+  else if (nsl == 3)
+    scan_wave_kernel<MODE, 3, 1><<<grid, kThreads, 0, st>>>(a, em);
   else
-    scan_wave_kernel<MODE, 1><<<grid, kThreads, 0, st>>>(a, em);
+    scan_wave_kernel<MODE, 2, 1><<<grid, kThreads, 0, st>>>(a, em);
   return launch_status("scan_wave_kernel");
 }
 

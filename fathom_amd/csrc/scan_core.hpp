@@ -47,7 +47,7 @@ constexpr int kWB = 16;                // token blocks per wave-tile: one MFMA c
 constexpr int kWTok = kWB * kBlk;      // tokens per wave-tile
 constexpr int kQS = 4;                 // quarters of a block (16 tokens each)
 constexpr int kR = 16;                 // token steps per quarter
-constexpr int kWaves = 8;              // waves per workgroup
+constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxD = 128;             // the reference's head dimension (kernels/bitplane.py:313)
 constexpr int kMaxUnits = 4 * kMaxD;   // (channel, plane) units of a plan
@@ -121,11 +121,15 @@ __device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
 // (the class 1 channel list, then 2, 3, 4; a channel's planes consecutive),
 // padded to whole slices with units of zero weight and zero scale.
 struct Shared {
-  uint32_t uoff[kMaxUnits];              // unit -> plane word byte offset in a superblock ((4 j + p) sub 8)
-  uint32_t soff[kMaxUnits];              // unit -> scale byte offset in a superblock (j sub 2)
+  union {
+    struct {
+      uint32_t uoff[kMaxUnits];          // unit -> plane word byte offset in a superblock ((4 j + p) sub 8)
+      uint32_t soff[kMaxUnits];          // unit -> scale byte offset in a superblock (j sub 2)
+    };
+    float qs[kMaxG][kMaxD];              // the queries (prologue, before the offsets are written)
+  };
   _Float16 qa[kRows][kMaxUnits];         // score A rows: 2h = hi(q_hj 2^-(p + sigma_h)), 2h + 1 = lo
   _Float16 ca[kRows][kMaxUnits];         // C A rows: the split of q_hj 2^-sigma_h (2^-t_j - 1), first units only
-  float qs[kMaxG][kMaxD];                // the queries (prologue)
   uint16_t schan[kMaxD];                 // channel slot -> channel (prologue)
   int sig[kMaxG];                        // sigma_h: the exponent of the head's largest |q|
   int U;                                 // units, padded to whole slices
@@ -152,8 +156,10 @@ __device__ __forceinline__ void set_priority_by_tiles_left(int64_t left) {
 // f16 truncation (round toward zero) of x.
 __device__ __forceinline__ _Float16 f16_rtz(float x) { return __builtin_amdgcn_cvt_pkrtz(x, 0.0f)[0]; }
 
-// Workgroup prologue: the plan tables in LDS.  Returns the padded unit count.
-__device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_t bh) {
+// Workgroup prologue: the plan tables in LDS, with zero units from the plan's
+// last up to upad units (at least to a whole slice).  Returns the padded unit
+// count.
+__device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_t bh, int upad) {
   const int tid = threadIdx.x;
   int nc[4], SF[4], UE[4];
   int s = 0, u = 0;
@@ -168,19 +174,22 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
   }
   const int nact = s, ureal = u;
   const int U = (ureal + kSlice - 1) / kSlice * kSlice;
+  const int UP = min(max(U, upad), kMaxUnits);
   {
-    // one wave per head: its largest |q| gives sigma_h
+    // a wave per head (the waves take heads w, w + waves, ...): its largest
+    // |q| gives sigma_h
     const int w = tid >> 6, l = tid & 63;
-    static_assert(kWaves >= kMaxG && kMaxD == 2 * kWave, "a wave per head, two channels per lane");
-    if (w < kMaxG) {
-      const float q0 = (w < a.G && l < a.D) ? a.q[(bh * a.G + w) * a.D + l] : 0.0f;
-      const float q1 = (w < a.G && l + 64 < a.D) ? a.q[(bh * a.G + w) * a.D + l + 64] : 0.0f;
-      sh.qs[w][l] = q0;
-      sh.qs[w][l + 64] = q1;
+    const int nw = (int)blockDim.x >> 6;
+    static_assert(kMaxD == 2 * kWave, "two channels per lane");
+    for (int h = w; h < kMaxG; h += nw) {
+      const float q0 = (h < a.G && l < a.D) ? a.q[(bh * a.G + h) * a.D + l] : 0.0f;
+      const float q1 = (h < a.G && l + 64 < a.D) ? a.q[(bh * a.G + h) * a.D + l + 64] : 0.0f;
+      sh.qs[h][l] = q0;
+      sh.qs[h][l + 64] = q1;
       float m = fmaxf(fabsf(q0), fabsf(q1));
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      if (l == 0) sh.sig[w] = __builtin_amdgcn_frexp_expf(m);
+      if (l == 0) sh.sig[h] = __builtin_amdgcn_frexp_expf(m);
     }
   }
   for (int e = tid; e < nact; e += (int)blockDim.x) {
@@ -194,38 +203,48 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
     sh.ureal = ureal;
   }
   __syncthreads();
+  // the A rows: one (unit, head) pair per thread, 64 units of a head at a time
+  // (consecutive threads, consecutive units of one row: no bank conflicts)
+  for (int base = 0; base < ureal; base += 64) {
+    for (int it = tid; it < 64 * kMaxG; it += (int)blockDim.x) {
+      const int v = base + (it & 63), h = it >> 6;
+      if (v >= ureal) continue;
+      const int c = (v >= UE[0]) + (v >= UE[1]) + (v >= UE[2]);  // the unit's class: c + 1 planes
+      const int r = v - (c == 0 ? 0 : UE[c - 1]);
+      const int q = c == 0 ? r : c == 1 ? r >> 1 : c == 3 ? r >> 2 : (int)(((uint32_t)r * 0xAAABu) >> 17);  // r / (c + 1)
+      const int p = r - q * (c + 1);
+      const int j = sh.schan[(c == 0 ? 0 : SF[c - 1]) + q];
+      const bool on = h < a.G;
+      const float qv = on ? sh.qs[h][j] : 0.0f;
+      const int sg = on ? sh.sig[h] : 0;
+      const float Q = ldexpf(qv, -(p + sg));
+      const _Float16 qh = f16_rtz(Q);
+      sh.qa[2 * h][v] = qh;
+      sh.qa[2 * h + 1][v] = f16_rtz(Q - (float)qh);
+      const float cq = p == 0 ? ldexpf(qv * (ldexpf(1.0f, -(c + 1)) - 1.0f), -sg) : 0.0f;
+      const _Float16 ch = f16_rtz(cq);
+      sh.ca[2 * h][v] = ch;
+      sh.ca[2 * h + 1][v] = f16_rtz(cq - (float)ch);
+    }
+  }
+  // zero-weight, zero-scale padding units (they read plane word 0 of the superblock)
+  for (int v = ureal + tid; v < UP; v += (int)blockDim.x) {
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) sh.qa[r][v] = sh.ca[r][v] = (_Float16)0.0f;
+  }
+  __syncthreads();  // the queries are read: the offsets take their place
   const uint32_t sub = (uint32_t)a.sub;
   for (int e = tid; e < nact; e += (int)blockDim.x) {
     const int c = (e >= SF[0]) + (e >= SF[1]) + (e >= SF[2]);
     const int lo = c == 0 ? 0 : SF[c - 1];
     const int ub = (c == 0 ? 0 : UE[c - 1]) + (e - lo) * (c + 1);
-    const int j = sh.schan[e];
-    const float cf = ldexpf(1.0f, -(c + 1)) - 1.0f;
+    const uint32_t j = sh.schan[e];
     for (int p = 0; p <= c; ++p) {
-      const int v = ub + p;
-      sh.uoff[v] = (uint32_t)(j * 4 + p) * sub * 8u;
-      sh.soff[v] = (uint32_t)j * sub * 2u;
-#pragma unroll
-      for (int h = 0; h < kMaxG; ++h) {
-        const bool on = h < a.G;
-        const float Q = on ? ldexpf(sh.qs[h][j], -(p + sh.sig[h])) : 0.0f;
-        const _Float16 qh = f16_rtz(Q);
-        sh.qa[2 * h][v] = qh;
-        sh.qa[2 * h + 1][v] = f16_rtz(Q - (float)qh);
-        const float cq = (on && p == 0) ? ldexpf(sh.qs[h][j] * cf, -sh.sig[h]) : 0.0f;
-        const _Float16 ch = f16_rtz(cq);
-        sh.ca[2 * h][v] = ch;
-        sh.ca[2 * h + 1][v] = f16_rtz(cq - (float)ch);
-      }
+      sh.uoff[ub + p] = (j * 4u + (uint32_t)p) * sub * 8u;
+      sh.soff[ub + p] = j * sub * 2u;
     }
   }
-  // zero-weight, zero-scale padding units (they read plane word 0 of the superblock)
-  for (int v = ureal + tid; v < U; v += (int)blockDim.x) {
-    sh.uoff[v] = 0u;
-    sh.soff[v] = 0u;
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) sh.qa[r][v] = sh.ca[r][v] = (_Float16)0.0f;
-  }
+  for (int v = ureal + tid; v < UP; v += (int)blockDim.x) sh.uoff[v] = sh.soff[v] = 0u;
   __syncthreads();
   return U;
 }
@@ -306,17 +325,18 @@ __device__ __forceinline__ void load_scales(uint32_t (&ap)[NS][2], const Shared 
   }
 }
 
-// Zeroes the scales of padding units (units >= ureal): only the last slice of
-// a plan has any.
+// Zeroes the scales of padding units (units >= ureal).
 template <int NS>
 __device__ __forceinline__ void mask_pad_scales(uint32_t (&ap)[NS][2], int s0, int g, int ureal) {
-  const int s = NS - 1;
-  if ((s0 + s + 1) * kSlice > ureal) {
-    const int u = (s0 + s) * kSlice + 4 * g;
-    const uint32_t m0 = (u < ureal ? 0xFFFFu : 0u) | (u + 1 < ureal ? 0xFFFF0000u : 0u);
-    const uint32_t m1 = (u + 2 < ureal ? 0xFFFFu : 0u) | (u + 3 < ureal ? 0xFFFF0000u : 0u);
-    ap[s][0] &= m0;
-    ap[s][1] &= m1;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    if ((s0 + s + 1) * kSlice > ureal) {  // uniform
+      const int u = (s0 + s) * kSlice + 4 * g;
+      const uint32_t m0 = (u < ureal ? 0xFFFFu : 0u) | (u + 1 < ureal ? 0xFFFF0000u : 0u);
+      const uint32_t m1 = (u + 2 < ureal ? 0xFFFFu : 0u) | (u + 3 < ureal ? 0xFFFF0000u : 0u);
+      ap[s][0] &= m0;
+      ap[s][1] &= m1;
+    }
   }
 }
 
@@ -478,85 +498,116 @@ __device__ __forceinline__ float threshold_value(uint32_t thr) {
   return key_value(thr);
 }
 
-// Accumulator-domain thresholds of a head for a tile with no masked token:
-// T_w = ((thr - C) - margin) / 2^(fe0 - e_w).  The score is RN(x 2^(fe0 - e_w)
-// + C) with the product exact, so a score >= thr needs x >= T_w; the margin
-// covers the rounding of that sum and of thr - C (NaN passes both).  When a
-// factor 2^(fe0 - e_w) is not a normal float, T is NaN and every token of the
-// tile takes the exact path.
-__device__ __forceinline__ void acc_thresholds(float (&T)[4], float thr, float C, int fe0) {
+// Accumulator-domain threshold numerator of a head for a tile with no masked
+// token: T_w = ((thr - C) - margin) / 2^(fe0 - e_w) = X 2^(e_w - fe0).  The
+// score is RN(x 2^(fe0 - e_w) + C) with the product exact, so a score >= thr
+// needs x >= T_w; the margin covers the rounding of that sum and of thr - C
+// (NaN passes both).  When a factor 2^(fe0 - e_w) is not a normal float, X is
+// NaN and every token of the tile takes the exact path.
+__device__ __forceinline__ float acc_threshold(float thr, float C, int fe0) {
   const float margin = (fabsf(thr) + fabsf(C)) * 0x1p-20f + 0x1p-126f;
   const bool ok = fabsf(C) < INFINITY && fe0 - bit_exp(3) >= -126 && fe0 - bit_exp(0) <= 127;
-  const float X = ok ? (thr - C) - margin : __int_as_float(0x7FC00000);
-#pragma unroll
-  for (int w = 0; w < 4; ++w) T[w] = ldexpf(X, bit_exp(w) - fe0);
+  return ok ? (thr - C) - margin : __int_as_float(0x7FC00000);
+}
+
+// Prefilter threshold of step class w for the high accumulator row alone: a
+// token can score >= thr only if hi + lo >= X_w = X 2^(e_w - fe), and the low
+// row's accumulator is at most M 2^e_w in magnitude (M = sum_u |lo_u| a'_u;
+// zero where the caller compares hi + lo itself).  The slack covers the
+// rounding of this arithmetic and of the matrix sums; NaN and infinities
+// propagate to NaN or the right sign (a NaN threshold passes every token).
+__device__ __forceinline__ float hi_threshold(float X, int fe, int w, float M) {
+  if (!(fabsf(X) < INFINITY)) return X;  // +inf: no token; -inf, NaN: every token
+  const float t = ldexpf(X, bit_exp(w) - fe);
+  const float mw = ldexpf(M, bit_exp(w)) * (1.0f + 0x1p-16f);
+  return ((t - mw) - fabsf(t) * 0x1p-20f) - 0x1p-120f;
 }
 
 // Emission state of a lane over a tile: its two heads (slots) 2 g' + i.
 struct EmitState {
-  float T[2][4];       // candidate prefilter thresholds (NaN: exact path everywhere; +inf: never)
+  float T[2][4];       // candidate prefilter thresholds per slot and step class, accumulator
+                       // units (NaN: every token takes the exact path; +inf: none does)
   float thr[2];        // row thresholds as floats
   uint32_t off[2];     // candidates written so far into the tile's region (per head)
   float gm[2];         // group maxima: running max of the quarter's masked scores
   bool gnan[2];
+  bool head[2];        // the slot's head is in the row and not skipped
   bool plain;          // no masking anywhere in the tile
+  // tile-relative token intervals (wave-uniform): tokens of the scanned range
+  // [vlo, vlo + vlen) and unmasked tokens [mlo, mlo + mlen)
+  uint32_t vlo, vlen, mlo, mlen;
 };
 
-// The exact score of slot i at step class w of a step group.
-__device__ __forceinline__ float slot_score(const f4 &acc, const TileK &k, int i, int w) {
-  const float x = i == 0 ? acc[0] + acc[1] : acc[2] + acc[3];
-  return fmaf(x, ldexpf(1.0f, k.fe[i] - bit_exp(w)), k.C[i]);
-}
-
-// Candidate emission of step group V of quarter qs (tokens 16 qs + 4V + w of
-// every block): a compare per slot and step against T in the accumulator
-// domain; only steps where some lane passes compute scores and keys, rank them
-// within their head's 16 lanes by ballots, and write them into the tile's
-// region.  Heads in skipm emit nothing.
-__device__ __forceinline__ void emit_filter(const Emit &em, const ScanArgs &a, const f4 (&acc)[4], const TileK &k,
-                                            EmitState &es, int64_t bh, int64_t beta0, int qs, int V, int lane,
-                                            uint32_t skipm) {
+// The candidates of one step class whose prefilter some lane passed: the
+// exact scores of both slots, their keys, ranked within each head's 16 lanes
+// by ballots and written into the tile's region.  In a tile with no masked
+// token a head outside the row or skipped has T = +inf and never passes the
+// prefilter; other tiles (T = NaN: every lane passes) check each token.
+template <int W>
+__device__ __forceinline__ void filter_hit(const Emit &em, const ScanArgs &a, float xa, float xb, bool pa, bool pb,
+                                           const TileK &k, EmitState &es, int64_t bh, int64_t beta0, int qs, int V,
+                                           int lane) {
   const int c = lane & 15, gp = lane >> 4;
-  const int64_t t0 = beta0 * kBlk;
-  const uint32_t lt = (1u << c) - 1u;
+  // the token within the tile and in the row (n <= 2^31); in a tile with no
+  // masked token both intervals hold the whole tile (one branch-free path:
+  // a uniform branch on the tile kind measured slower)
+  const uint32_t tt = (uint32_t)(c * kBlk) + (uint32_t)(16 * qs + 4 * V + W);
+  const uint32_t tok = (uint32_t)(beta0 * kBlk) + tt;
+  const bool inr = tt - es.vlo < es.vlen, um = tt - es.mlo < es.mlen;
+  const uint32_t sh = 8u * (uint32_t)gp;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float xa = acc[w][0] + acc[w][1], xb = acc[w][2] + acc[w][3];
-    const bool pa = !(xa < es.T[0][w]), pb = !(xb < es.T[1][w]);
-    if (__ballot(pa || pb) == 0ull) continue;  // uniform
-    const int64_t tok = (beta0 + c) * kBlk + 16 * qs + 4 * V + w;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int h = 2 * gp + i;
-      const bool head = h < a.G && !((skipm >> h) & 1u);
-      const float v = slot_score(acc[w], k, i, w);
-      bool valid = head;
-      float vm = v;
-      if (!es.plain) {
-        const int64_t blk = beta0 + c;
-        valid = valid && blk >= a.blk0 && blk < a.blk_end && tok < a.n;
-        vm = (tok < em.sink || tok >= em.lstart) ? -INFINITY : v;
-      }
-      const bool pass = valid && !(vm < es.thr[i]);
-      const uint64_t m = __ballot(pass);
-      const uint32_t rb = (uint32_t)(m >> (16 * gp)) & 0xFFFFu;
-      if (pass) {
-        const int64_t row = bh * a.G + h;
-        uint64_t *dst = em.sel.cand + row * em.sel.cand_cap + t0;
-        dst[es.off[i] + (uint32_t)__builtin_popcount(rb & lt)] =
-            k64_of(vm == -INFINITY ? kKeyNegInf : score_key(vm), tok);
-      }
-      es.off[i] += (uint32_t)__builtin_popcount(rb);
+  for (int i = 0; i < 2; ++i) {
+    const float v = fmaf(i == 0 ? xa : xb, ldexpf(1.0f, k.fe[i] - bit_exp(W)), k.C[i]);
+    const float vm = um ? v : -INFINITY;  // score_key(-inf) is kKeyNegInf
+    const bool pass = es.head[i] && inr && (i == 0 ? pa : pb) && !(vm < es.thr[i]);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(pass);
+    if (m == 0ull) continue;  // uniform
+    // per row group (16 lanes, one head): the passing lanes below each group
+    // and in it, one byte per group (wave-uniform)
+    const uint32_t n0 = (uint32_t)__builtin_popcountll(m & 0xFFFFull);
+    const uint32_t n1 = (uint32_t)__builtin_popcountll(m & 0xFFFF0000ull);
+    const uint32_t n2 = (uint32_t)__builtin_popcountll(m & 0xFFFF00000000ull);
+    const uint32_t n3 = (uint32_t)__builtin_popcountll(m >> 48);
+    const uint32_t below = (n0 << 8) | ((n0 + n1) << 16) | ((n0 + n1 + n2) << 24);
+    const uint32_t in = n0 | (n1 << 8) | (n2 << 16) | (n3 << 24);
+    if (pass) {
+      const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      const uint32_t at = es.off[i] + before - ((below >> sh) & 0xFFu);
+      uint64_t *dst = em.sel.cand + (bh * a.G + i) * em.sel.cand_cap + beta0 * kBlk +
+                      (uint64_t)(uint32_t)(2 * gp) * (uint64_t)em.sel.cand_cap;
+      dst[at] = k64_of(score_key(vm), tok);
     }
+    es.off[i] += (in >> sh) & 0xFFu;
   }
 }
 
-// Scores of step group V of quarter qs: each lane stores its block's four
-// consecutive tokens per head (and, GMAX, folds them into the quarter's group
-// maximum, written once the quarter ends).
+// Candidate emission of step class w of step group V of quarter qs (token
+// 16 qs + 4V + w of every block): a compare per slot against T in the
+// accumulator domain (HI: the high row alone, T allowing for the low row;
+// else the sum of both rows); only steps where some lane passes compute
+// exact scores and keys (filter_hit).  Heads in skipm emit nothing.
+template <int W, bool HI>
+__device__ __forceinline__ void emit_filter_w(const Emit &em, const ScanArgs &a, const f4 &acc, const TileK &k,
+                                              EmitState &es, int64_t bh, int64_t beta0, int qs, int V, int lane) {
+  bool pa, pb;
+  if constexpr (HI) {
+    pa = !(acc[0] < es.T[0][W]);
+    pb = !(acc[2] < es.T[1][W]);
+  } else {
+    pa = !(acc[0] + acc[1] < es.T[0][W]);
+    pb = !(acc[2] + acc[3] < es.T[1][W]);
+  }
+  if (__builtin_amdgcn_ballot_w64(pa || pb) == 0ull) return;  // uniform
+  filter_hit<W>(em, a, acc[0] + acc[1], acc[2] + acc[3], pa, pb, k, es, bh, beta0, qs, V, lane);
+}
+
+// Scores of step group V of quarter qs, from the four step classes' scores
+// s4[slot][w]: each lane stores its block's four consecutive tokens per head
+// (and, GMAX, folds them into the quarter's group maximum, written once the
+// quarter ends).
 template <bool GMAX>
-__device__ __forceinline__ void emit_scores(const Emit &em, const ScanArgs &a, const f4 (&acc)[4], const TileK &k,
-                                            EmitState &es, int64_t bh, int64_t beta0, int qs, int V, int lane) {
+__device__ __forceinline__ void store_scores(const Emit &em, const ScanArgs &a, const float (&s4)[2][4], EmitState &es,
+                                             int64_t bh, int64_t beta0, int qs, int V, int lane) {
   const int c = lane & 15, gp = lane >> 4;
   const int64_t blk = beta0 + c;
   const bool inr = blk >= a.blk0 && blk < a.blk_end;
@@ -566,19 +617,17 @@ __device__ __forceinline__ void emit_scores(const Emit &em, const ScanArgs &a, c
   for (int i = 0; i < 2; ++i) {
     const int h = 2 * gp + i;
     if (h >= a.G || !inr || tq >= a.n) continue;
-    float s[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) s[w] = slot_score(acc[w], k, i, w);
+    const float *s = s4[i];
     float *dst = em.out + (bh * a.G + h) * a.n + t4;
     if (t4 + 4 <= a.n && (a.n & 3) == 0) {
-      *reinterpret_cast<float4 *>(dst) = make_float4(s[0], s[1], s[2], s[3]);
+      *reinterpret_cast<f4 *>(dst) = f4{s[0], s[1], s[2], s[3]};
     } else {
 #pragma unroll
       for (int w = 0; w < 4; ++w)
         if (t4 + w < a.n) dst[w] = s[w];
     }
-    if constexpr (GMAX) {
-      if (V == 0) {
+    if constexpr (GMAX) {  // a quarter's step groups come V = 3 first, V = 0 last
+      if (V == 3) {
         es.gm[i] = -INFINITY;
         es.gnan[i] = false;
       }
@@ -589,7 +638,7 @@ __device__ __forceinline__ void emit_scores(const Emit &em, const ScanArgs &a, c
         es.gm[i] = fmaxf(es.gm[i], v);
         es.gnan[i] = es.gnan[i] || (v != v);
       }
-      if (V == 3) {
+      if (V == 0) {
         const int64_t ngrp = (a.n + kR - 1) / kR;
         em.gmax[(bh * a.G + h) * ngrp + blk * 4 + qs] = es.gnan[i] ? 0xFFFFFFFFu : score_key(es.gm[i]);
       }
@@ -599,8 +648,8 @@ __device__ __forceinline__ void emit_scores(const Emit &em, const ScanArgs &a, c
 
 // Sampled keys of step group V of quarter qs of list entry L (sink/local
 // masked, 0 beyond the row).
-__device__ __forceinline__ void emit_sample(const Emit &em, const ScanArgs &a, const f4 (&acc)[4], const TileK &k,
-                                            int64_t bh, int64_t beta0, int64_t L, int qs, int V, int lane) {
+__device__ __forceinline__ void store_sample(const Emit &em, const ScanArgs &a, const float (&s4)[2][4], int64_t bh,
+                                             int64_t beta0, int64_t L, int qs, int V, int lane) {
   const int c = lane & 15, gp = lane >> 4;
   const int64_t t4 = (beta0 + c) * kBlk + 16 * qs + 4 * V;
 #pragma unroll
@@ -612,38 +661,100 @@ __device__ __forceinline__ void emit_sample(const Emit &em, const ScanArgs &a, c
     for (int w = 0; w < 4; ++w) {
       const int64_t tok = t4 + w;
       const bool masked = tok < em.sink || tok >= em.lstart;
-      key[w] = tok < a.n ? (masked ? kKeyNegInf : score_key(slot_score(acc[w], k, i, w))) : 0u;
+      key[w] = tok < a.n ? (masked ? kKeyNegInf : score_key(s4[i][w])) : 0u;
     }
     uint32_t *dst = em.samp + (bh * a.G + h) * em.samp_cap + L * kWTok + c * kBlk + 16 * qs + 4 * V;
     *reinterpret_cast<uint4 *>(dst) = make_uint4(key[0], key[1], key[2], key[3]);
   }
 }
 
-// ------------------------------------------------------------------ tile loop
-// Per-mode state set up once a tile's scale pass is done.
+// Per-step-class emission state of a step group: the two slots' scores of the
+// four classes (score modes).
+struct StepOut {
+  float s4[2][4];
+};
+
+// Emission of step class W of step group V: the candidate compare at once, or
+// the scores kept for the group's stores.
+template <int MODE, int W, bool HI>
+__device__ __forceinline__ void emit_w(const Emit &em, const ScanArgs &a, const f4 &acc, const TileK &k, EmitState &es,
+                                       StepOut &o, int64_t bh, int64_t beta0, int qs, int V, int lane) {
+  if constexpr (MODE == kEmitFilter) {
+    emit_filter_w<W, HI>(em, a, acc, k, es, bh, beta0, qs, V, lane);
+  } else {
+    const float f0 = ldexpf(1.0f, k.fe[0] - bit_exp(W)), f1 = ldexpf(1.0f, k.fe[1] - bit_exp(W));
+    o.s4[0][W] = fmaf(acc[0] + acc[1], f0, k.C[0]);
+    o.s4[1][W] = fmaf(acc[2] + acc[3], f1, k.C[1]);
+  }
+}
+
+// The stores of a step group's scores (score modes).
 template <int MODE>
-__device__ __forceinline__ void tile_setup(EmitState &es, const Emit &em, const ScanArgs &a, const TileK &k, int64_t bh,
-                                           int64_t beta0, int lane, bool fb, uint32_t skipm) {
-  const int gp = lane >> 4;
+__device__ __forceinline__ void emit_flush(const Emit &em, const ScanArgs &a, EmitState &es, const StepOut &o,
+                                           int64_t bh, int64_t beta0, int64_t L, int qs, int V, int lane) {
+  if constexpr (MODE == kEmitScores) store_scores<false>(em, a, o.s4, es, bh, beta0, qs, V, lane);
+  if constexpr (MODE == kEmitScoresMax) store_scores<true>(em, a, o.s4, es, bh, beta0, qs, V, lane);
+  if constexpr (MODE == kEmitSample) store_sample(em, a, o.s4, bh, beta0, L, qs, V, lane);
+}
+
+// ------------------------------------------------------------------ tile loop
+// A candidate wave's constants of its row (every tile of a wave is in one
+// row): the lane's two heads' thresholds and whether they emit (in the row
+// and not skipped).
+struct RowK {
+  float thr[2];
+  bool head[2];
+};
+
+__device__ __forceinline__ RowK row_consts(const Emit &em, const ScanArgs &a, int64_t bh, int lane, bool fb,
+                                           uint32_t skipm) {
+  RowK r;
+  const uint32_t *thr = fb ? em.sel.thr_lo : em.sel.thr;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int h = 2 * (lane >> 4) + i;
+    r.head[i] = h < a.G && !((skipm >> h) & 1u);
+    r.thr[i] = r.head[i] ? threshold_value(thr[bh * a.G + h]) : INFINITY;
+  }
+  return r;
+}
+
+// Per-mode state set up once a tile's scale pass is done; M: the bound of
+// the low rows' accumulators per unit 2^e_w (zero where the prefilter
+// compares both rows).
+template <int MODE>
+__device__ __forceinline__ void tile_setup(EmitState &es, const Emit &em, const ScanArgs &a, const TileK &k,
+                                           int64_t beta0, const RowK &rk, const float (&M)[2]) {
   const int64_t t0 = beta0 * kBlk, t1 = t0 + kWTok;
   es.plain = beta0 >= a.blk0 && beta0 + kWB <= a.blk_end && t1 <= a.n && t0 >= em.sink && t1 <= em.lstart;
   es.off[0] = es.off[1] = 0u;
   if constexpr (MODE == kEmitFilter) {
-    const uint32_t *thr = fb ? em.sel.thr_lo : em.sel.thr;
+    if (es.plain) {  // uniform
+      es.vlo = es.mlo = 0u;
+      es.vlen = es.mlen = (uint32_t)kWTok;
+    } else {
+      // [lo, hi) of the row clipped to the tile, relative to its first token
+      auto rel = [&](int64_t lo, int64_t hi, uint32_t &rlo, uint32_t &rlen) {
+        const int64_t l = min(max(lo - t0, (int64_t)0), (int64_t)kWTok);
+        const int64_t h = min(max(hi - t0, (int64_t)0), (int64_t)kWTok);
+        rlo = (uint32_t)l;
+        rlen = (uint32_t)max(h - l, (int64_t)0);
+      };
+      rel(max(a.blk0 * kBlk, (int64_t)0), min(a.blk_end * kBlk, a.n), es.vlo, es.vlen);
+      rel(em.sink, em.lstart, es.mlo, es.mlen);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int h = 2 * gp + i;
-      const bool head = h < a.G && !((skipm >> h) & 1u);
-      es.thr[i] = head ? threshold_value(thr[bh * a.G + h]) : INFINITY;
-      if (!head) {
+      es.head[i] = rk.head[i];
+      es.thr[i] = rk.thr[i];
+      const float X = !es.head[i] ? INFINITY
+                      : es.plain  ? acc_threshold(es.thr[i], k.C[i], k.fe[i])
+                                  : __int_as_float(0x7FC00000);
+      // T_w = T_0 2^(e_w - e_0) exactly (a threshold past the float range
+      // becomes +inf, which no finite accumulator reaches)
+      es.T[i][0] = hi_threshold(X, k.fe[i], 0, M[i]);
 #pragma unroll
-        for (int w = 0; w < 4; ++w) es.T[i][w] = INFINITY;
-      } else if (es.plain) {
-        acc_thresholds(es.T[i], es.thr[i], k.C[i], k.fe[i]);
-      } else {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) es.T[i][w] = __int_as_float(0x7FC00000);
-      }
+      for (int w = 1; w < 4; ++w) es.T[i][w] = es.T[i][0] * (float)(1 << (bit_exp(w) - bit_exp(0)));
     }
   }
 }
@@ -693,18 +804,56 @@ __device__ __forceinline__ void step_group(f4 (&acc)[4], const uint32_t (&qa)[NS
     if (w == 2) b_operands<NS, 2>(b, Y, ap);
     if (w == 3) b_operands<NS, 3>(b, Y, ap);
     acc[w] = chain<NS, FIRST>(acc[w], qa, b);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// Emission of step group V of quarter qs, whichever the mode.
+// Emission of step group V of quarter qs from its four accumulators (the
+// grouped path), whichever the mode.
 template <int MODE>
 __device__ __forceinline__ void emit_group(const Emit &em, const ScanArgs &a, const f4 (&acc)[4], const TileK &k,
                                            EmitState &es, int64_t bh, int64_t beta0, int64_t L, int qs, int V,
-                                           int lane, uint32_t skipm) {
-  if constexpr (MODE == kEmitFilter) emit_filter(em, a, acc, k, es, bh, beta0, qs, V, lane, skipm);
-  if constexpr (MODE == kEmitScores) emit_scores<false>(em, a, acc, k, es, bh, beta0, qs, V, lane);
-  if constexpr (MODE == kEmitScoresMax) emit_scores<true>(em, a, acc, k, es, bh, beta0, qs, V, lane);
-  if constexpr (MODE == kEmitSample) emit_sample(em, a, acc, k, bh, beta0, L, qs, V, lane);
+                                           int lane) {
+  StepOut o;
+  emit_w<MODE, 0, false>(em, a, acc[0], k, es, o, bh, beta0, qs, V, lane);
+  emit_w<MODE, 1, false>(em, a, acc[1], k, es, o, bh, beta0, qs, V, lane);
+  emit_w<MODE, 2, false>(em, a, acc[2], k, es, o, bh, beta0, qs, V, lane);
+  emit_w<MODE, 3, false>(em, a, acc[3], k, es, o, bh, beta0, qs, V, lane);
+  emit_flush<MODE>(em, a, es, o, bh, beta0, L, qs, V, lane);
+}
+
+// One step group of a plan of NS slices held in registers (Y: the quarter's
+// halves shifted for step group V), each step class emitted as soon as its
+// chain is done (one accumulator live at a time).
+template <int MODE, int NS>
+__device__ __forceinline__ void step_group_emit(const uint32_t (&qa)[NS][2], const uint32_t (&ap)[NS][2],
+                                                const uint32_t (&Y)[NS][2], const Emit &em, const ScanArgs &a,
+                                                const TileK &k, EmitState &es, int64_t bh, int64_t beta0, int64_t L,
+                                                int qs, int V, int lane) {
+  StepOut o;
+  // each step class's chain is issued before the previous class is emitted,
+  // so the emission does not wait on the matrix pipe
+  f4 prev;
+  {
+    uint32_t b[NS][2];
+    b_operands<NS, 0>(b, Y, ap);
+    prev = chain<NS, true>(f4{}, qa, b);
+  }
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    uint32_t b[NS][2];
+    if (w == 1) b_operands<NS, 1>(b, Y, ap);
+    if (w == 2) b_operands<NS, 2>(b, Y, ap);
+    if (w == 3) b_operands<NS, 3>(b, Y, ap);
+    const f4 acc = chain<NS, true>(f4{}, qa, b);
+    if (w == 1) emit_w<MODE, 0, true>(em, a, prev, k, es, o, bh, beta0, qs, V, lane);
+    if (w == 2) emit_w<MODE, 1, true>(em, a, prev, k, es, o, bh, beta0, qs, V, lane);
+    if (w == 3) emit_w<MODE, 2, true>(em, a, prev, k, es, o, bh, beta0, qs, V, lane);
+    prev = acc;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  emit_w<MODE, 3, true>(em, a, prev, k, es, o, bh, beta0, qs, V, lane);
+  emit_flush<MODE>(em, a, es, o, bh, beta0, L, qs, V, lane);
 }
 
 // The work of one wave on one tile: wave-tile beta0 (blocks beta0 .. beta0 +
@@ -716,11 +865,57 @@ struct TileJob {
   int qa0, qa1, lane, ureal;
   bool fb;
   uint32_t skipm;
+  RowK rk;
 };
 
+// The bound M of the low rows' accumulators of the lane's heads per unit
+// 2^e_w: sum_u |lo_u| |a'_u|, by the matrix instruction (rows 4g' + 1 and
+// 4g' + 3 of |A| |B| are the low rows of heads 2g' and 2g' + 1).
+template <int NS>
+__device__ __forceinline__ void lo_bound(float (&M)[2], const uint32_t (&qreg)[NS][2], const uint32_t (&ap)[NS][2]) {
+  uint32_t aq[NS][2], ab[NS][2];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    aq[s][0] = qreg[s][0] & 0x7FFF7FFFu;
+    aq[s][1] = qreg[s][1] & 0x7FFF7FFFu;
+    ab[s][0] = ap[s][0] & 0x7FFF7FFFu;
+    ab[s][1] = ap[s][1] & 0x7FFF7FFFu;
+  }
+  const f4 d = chain<NS, true>(f4{}, aq, ab);
+  M[0] = d[1];
+  M[1] = d[3];
+}
+
+// The four step groups of quarter qs, V = 3 down to 0, on the quarter's halves
+// Y (consumed).  Each dword turns as a whole: right by one for V = 3, then left
+// by four per step group, so the half bits 4V..4V+3 sit on bits 11..14 of each
+// half at step group V.  No bit is lost; the bits that wrap from one half into
+// the other land on bits 0..10 or 15 of a half, which no mask selects.
+template <int MODE, int NS>
+__device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], const uint32_t (&ap)[NS][2],
+                                             uint32_t (&Y)[NS][2], const Emit &em, const ScanArgs &a,
+                                             const TileK &k, EmitState &es, const TileJob &j, int qs) {
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    Y[s][0] = __builtin_rotateright32(Y[s][0], 1);
+    Y[s][1] = __builtin_rotateright32(Y[s][1], 1);
+  }
+  step_group_emit<MODE, NS>(qreg, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, 3, j.lane);
+#pragma unroll 1
+  for (int V = 2; V >= 0; --V) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      Y[s][0] = __builtin_rotateleft32(Y[s][0], 4);
+      Y[s][1] = __builtin_rotateleft32(Y[s][1], 4);
+    }
+    step_group_emit<MODE, NS>(qreg, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, V, j.lane);
+  }
+}
+
 // A plan of NS (1..4) slices: the scales stay in registers for the whole tile
-// and the A rows (qreg) for every tile; the next quarter pair's plane dwords
-// load while the current pair's quarters compute.
+// and the A rows (qreg) for every tile.  Both quarters' halves are taken from a
+// quarter pair's plane dwords at once; the next pair's dwords load while the
+// second quarter computes.
 template <int MODE, int NS>
 __device__ __forceinline__ void tile_fast(const ScanArgs &a, const Emit &em, const Shared &sh,
                                           const uint32_t (&qreg)[NS][2], const TileJob &j) {
@@ -735,30 +930,18 @@ __device__ __forceinline__ void tile_fast(const ScanArgs &a, const Emit &em, con
   scale_group<NS, true>(ap, amax, dc, sh, ta, 0, j.lane, j.ureal);
   const TileK k = scale_finish(amax, dc, sh, a, j.lane);
   rescale<NS>(ap, k.sx);
+  float M[2] = {0.0f, 0.0f};
+  if constexpr (MODE == kEmitFilter) lo_bound<NS>(M, qreg, ap);
   EmitState es;
-  tile_setup<MODE>(es, em, a, k, j.bh, j.beta0, j.lane, j.fb, j.skipm);
+  tile_setup<MODE>(es, em, a, k, j.beta0, j.rk, M);
 #pragma unroll 1
   for (int qp = qp0; qp < qp1; ++qp) {
     uint32_t X0[NS][2], X1[NS][2];
     quarter_halves<NS, 0>(X0, d);
     quarter_halves<NS, 1>(X1, d);
-    if (qp + 1 < qp1) load_planes<NS>(d, sh, ta, 0, g, qp + 1);
-    if (2 * qp >= j.qa0) {
-#pragma unroll 1
-      for (int V = 0; V < 4; ++V) {
-        f4 acc[4];
-        step_group<NS, true>(acc, qreg, ap, X0, V);
-        emit_group<MODE>(em, a, acc, k, es, j.bh, j.beta0, j.L, 2 * qp, V, j.lane, j.skipm);
-      }
-    }
-    if (2 * qp + 1 < j.qa1) {
-#pragma unroll 1
-      for (int V = 0; V < 4; ++V) {
-        f4 acc[4];
-        step_group<NS, true>(acc, qreg, ap, X1, V);
-        emit_group<MODE>(em, a, acc, k, es, j.bh, j.beta0, j.L, 2 * qp + 1, V, j.lane, j.skipm);
-      }
-    }
+    if (2 * qp >= j.qa0) quarter_fast<MODE, NS>(qreg, ap, X0, em, a, k, es, j, 2 * qp);
+    if (qp + 1 < qp1) load_planes<NS>(d, sh, ta, 0, g, qp + 1);  // in flight during the second quarter
+    if (2 * qp + 1 < j.qa1) quarter_fast<MODE, NS>(qreg, ap, X1, em, a, k, es, j, 2 * qp + 1);
   }
   if constexpr (MODE == kEmitFilter) tile_counts(em, a, es, j.bh, j.beta0, j.lane, j.fb, j.skipm);
 }
@@ -779,68 +962,57 @@ __device__ __forceinline__ void run_group(f4 (&acc)[ACC][4], const Shared &sh, c
   for (int v = 0; v < ACC; ++v) step_group<NS, FIRST>(acc[v], qa, ap, X, V0 + v);
 }
 
-// A plan of more than four slices: every step group's chain runs over the
-// register groups in order (full groups of four slices, then the rest), each
-// group's planes, A rows and scales reloaded per pass of ACC step groups.
-template <int MODE, int ACC>
+// A plan of more slices than the kernel holds in registers: every step
+// group's chain runs over register groups of GS slices in order (GS even, so
+// the slices pair as in one chain), each group's planes, A rows and scales
+// reloaded per pass of ACC step groups.
+template <int MODE, int ACC, int GS>
 __device__ __forceinline__ void tile_grouped(const ScanArgs &a, const Emit &em, const Shared &sh, int nsl,
                                              const TileJob &j) {
+  static_assert(GS % 2 == 0, "register groups of whole slice pairs");
   const int c = j.lane & 15;
   const TileAddr ta = tile_addr(a, j.bh, j.beta0, c);
-  const int nfull = nsl / kGS, tail = nsl - nfull * kGS;
+  const int nfull = nsl / GS, tail = nsl - nfull * GS;
   float amax = 0.0f;
   f4 dc;
   {
-    uint32_t raw[kGS][2];
-    scale_group<kGS, true>(raw, amax, dc, sh, ta, 0, j.lane, j.ureal);
+    uint32_t raw[GS][2];
+    scale_group<GS, true>(raw, amax, dc, sh, ta, 0, j.lane, j.ureal);
 #pragma unroll 1
-    for (int gi = 1; gi < nfull; ++gi) scale_group<kGS, false>(raw, amax, dc, sh, ta, gi * kGS, j.lane, j.ureal);
+    for (int gi = 1; gi < nfull; ++gi) scale_group<GS, false>(raw, amax, dc, sh, ta, gi * GS, j.lane, j.ureal);
     uint32_t r1[1][2], r2[2][2], r3[3][2];
-    if (tail == 1) scale_group<1, false>(r1, amax, dc, sh, ta, nfull * kGS, j.lane, j.ureal);
-    if (tail == 2) scale_group<2, false>(r2, amax, dc, sh, ta, nfull * kGS, j.lane, j.ureal);
-    if (tail == 3) scale_group<3, false>(r3, amax, dc, sh, ta, nfull * kGS, j.lane, j.ureal);
+    if (tail == 1) scale_group<1, false>(r1, amax, dc, sh, ta, nfull * GS, j.lane, j.ureal);
+    if (GS > 2 && tail == 2) scale_group<2, false>(r2, amax, dc, sh, ta, nfull * GS, j.lane, j.ureal);
+    if (GS > 3 && tail == 3) scale_group<3, false>(r3, amax, dc, sh, ta, nfull * GS, j.lane, j.ureal);
   }
   const TileK k = scale_finish(amax, dc, sh, a, j.lane);
+  const float M[2] = {0.0f, 0.0f};  // the grouped path compares both rows
   EmitState es;
-  tile_setup<MODE>(es, em, a, k, j.bh, j.beta0, j.lane, j.fb, j.skipm);
+  tile_setup<MODE>(es, em, a, k, j.beta0, j.rk, M);
 #pragma unroll 1
   for (int qs = j.qa0; qs < j.qa1; ++qs) {
 #pragma unroll 1
-    for (int V0 = 0; V0 < 4; V0 += ACC) {
+    for (int V0 = 4 - ACC; V0 >= 0; V0 -= ACC) {
       f4 acc[ACC][4];
-      run_group<kGS, true, ACC>(acc, sh, ta, 0, j.lane, k.sx, j.ureal, qs, V0);
+      run_group<GS, true, ACC>(acc, sh, ta, 0, j.lane, k.sx, j.ureal, qs, V0);
 #pragma unroll 1
-      for (int gi = 1; gi < nfull; ++gi) run_group<kGS, false, ACC>(acc, sh, ta, gi * kGS, j.lane, k.sx, j.ureal, qs, V0);
-      if (tail == 1) run_group<1, false, ACC>(acc, sh, ta, nfull * kGS, j.lane, k.sx, j.ureal, qs, V0);
-      if (tail == 2) run_group<2, false, ACC>(acc, sh, ta, nfull * kGS, j.lane, k.sx, j.ureal, qs, V0);
-      if (tail == 3) run_group<3, false, ACC>(acc, sh, ta, nfull * kGS, j.lane, k.sx, j.ureal, qs, V0);
+      for (int gi = 1; gi < nfull; ++gi) run_group<GS, false, ACC>(acc, sh, ta, gi * GS, j.lane, k.sx, j.ureal, qs, V0);
+      if (tail == 1) run_group<1, false, ACC>(acc, sh, ta, nfull * GS, j.lane, k.sx, j.ureal, qs, V0);
+      if (GS > 2 && tail == 2) run_group<2, false, ACC>(acc, sh, ta, nfull * GS, j.lane, k.sx, j.ureal, qs, V0);
+      if (GS > 3 && tail == 3) run_group<3, false, ACC>(acc, sh, ta, nfull * GS, j.lane, k.sx, j.ureal, qs, V0);
 #pragma unroll
-      for (int v = 0; v < ACC; ++v) emit_group<MODE>(em, a, acc[v], k, es, j.bh, j.beta0, j.L, qs, V0 + v, j.lane, j.skipm);
+      for (int v = ACC - 1; v >= 0; --v) emit_group<MODE>(em, a, acc[v], k, es, j.bh, j.beta0, j.L, qs, V0 + v, j.lane);
     }
   }
   if constexpr (MODE == kEmitFilter) tile_counts(em, a, es, j.bh, j.beta0, j.lane, j.fb, j.skipm);
 }
 
-// A plan with no unit: every score is C = 0.
-template <int MODE>
-__device__ __forceinline__ void tile_empty(const ScanArgs &a, const Emit &em, const TileJob &j) {
-  const TileK k{0, {0.0f, 0.0f}, {0, 0}};
-  EmitState es;
-  tile_setup<MODE>(es, em, a, k, j.bh, j.beta0, j.lane, j.fb, j.skipm);
-  const f4 z[4] = {};
-#pragma unroll 1
-  for (int qs = j.qa0; qs < j.qa1; ++qs)
-#pragma unroll 1
-    for (int V = 0; V < 4; ++V) emit_group<MODE>(em, a, z, k, es, j.bh, j.beta0, j.L, qs, V, j.lane, j.skipm);
-  if constexpr (MODE == kEmitFilter) tile_counts(em, a, es, j.bh, j.beta0, j.lane, j.fb, j.skipm);
-}
-
-// The tile loop of one plan kind (NSK slices 1..4; 0: no unit; -1: more than
-// four): list entries L0, L0 + Ls, ... < nlist, quarters [qa0, qa1).  FB: the
-// candidate pass's fallback rescan (T_lo, second count array; heads in skipm
-// emit nothing).  The candidate pass's entries past the row's tiles (padding
-// regions) get zero counts.
-template <int MODE, int NSK, int ACC, bool FB>
+// The tile loop of one plan kind (NSK slices 1..4, the plan padded with zero
+// units; -1: more than the kernel holds): list entries L0, L0 + Ls, ... <
+// nlist, quarters [qa0, qa1).  FB: the candidate pass's fallback rescan (T_lo,
+// second count array; heads in skipm emit nothing).  The candidate pass's
+// entries past the row's tiles (padding regions) get zero counts.
+template <int MODE, int NSK, int ACC, bool FB, int GS>
 __device__ __forceinline__ void tile_loop(const ScanArgs &a, const Emit &em, const Shared &sh, int64_t bh, int lane,
                                           int64_t L0, int64_t Ls, int64_t nlist, int qa0, int qa1, uint32_t skipm,
                                           int nsl, int ureal) {
@@ -849,37 +1021,41 @@ __device__ __forceinline__ void tile_loop(const ScanArgs &a, const Emit &em, con
   uint32_t *rcp = FB ? em.sel.rc2 : em.sel.rc1;
   uint32_t qreg[NQ][2];
   if constexpr (NSK > 0) load_arows<NQ>(qreg, sh.qa, 0, lane & 15, lane >> 4);
+  RowK rk{};
+  if constexpr (kCand) rk = row_consts(em, a, bh, lane, FB, skipm);
+  int64_t left = L0 < nlist ? (nlist - 1 - L0) / Ls : 0;  // the wave's entries after the current one
 #pragma unroll 1
-  for (int64_t L = L0; L < nlist; L += Ls) {
+  for (int64_t L = L0; L < nlist; L += Ls, --left) {
     if (kCand && L >= a.nwt) {
       if (lane < a.G && !((skipm >> lane) & 1u)) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
       continue;
     }
     const int64_t beta0 = (a.wt0 + L * a.wt_stride) * kWB;
     if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
-    set_priority_by_tiles_left((nlist - 1 - L) / Ls);
-    const TileJob j{bh, beta0, L, qa0, qa1, lane, ureal, FB, skipm};
+    set_priority_by_tiles_left(left);
+    const TileJob j{bh, beta0, L, qa0, qa1, lane, ureal, FB, skipm, rk};
     if constexpr (NSK > 0) tile_fast<MODE, NQ>(a, em, sh, qreg, j);
-    else if constexpr (NSK == 0) tile_empty<MODE>(a, em, j);
-    else tile_grouped<MODE, ACC>(a, em, sh, nsl, j);
+    else tile_grouped<MODE, ACC, GS>(a, em, sh, nsl, j);
   }
 }
 
-// Every tile of a wave, dispatched once on the plan's slice count (uniform per
-// workgroup: one row).
-template <int MODE, int ACC, bool FB>
+// Every tile of a wave.  A plan of up to NSMAX slices (the workgroup's tables
+// padded to NSMAX slices by plan_tables) runs with everything in registers;
+// a larger one in register groups (a kernel picked for small plans still
+// scans any plan correctly, only slower).  Zero units add exact zeros to
+// every chain (a chain from zero is never -0), so the scores do not depend on
+// the padding.
+template <int MODE, int ACC, bool FB, int NSMAX>
 __device__ __forceinline__ void tile_pass(const ScanArgs &a, const Emit &em, const Shared &sh, int64_t bh, int lane,
                                           int64_t L0, int64_t Ls, int64_t nlist, int qa0, int qa1, uint32_t skipm) {
+  static_assert(NSMAX >= 1 && NSMAX <= kGS, "one to four slices held in registers");
+  constexpr int GS = ACC == 4 ? kGS : 2;  // the register groups of a kernel tuned for small plans stay small
   const int nsl = __builtin_amdgcn_readfirstlane(sh.U) / kSlice;
   const int ureal = __builtin_amdgcn_readfirstlane(sh.ureal);
-  switch (nsl) {
-    case 0: tile_loop<MODE, 0, ACC, FB>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal); break;
-    case 1: tile_loop<MODE, 1, ACC, FB>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal); break;
-    case 2: tile_loop<MODE, 2, ACC, FB>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal); break;
-    case 3: tile_loop<MODE, 3, ACC, FB>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal); break;
-    case 4: tile_loop<MODE, 4, ACC, FB>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal); break;
-    default: tile_loop<MODE, -1, ACC, FB>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal); break;
-  }
+  if (nsl <= NSMAX)
+    tile_loop<MODE, NSMAX, ACC, FB, GS>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal);
+  else
+    tile_loop<MODE, -1, ACC, FB, GS>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal);
 }
 
 }  // namespace sc

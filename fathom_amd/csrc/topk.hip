@@ -684,12 +684,12 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(int64_t m, int64_
 // bit for bit (the same chain of matrix instructions per token).
 __device__ __forceinline__ void rescan_row(const sc::ScanArgs &a, const sc::Emit &em, int64_t bh, int h,
                                            sc::Shared &tsh) {
-  sc::plan_tables(tsh, a, bh);
+  sc::plan_tables(tsh, a, bh, sc::kGS * sc::kSlice);
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (wave < sc::kWaves) {
     const int64_t nlist = em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
     const uint32_t skipm = ((1u << a.G) - 1u) & ~(1u << h);
-    sc::tile_pass<sc::kEmitFilter, 1, true>(a, em, tsh, bh, lane, wave, sc::kWaves, nlist, 0, sc::kQS, skipm);
+    sc::tile_pass<sc::kEmitFilter, 1, true, sc::kGS>(a, em, tsh, bh, lane, wave, sc::kWaves, nlist, 0, sc::kQS, skipm);
     __builtin_amdgcn_s_setprio(0);
   }
   // the rescan's region counts and candidates are read back by other waves of
