@@ -20,18 +20,18 @@ using namespace sc;
 // choice; the launch picks them from the plan's units bound.
 template <int MODE, int NSMAX, int ACC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
-    ACC == 4 ? 2 : 4))) void scan_wave_kernel(ScanArgs a, Emit em) {
+    ACC == 4 ? 2 : 4))) void scan_wave_kernel(ScanArgs a, Emit em, int split) {
   __shared__ Shared sh;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
   plan_tables(sh, a, bh, NSMAX * kSlice);
-  if constexpr (MODE == kEmitSample) {
-    // the sample pass is latency-bound (a few tiles per row): four waves per
-    // tile, one quarter each
-    static_assert(kWaves == kQS, "a wave per quarter of a sample tile");
-    tile_pass<kEmitSample, ACC, false, NSMAX>(a, em, sh, bh, lane, (int64_t)blockIdx.x, (int64_t)gridDim.x, a.nwt,
-                                              wave, wave + 1, 0u);
+  if (MODE == kEmitSample || (MODE != kEmitFilter && split)) {
+    // few tiles (the sample pass, short rows): four waves per tile, one
+    // quarter each; the candidate pass keeps whole tiles (a region per tile)
+    static_assert(kWaves == kQS, "a wave per quarter of a tile");
+    tile_pass<MODE, ACC, false, NSMAX>(a, em, sh, bh, lane, (int64_t)blockIdx.x, (int64_t)gridDim.x, a.nwt,
+                                       wave, wave + 1, 0u);
   } else {
     // the candidate pass also writes the (zero) counts of the padding regions past the row
     constexpr bool kCand = MODE == kEmitFilter;
@@ -50,8 +50,10 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int
   ScanArgs a = a0;
   a.nwt = nwt;
   int64_t wgs;
-  if (MODE == kEmitSample) {
-    wgs = nwt;  // four waves per tile
+  int split = 0;
+  if (MODE == kEmitSample || (MODE != kEmitFilter && nwt * BH < kTargetWaves)) {
+    wgs = nwt;  // four waves per tile, a quarter each
+    split = 1;
   } else {
     // enough waves to fill the chip, each taking a whole number of tiles
     const int64_t per = cdiv(nwt * BH, kTargetWaves);
@@ -60,13 +62,13 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int
   const dim3 grid((unsigned)wgs, (unsigned)BH);
   const int64_t nsl = cdiv(units_max, kSlice);
   if (nsl > kGS)
-    scan_wave_kernel<MODE, kGS, 4><<<grid, kThreads, 0, st>>>(a, em);
+    scan_wave_kernel<MODE, kGS, 4><<<grid, kThreads, 0, st>>>(a, em, split);
   else if (nsl == 4)
-    scan_wave_kernel<MODE, 4, 1><<<grid, kThreads, 0, st>>>(a, em);
+    scan_wave_kernel<MODE, 4, 1><<<grid, kThreads, 0, st>>>(a, em, split);
   else if (nsl == 3)
-    scan_wave_kernel<MODE, 3, 1><<<grid, kThreads, 0, st>>>(a, em);
+    scan_wave_kernel<MODE, 3, 1><<<grid, kThreads, 0, st>>>(a, em, split);
   else
-    scan_wave_kernel<MODE, 2, 1><<<grid, kThreads, 0, st>>>(a, em);
+    scan_wave_kernel<MODE, 2, 1><<<grid, kThreads, 0, st>>>(a, em, split);
   return launch_status("scan_wave_kernel");
 }
 

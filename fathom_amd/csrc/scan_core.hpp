@@ -175,28 +175,48 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
   const int nact = s, ureal = u;
   const int U = (ureal + kSlice - 1) / kSlice * kSlice;
   const int UP = min(max(U, upad), kMaxUnits);
+  // the prologue's global loads are issued together: the class lists (every
+  // in-range entry of the bmax x D table) and the queries
   {
-    // a wave per head (the waves take heads w, w + waves, ...): its largest
-    // |q| gives sigma_h
-    const int w = tid >> 6, l = tid & 63;
-    const int nw = (int)blockDim.x >> 6;
     static_assert(kMaxD == 2 * kWave, "two channels per lane");
-    for (int h = w; h < kMaxG; h += nw) {
-      const float q0 = (h < a.G && l < a.D) ? a.q[(bh * a.G + h) * a.D + l] : 0.0f;
-      const float q1 = (h < a.G && l + 64 < a.D) ? a.q[(bh * a.G + h) * a.D + l + 64] : 0.0f;
-      sh.qs[h][l] = q0;
-      sh.qs[h][l + 64] = q1;
-      float m = fmaxf(fabsf(q0), fabsf(q1));
+    const int nthr = (int)blockDim.x;
+    const int w = tid >> 6, l = tid & 63, nw = nthr >> 6;
+    for (int i0 = tid; i0 < 4 * kMaxD; i0 += 2 * nthr) {
+      int jr[2];
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      if (l == 0) sh.sig[h] = __builtin_amdgcn_frexp_expf(m);
+      for (int u2 = 0; u2 < 2; ++u2) {
+        const int i = i0 + u2 * nthr, c = i / kMaxD, e = i % kMaxD;
+        jr[u2] = (i < 4 * kMaxD && c < a.ncls && e < a.D) ? a.cls[(bh * a.bmax + c) * a.D + e] : 0;  // no wait on nc
+      }
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2) {
+        const int i = i0 + u2 * nthr, c = i / kMaxD, e = i % kMaxD;
+        if (i < 4 * kMaxD && c < a.ncls && e < nc[c])  // slot SF[c - 1] + e (make_plan lists only valid channels)
+          sh.schan[(c == 0 ? 0 : SF[c - 1]) + e] = (uint16_t)min(max(jr[u2], 0), a.D - 1);
+      }
     }
-  }
-  for (int e = tid; e < nact; e += (int)blockDim.x) {
-    const int c = (e >= SF[0]) + (e >= SF[1]) + (e >= SF[2]);
-    const int lo = c == 0 ? 0 : SF[c - 1];
-    const int jr = a.cls[(bh * a.bmax + c) * a.D + (e - lo)];
-    sh.schan[e] = (uint16_t)min(max(jr, 0), a.D - 1);  // memory-safe; make_plan lists only valid channels
+    // a wave per head (heads w, w + nw, ...): its largest |q| gives sigma_h
+    for (int h0 = w; h0 < kMaxG; h0 += 2 * nw) {
+      float qv[2][2];
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2) {
+        const int h = h0 + u2 * nw;
+        const bool on = h < kMaxG && h < a.G;
+        qv[u2][0] = (on && l < a.D) ? a.q[(bh * a.G + h) * a.D + l] : 0.0f;
+        qv[u2][1] = (on && l + 64 < a.D) ? a.q[(bh * a.G + h) * a.D + l + 64] : 0.0f;
+      }
+#pragma unroll
+      for (int u2 = 0; u2 < 2; ++u2) {
+        const int h = h0 + u2 * nw;
+        if (h >= kMaxG) continue;  // uniform
+        sh.qs[h][l] = qv[u2][0];
+        sh.qs[h][l + 64] = qv[u2][1];
+        float m = fmaxf(fabsf(qv[u2][0]), fabsf(qv[u2][1]));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (l == 0) sh.sig[h] = __builtin_amdgcn_frexp_expf(m);
+      }
+    }
   }
   if (tid == 0) {
     sh.U = U;
@@ -747,9 +767,9 @@ __device__ __forceinline__ void tile_setup(EmitState &es, const Emit &em, const 
     for (int i = 0; i < 2; ++i) {
       es.head[i] = rk.head[i];
       es.thr[i] = rk.thr[i];
-      const float X = !es.head[i] ? INFINITY
-                      : es.plain  ? acc_threshold(es.thr[i], k.C[i], k.fe[i])
-                                  : __int_as_float(0x7FC00000);
+      // masked tiles too: a masked token scores -inf in the exact check, so
+      // only thr = -inf (X = -inf: every token) lets one through
+      const float X = es.head[i] ? acc_threshold(es.thr[i], k.C[i], k.fe[i]) : INFINITY;
       // T_w = T_0 2^(e_w - e_0) exactly (a threshold past the float range
       // becomes +inf, which no finite accumulator reaches)
       es.T[i][0] = hi_threshold(X, k.fe[i], 0, M[i]);
