@@ -14,7 +14,8 @@ resident in HBM (n * BH / t_scan_topk, t_scan_topk the GPU time of one fused
 call: 20 calls captured in one HIP graph, replayed for 30 ms before 10 timed
 replays, checked equal to the eager call).
 The roofline object is for the dominant kernel of that call, the candidate
-pass (scan_wave_kernel<1, 2>), run on its own through the stage entry point
+pass (scan_wave_kernel<2, NS, 1>, NS the plan's slices of 16 units held in
+registers), run on its own through the stage entry point
 (20 launches in one HIP graph, events on the launching stream; algorithmic
 bytes = bytes_planes), with the whole call's and the whole step's fractions
 and the instruction-issue ceiling beside it.  The same step with the plane
@@ -42,7 +43,14 @@ HOST_SUB = 64                 # superblock of the host-resident store (a multipl
 SIMDS = 256 * 4               # MI355X: 256 CUs x 4 SIMDs
 CLOCK_HZ = 2.4e9              # MI355X peak engine clock
 VALU_CYCLES = 4               # a wave64 VALU instruction occupies a 16-lane SIMD 4 cycles
-CAND_KERNEL = "scan_wave_kernel<1, 2>"
+
+
+def cand_kernel(units_max):
+    """The candidate pass's kernel for a plan bound (scan.hip launch_scan)."""
+    nsl = -(-int(units_max) // 16)
+    if units_max <= 0 or nsl > 4:
+        return "scan_wave_kernel<2, 4, 4>"
+    return f"scan_wave_kernel<2, {max(nsl, 2)}, 1>"
 
 
 def parse():
@@ -454,32 +462,40 @@ def read_traffic():
 
 def issue_ceiling(scan_bytes, blockrows, achieved):
     """Instruction-issue ceiling of the candidate pass from its committed
-    rocprofv3 --pmc counts (per launch): the VALU instructions other than MFMA
-    occupy a SIMD VALU_CYCLES cycles each, the MFMAs their measured busy
-    cycles; spread evenly over the chip's SIMDs at the peak clock, the larger
-    of the two is the shortest time the launch could take, and
-    algorithmic bytes / that time the highest rate it could reach."""
+    rocprofv3 --pmc counts (per launch), no-overlap model: every VALU
+    instruction other than an MFMA holds its SIMD VALU_CYCLES cycles (a wave64
+    instruction on 16 lanes), each MFMA its measured busy cycles
+    (SQ_VALU_MFMA_BUSY_CYCLES), and the two do not overlap; spread evenly over
+    the chip's SIMDs at the peak clock, their sum is the shortest time the
+    launch could take, and algorithmic bytes / that time the highest rate it
+    could reach.  The overlapped bound (the larger of the two alone) is
+    reported beside it."""
     c = _profile_lines("scan_c3_candidate_counters.md")
     if not {"SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES"} <= set(c):
         return None
     valu, mfma = c["SQ_INSTS_VALU"], c["SQ_INSTS_MFMA"]
     valu_s = VALU_CYCLES * (valu - mfma) / (SIMDS * CLOCK_HZ)
     mfma_s = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (SIMDS * CLOCK_HZ)
-    t = max(valu_s, mfma_s)
+    t = valu_s + mfma_s
     ceil = scan_bytes / t / 1e9
-    return {"valu_per_block_row": valu / blockrows, "mfma_per_block_row": mfma / blockrows,
+    ceil_ov = scan_bytes / max(valu_s, mfma_s) / 1e9
+    return {"model": "no overlap: non-MFMA VALU x 4 cycles + measured MFMA busy cycles, per SIMD at 2.4 GHz",
+            "valu_per_block_row": valu / blockrows, "mfma_per_block_row": mfma / blockrows,
+            "non_mfma_valu_per_block_row": (valu - mfma) / blockrows,
             "salu_per_block_row": c.get("SQ_INSTS_SALU", 0.0) / blockrows,
-            "valu_issue_us": valu_s * 1e6, "mfma_busy_us": mfma_s * 1e6,
+            "valu_issue_us": valu_s * 1e6, "mfma_busy_us": mfma_s * 1e6, "issue_us": t * 1e6,
             "ceiling_GBps": ceil, "frac_of_ceiling": achieved / ceil,
+            "overlapped_ceiling_GBps": ceil_ov,
             "source": "profiles/scan_c3_candidate_counters.md (per-launch counts, C3 shape)"}
 
 
-def cpu_baseline(W):
+def cpu_baseline(W, x3):
     """The reference's torch CPU path (scripts/sketch.py:110-131 planes branch:
     water-filling plan + per-level qblock contraction; then the exact sink/local
-    top-k with torch.topk), restated in oracle/sketch_torch.py, on one KV head
-    (G query heads) of the same synthetic distribution: the C3 shape at all
-    threads and, bounded, a quarter of it at 1 thread; C1 at both."""
+    top-k with torch.topk), restated in oracle/sketch_torch.py, timed on the GPU
+    run's own bytes: KV head 0 of the C3 inputs (keys, queries, variances copied
+    back from the device) at all threads and, bounded, its first quarter at 1
+    thread; C1 (not a GPU leg) generated on the CPU, at both."""
     import torch
     from oracle import sketch_torch as S
 
@@ -489,9 +505,11 @@ def cpu_baseline(W):
         threads_all = min(threads_all, int(env))  # the box's CPU share
     saved = torch.get_num_threads()
 
-    def timed(x, threads, reps=5):
+    def timed(x, threads, reps=5, n=None):
         torch.set_num_threads(threads)
         K, q, var = x["K"][0].float(), x["q"][0].float(), x["var"][0].float()
+        if n is not None:
+            K = K[:n].contiguous()
         ts = []
         for _ in range(reps + 1):
             t0 = time.perf_counter()
@@ -501,23 +519,23 @@ def cpu_baseline(W):
         return {"tokens_per_s": K.shape[0] / med, "s": med, "n": K.shape[0], "G": q.shape[0], "threads": threads}
 
     try:
-        x3 = W.config_inputs(3, device="cpu", BH=1)
-        c3_all = timed(x3, threads_all)
-        del x3
-        x3q = W.config_inputs(3, device="cpu", BH=1, n=1 << 18)
-        c3_one = timed(x3q, 1)
-        del x3q
+        xc = {"K": x3["K"][:1].cpu(), "q": x3["q"][:1].cpu(), "var": x3["var"][:1].cpu(),
+              "budget": x3["budget"], "k": x3["k"], "sink": x3["sink"], "local": x3["local"]}
+        c3_all = timed(xc, threads_all)
+        c3_one = timed(xc, 1, n=1 << 18)
+        del xc
         x1 = W.config_inputs(1, device="cpu")
         c1_all, c1_one = timed(x1, threads_all), timed(x1, 1)
     finally:
         torch.set_num_threads(saved)
     return {"value": c3_all["tokens_per_s"], "unit": "token*heads/s", "cores": threads_all, "kind": "port",
-            "sample": f"torch restatement of scripts/sketch.py:110-131 + torch.topk sink/local top-k, one KV head "
-                      f"(G={c3_all['G']}) x {c3_all['n']} tokens of the C3 distribution, B=48, k=512, "
-                      f"torch.set_num_threads({threads_all}) (os.cpu_count()={os.cpu_count()}), "
-                      f"median of 5 after 1 warm-up: {c3_all['s']:.3f} s",
-            "single_thread": dict(c3_one, sample="C3 distribution, 262144 tokens (a quarter of the C3 row), 1 thread"),
-            "config1": {"all_threads": c1_all, "single_thread": c1_one}}
+            "sample": f"torch restatement of scripts/sketch.py:110-131 + torch.topk sink/local top-k on the GPU "
+                      f"run's own bytes: KV head 0 of the C3 inputs (G={c3_all['G']} query heads x {c3_all['n']} "
+                      f"tokens, copied back from the device), B=48, k=512, torch.set_num_threads({threads_all}) "
+                      f"(os.cpu_count()={os.cpu_count()}), median of 5 after 1 warm-up: {c3_all['s']:.3f} s",
+            "single_thread": dict(c3_one, sample="the same row's first 262144 tokens (a quarter), 1 thread"),
+            "config1": {"all_threads": c1_all, "single_thread": c1_one,
+                        "sample": "C1 generated on the CPU (C1 is not a GPU leg of this run)"}}
 
 
 def calib_copy(torch, dev, mib):
@@ -730,14 +748,15 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        cpu = cpu_baseline(W)
+        cpu = cpu_baseline(W, x)
         log(f"[bench] cpu baseline: {json.dumps(cpu)}")
 
     rec = {
         "metric": "scanned tokens/s/GPU (scan+top-k) at 1M ctx",
         "value": value, "unit": "token*heads/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": st["plan"] + st["scan_topk"] + st.get("attn", 0.0), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (seeded lognormal-scaled keys, planted keys; no model weights)",
+        "dtype": "f32 accumulate (f16 hi + lo split query weights, 21 significant bits, times exact f16 block scales)",
+        "data": "synthetic (seeded lognormal-scaled keys, planted keys; no model weights)",
         "config": {"workload": W.CONFIGS[a.config]["name"] + ", index + rows in HBM", "BH": BH, "G": x["G"],
                    "n": n, "budget_bits": x["budget"], "k": x["k"], "sink": x["sink"], "local": x["local"],
                    "bits_per_token": round(hbm["bits_per_token"], 3), "parallelism": "single GPU"},
@@ -745,7 +764,8 @@ def main():
         "scan_topk_ms": scan_topk_ms,
         "scan_topk_timing": "20 fused calls captured in one HIP graph, 10 replays after 30 ms of warm-up replays (eager per-stage time: stage_ms)",
         "unfused_scan_plus_topk_ms": st["scan"] + st["topk"],
-        "roofline": {"bound": "hbm", "kernel": CAND_KERNEL + " (candidate pass of the fused scan + top-k)",
+        "roofline": {"bound": "hbm",
+                     "kernel": cand_kernel(hbm["plan"].get("units_max", 0)) + " (candidate pass of the fused scan + top-k)",
                      "achieved": achieved, "launch_ms": cand_ms, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": read_traffic(),
                      "algorithmic_bytes_per_launch": hbm["scan_bytes"],
@@ -761,6 +781,14 @@ def main():
                          "what": "make_plan + fused scan/top-k + attention over the union-gathered rows, one HIP "
                                  "graph; bytes = plane/scale bytes + distinct K/V rows"},
                      "scores_mode_scan_ms": scan_ms},
+        "roofline_pcie": None if host is None else {
+            "what": "config 3 as written: plane index and K/V rows in mapped pinned host memory, the scan and "
+                    "the row gather reading them zero-copy over PCIe",
+            "bound": "pcie", "achieved": host["pcie_GBps_step"], "peak": PCIE_PEAK_GBPS, "unit": "GB/s",
+            "frac": host["roofline_pcie"]["frac_step"], "frac_scan": host["roofline_pcie"]["frac_scan"],
+            "step_ms": host["step_ms"], "scan_topk_ms": host["stage_ms"]["scan_topk"],
+            "measured_h2d_memcpy_GBps": host["measured_h2d_memcpy_GBps"],
+            "index_sets_equal_hbm": host["index_sets_equal_hbm"]},
         "host_resident": host,
         "decode_step": decode,
         "kernel_table": ktab,

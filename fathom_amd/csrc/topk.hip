@@ -1025,7 +1025,7 @@ __device__ __forceinline__ void two_bounds(const uint32_t (&v)[PER], int cnt, ui
 // its r_hi-th largest (r_hi <= kk, so T_hi >= T_lo up to the bounds' bins).
 // The sample is a subset of the row, so T_lo never exceeds the row's kk-th
 // largest: every element of the row's top kk has key >= T_lo.  Also clears
-// the row's candidate counters.
+// the row's candidate counters (list layout; the region layout has none).
 template <int PER>
 __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t *__restrict__ samp,
                                                                   int64_t samp_cap, uint32_t kk, uint32_t r_hi,
@@ -1047,8 +1047,10 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
   if (threadIdx.x == 0) {
     s.thr[row] = r_hi < kk ? t_hi : t_lo;
     s.thr_lo[row] = t_lo;
-    *s.cnt1(row) = 0u;
-    *s.cnt2(row) = 0u;
+    if (!s.rc1) {  // the list layout's filter passes append at these counters
+      *s.cnt1(row) = 0u;
+      *s.cnt2(row) = 0u;
+    }
   }
 }
 

@@ -8,7 +8,7 @@
 * gather_union: the decode step's union of the G query heads' selections --
   every distinct host row is read once, duplicates are filled on the device,
   recent tokens (index >= n) come from a device buffer.
-* select_and_gather: plan -> scan -> sink/local top-k -> union gather, the
+* select_and_gather: plan -> fused scan + sink/local top-k -> union gather, the
   selection half of offload_attn (scripts/B_e2e_offload_v2.py:163-242).
 * chunk_bounds / stream_planes / stream_chan4: the chunked two-stream pipeline
   (scripts/B_e2e_offload_v2.py:103-144): chunk c + 1's runs cross PCIe on a copy
@@ -309,16 +309,25 @@ def gather_attn(q, Kc, Vc, idx):
 
 
 def select_and_gather(store, q, var, budget, k, Ksrc, Vsrc, sink=4, local=32, m=None, Krec=None, Vrec=None,
-                      dtype=torch.bfloat16):
+                      dtype=torch.bfloat16, scores=False):
     """One decode step's selection for all (batch, KV head) rows: g = sum_g q^2 var,
     plan, scan over `store` (HBM or host-resident), sink/local top-k, union row
     gather.  q [BH, G, D] fp32, var [BH, D].  Returns dict(plan, scores, idx, K, V,
-    n_unique) -- scripts/B_e2e_offload_v2.py:181, 203, 224-241."""
+    n_unique) -- scripts/B_e2e_offload_v2.py:181, 203, 224-241.
+
+    The selection is the fused scan + top-k (store.scan_topk: no score tensor,
+    "scores" is None); scores=True runs the reference's two steps instead (the
+    score rows, then sink_local_topk of them) and returns the scores too.  Both
+    select the same indices."""
     g = ((q.float() ** 2) * var[:, None, :]).sum(1)
     plan = make_plan(g, budget)
-    scores = store.scan(q, plan)
     n = store.n
     m = n if m is None else m
-    idx = sink_local_topk(scores, k, sink, local, m=m)
+    if scores:
+        scores = store.scan(q, plan)
+        idx = sink_local_topk(scores, k, sink, local, m=m)
+    else:
+        scores = None
+        idx = store.scan_topk(q, plan, k, sink, local, m=m)
     Ks, Vs, nu = gather_union(idx, n, Ksrc, Vsrc, n, Krec, Vrec, dtype=dtype, d=q.shape[-1])
     return {"plan": plan, "scores": scores, "idx": idx, "K": Ks, "V": Vs, "n_unique": nu}

@@ -212,7 +212,10 @@ int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, co
  * rejected with FATHOM_ERR_WORKSPACE before any launch.  The call allocates
  * nothing (no hipMalloc, no library allocation).  Calls that overlap on one
  * device (several streams or threads) share the array and race.  Results are
- * those of fathom_scan_topk on the same arguments.
+ * those of fathom_scan_topk on the same arguments.  The array's device address
+ * is looked up on a device's first call and kept: make one call on a device
+ * before capturing the call in a graph, and do not call it again on a device
+ * after hipDeviceReset (the kept address no longer names the array).
  */
 #define FATHOM_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls,

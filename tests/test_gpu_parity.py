@@ -395,7 +395,7 @@ def test_select_and_gather_matches_oracle(host):
     """select_and_gather (one decode step's selection, scripts/B_e2e_offload_v2.py:
     181, 203, 224-241) over an HBM or host-resident store: plan, scores, indices
     and union rows against the oracle (indices given the GPU scores, rows given
-    the indices)."""
+    the indices); the default fused selection returns the same indices and rows."""
     print(f"[select_and_gather] host={host}", flush=True)
     x = W.config_inputs(2, n=40000, BH=2)
     K = x["K"]
@@ -416,8 +416,13 @@ def test_select_and_gather_matches_oracle(host):
         else:
             Ksrc, Vsrc = K.to(DEV), V.to(DEV)
         r = off.select_and_gather(st, x["q"].to(DEV), x["var"].to(DEV), x["budget"], 512, Ksrc, Vsrc,
-                                  x["sink"], x["local"])
+                                  x["sink"], x["local"], scores=True)
+        fused = off.select_and_gather(st, x["q"].to(DEV), x["var"].to(DEV), x["budget"], 512, Ksrc, Vsrc,
+                                      x["sink"], x["local"])
         torch.cuda.synchronize()
+        assert fused["scores"] is None
+        for key in ("idx", "K", "V", "n_unique"):  # the default (fused) selection is the same
+            torch.testing.assert_close(fused[key], r[key], rtol=0, atol=0)
         qd, vd = x["q"].to(DEV).float(), x["var"].to(DEV)
         g = ((qd ** 2) * vd[:, None, :]).sum(1)          # the gain as select_and_gather forms it
         pr = O.make_plan(g.cpu().numpy(), x["budget"])
