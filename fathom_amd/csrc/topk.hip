@@ -199,15 +199,16 @@ __device__ __forceinline__ void block_rank_desc(const uint64_t (&v)[E], uint64_t
 // values placed in bin order).  Values crowd a bin only where their range is
 // dominated by a few outliers: then (more than kCrowd in one bin) the ranks
 // come from block_rank_desc over the first nlim slots instead.  put(rank, v)
-// is called for every valid value.  scratch: LDS of 4096 values.
+// is called for every valid value.  scratch: LDS of max(E * 1024 + 2048,
+// 2 * nlim) values.
 constexpr uint32_t kCrowd = 48;
 template <int E, typename Put>
 __device__ __forceinline__ void bin_rank_desc(const uint64_t (&v)[E], int cnt, uint64_t *scratch, RangeShared &sh,
                                               int nlim, Put put) {
   static_assert(kBins == 2 * kFinThreads, "two bins per thread");
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = kFinThreads >> 6;
-  uint64_t *placed = scratch;                                           // [2048] values in bin order
-  uint32_t *hist = reinterpret_cast<uint32_t *>(scratch + kBins);       // [2048] values per bin
+  uint64_t *placed = scratch;                                           // [E * 1024] values in bin order
+  uint32_t *hist = reinterpret_cast<uint32_t *>(scratch + E * 1024);    // [2048] values per bin
   uint32_t *above = hist + kBins;                                       // [2048] values in higher bins
   uint64_t mn = ~0ull, mx = 0ull;
 #pragma unroll
@@ -247,7 +248,7 @@ __device__ __forceinline__ void bin_rank_desc(const uint64_t (&v)[E], int cnt, u
   if (c0 > kCrowd || c1 > kCrowd) sh.fcnt = 1u;  // any thread: the same value
   __syncthreads();
   if (sh.fcnt) {  // uniform
-    block_rank_desc<E>(v, scratch, scratch + 2 * kFinThreads, nlim, [&](int rank, uint64_t x) {
+    block_rank_desc<E>(v, scratch, scratch + nlim, nlim, [&](int rank, uint64_t x) {
       if (rank < cnt) put(rank, x);
     });
     return;
@@ -725,10 +726,28 @@ __global__ __launch_bounds__(kFinThreads) void finalize_fused_kernel(int64_t m, 
     src.rc = s.rc2 + row * s.nreg;
     cnt = stage_regions(src.rc, gc, s.nreg, cl, (uint32_t)kCandLds, pre, sh);
   }
-  if (cnt <= (uint32_t)kCandLds)
+  if (cnt <= (uint32_t)(4 * kFinThreads)) {  // uniform
+    // every candidate ranked at once (a few times kk of them): the top kk by
+    // rank, written in order
+    uint64_t v4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t i = threadIdx.x + (uint32_t)e * kFinThreads;
+      v4[e] = i < cnt ? cl[i] : 0ull;
+    }
+    __syncthreads();  // cl is the ranking scratch from here
+    int nlim = kWave;
+    while (nlim < (int)cnt) nlim <<= 1;
+    const int got = (int64_t)cnt < kk ? (int)cnt : (int)kk;
+    bin_rank_desc<4>(v4, (int)cnt, cl, sh, nlim, [&](int rank, uint64_t x) {
+      if (rank < got) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x);
+    });
+    write_fixed(out, got, kk, m, sink, local);
+  } else if (cnt <= (uint32_t)kCandLds) {
     select_sorted(ArraySrc{cl, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
-  else
+  } else {
     select_sorted(src, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
+  }
 }
 
 // Exact top kk of a whole score row (rows up to kRowSelectMax): every element
@@ -960,17 +979,20 @@ __device__ __forceinline__ void two_bins(const uint32_t *hist, uint32_t na, uint
 // both ranks: 2048 bins over [min, max], then 2048 bins over each rank's bin
 // (the second histogram in hist2).  Each bound is the lower edge of the final
 // bin that holds its rank: at least that many values reach it, and it lies
-// within (max - min) / 2^22 of the value of that rank.
+// within (max - min) / 2^22 of the value of that rank.  Only values >= floor
+// take part (floor must not exceed the na-th largest value: the ranks are the
+// same among them), so a floor near the ranks keeps the bins narrow and the
+// histogram atomics few.
 template <int PER>
 __device__ __forceinline__ void two_bounds(const uint32_t (&v)[PER], int cnt, uint32_t na, uint32_t nb,
                                            RangeShared &sh, uint32_t *hist2, uint32_t *s_sel, uint32_t &ta,
-                                           uint32_t &tb) {
+                                           uint32_t &tb, uint32_t floor = 0u) {
   static_assert(kBins == 2 * kFinThreads, "two bins per thread");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
   uint32_t mn = ~0u, mx = 0u;
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    if (tid + u * kFinThreads < cnt) {
+    if (tid + u * kFinThreads < cnt && v[u] >= floor) {
       mn = min(mn, v[u]);
       mx = max(mx, v[u]);
     }
@@ -992,7 +1014,7 @@ __device__ __forceinline__ void two_bounds(const uint32_t (&v)[PER], int cnt, ui
   const int sft = bl > 11 ? bl - 11 : 0;  // (v - lo) >> sft < 2048
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    if (tid + u * kFinThreads < cnt) atomicAdd(&sh.hist[(v[u] - lo) >> sft], 1u);
+    if (tid + u * kFinThreads < cnt && v[u] >= floor) atomicAdd(&sh.hist[(v[u] - lo) >> sft], 1u);
   __syncthreads();
   uint32_t sel[2], above[2];
   two_bins(sh.hist, na, nb, sh, sel, above, s_sel);
@@ -1007,7 +1029,7 @@ __device__ __forceinline__ void two_bounds(const uint32_t (&v)[PER], int cnt, ui
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    if (tid + u * kFinThreads < cnt) {
+    if (tid + u * kFinThreads < cnt && v[u] >= floor) {
       const uint32_t b = (v[u] - lo) >> sft;
       if (b == sel[0]) atomicAdd(&sh.hist[(v[u] - base_a) >> sft2], 1u);
       if (b == sel[1]) atomicAdd(&hist2[(v[u] - base_b) >> sft2], 1u);
@@ -1048,6 +1070,48 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
     s.thr[row] = r_hi < kk ? t_hi : t_lo;
     s.thr_lo[row] = t_lo;
     if (!s.rc1) {  // the list layout's filter passes append at these counters
+      *s.cnt1(row) = 0u;
+      *s.cnt2(row) = 0u;
+    }
+  }
+}
+
+// The same thresholds from the maxima of the sample's 16-key groups (thread t
+// holds groups t + 1024 u): each maximum is a sampled key, so the kk-th
+// largest maximum bounds the sample's kk-th largest key from below (T_lo stays
+// safe), and T_hi only falls (more candidates) where a group holds several of
+// the top r_hi keys -- rare when kk is at most a quarter of the groups, the
+// launch's condition.  Ranks 16 times fewer values than select_keys_kernel.
+template <int PER>
+__global__ __launch_bounds__(kSelThreads) void select_groups_kernel(const uint32_t *__restrict__ samp,
+                                                                    int64_t samp_cap, uint32_t kk, uint32_t r_hi,
+                                                                    TopkSel s) {
+  __shared__ RangeShared sh;
+  __shared__ uint32_t hist2[kBins];
+  __shared__ uint32_t s_sel[4];
+  const int64_t row = blockIdx.x;
+  const uint4 *src = reinterpret_cast<const uint4 *>(samp + row * samp_cap);
+  const int ng = (int)(samp_cap / 16);
+  uint32_t g[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = (int)threadIdx.x + u * kSelThreads;
+    uint4 q[4] = {};
+    if (i < ng) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[j] = src[4 * i + j];
+    }
+    uint32_t m = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = max(m, max(max(q[j].x, q[j].y), max(q[j].z, q[j].w)));
+    g[u] = m;
+  }
+  uint32_t t_lo = 0u, t_hi = 0u;
+  two_bounds<PER>(g, ng, kk, r_hi < kk ? r_hi : kk, sh, hist2, s_sel, t_lo, t_hi);
+  if (threadIdx.x == 0) {
+    s.thr[row] = r_hi < kk ? t_hi : t_lo;
+    s.thr_lo[row] = t_lo;
+    if (!s.rc1) {
       *s.cnt1(row) = 0u;
       *s.cnt2(row) = 0u;
     }
@@ -1229,6 +1293,16 @@ int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int
   if (samp_cap > kMaxSample) return fail(FATHOM_ERR_INVALID, "select: %lld sampled keys exceed %lld", (long long)samp_cap, (long long)kMaxSample);
   const unsigned g = (unsigned)rows;
   const uint32_t ukk = (uint32_t)kk, urh = (uint32_t)r_hi;
+  const int64_t ng = samp_cap / 16;
+  if (samp_cap % 16 == 0 && ng >= 4 * kk && kk > 0) {  // 16-key group maxima (see select_groups_kernel)
+    if (ng <= kSelThreads)
+      select_groups_kernel<1><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+    else if (ng <= 2 * kSelThreads)
+      select_groups_kernel<2><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+    else
+      select_groups_kernel<4><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+    return launch_status("select_groups_kernel");
+  }
   if (samp_cap <= 8 * kSelThreads)
     select_keys_kernel<8><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
   else if (samp_cap <= 16 * kSelThreads)

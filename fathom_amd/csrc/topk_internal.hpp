@@ -4,9 +4,9 @@
 //   select    from a sample of the row (tiles of 2048 tokens, every S-th
 //             tile): T_lo, a lower bound of the sample's kk-th largest key,
 //             and T_hi, a lower bound of its r-th largest, r = about
-//             kAlpha * kk * (sample size / n).  A sample is a subset of the
+//             kAlphaX2 / 2 * kk * (sample size / n).  A sample is a subset of the
 //             row, so T_lo never exceeds the row's kk-th largest key; T_hi is
-//             a guess that about kAlpha * kk elements of the row reach;
+//             a guess that about kAlphaX2 / 2 * kk elements of the row reach;
 //   filter    elements with key >= T_hi become the row's candidates.  If there
 //             are at least kk, T_hi <= the row's kk-th largest key and they
 //             hold the whole top kk;
@@ -35,7 +35,8 @@ constexpr int64_t kTileTok = 2048;  // tokens per sample tile of the score-row t
 constexpr int64_t kRegTok = 1024;   // tokens per candidate region and sample tile of the fused scan (one wave-tile)
 constexpr int64_t kMaxSample = 65536; // sampled keys per row (held in registers by select)
 
-constexpr int64_t kAlpha = 4;  // expected first-pass candidates per row, in units of kk
+// expected first-pass candidates per row, in units of kk: kAlphaX2 / 2
+constexpr int64_t kAlphaX2 = 5;
 
 // Score rows up to this length (their 32-bit keys fit in one workgroup's LDS)
 // select their top kk in one kernel, one workgroup per row, instead of
@@ -67,16 +68,18 @@ struct TopkSel {
 };
 
 // Sample stride in tiles of `tile` tokens: about 16384 sampled tokens per row
-// (8192 for the fused scan's wave-tiles: a launch of half the workgroups for
-// its latency-bound sample pass), more where the sample must hold 2 kk keys
-// or where about 16 sampled keys must reach the first-pass threshold (kAlpha *
-// kk * sample / n >= 16), at most kMaxSample keys.  The stride rounds up, so
-// the sample never exceeds that many tiles.
+// (32768 for the fused scan's wave-tiles, whose first-pass threshold then sits
+// at about 40 sampled keys for 1M-token rows: a fallback rescan of a row, the
+// price of a threshold above the row's kk-th key, stays below 1e-6 per row),
+// more where the sample must hold 2 kk keys or where about 16 sampled keys must
+// reach the first-pass threshold (kAlphaX2 / 2 * kk * sample / n >= 16), at
+// most kMaxSample keys.  The stride rounds up, so the sample never exceeds
+// that many tiles.
 inline int64_t topk_tile_stride(int64_t n, int64_t kk, int64_t tile) {
   const int64_t ntiles = cdiv(n, tile);
-  int64_t want = tile == kRegTok ? 8 : cdiv(8 * kTileTok, tile);
+  int64_t want = tile == kRegTok ? 32 : cdiv(8 * kTileTok, tile);
   if (kk > 0) {
-    const int64_t a = cdiv(2 * kk, tile), b = cdiv(16 * n, kAlpha * kk * tile);
+    const int64_t a = cdiv(2 * kk, tile), b = cdiv(32 * n, kAlphaX2 * kk * tile);
     want = a > want ? a : want;
     want = b > want ? b : want;
   }
@@ -88,7 +91,7 @@ inline int64_t topk_tile_stride(int64_t n, int64_t kk, int64_t tile) {
 
 inline int64_t topk_sample_tiles(int64_t n, int64_t S, int64_t tile) { return cdiv(cdiv(n, tile), S); }
 
-// Rank in the sample of the first-pass threshold: about kAlpha * kk of the row's
+// Rank in the sample of the first-pass threshold: about kAlphaX2 / 2 * kk of the row's
 // n elements are expected at or above it (kk when the sample is the row).
 inline int64_t topk_hi_rank(int64_t n, int64_t S, int64_t kk, int64_t tile) {
   int64_t sampled = 0;
@@ -96,7 +99,7 @@ inline int64_t topk_hi_rank(int64_t n, int64_t S, int64_t kk, int64_t tile) {
     const int64_t left = n - t * S * tile;
     sampled += left < tile ? (left > 0 ? left : 0) : tile;
   }
-  const int64_t r = (kAlpha * kk * sampled + n - 1) / n;
+  const int64_t r = (kAlphaX2 * kk * sampled + 2 * n - 1) / (2 * n);
   return r < 1 ? 1 : (r > kk ? kk : r);
 }
 
