@@ -217,7 +217,7 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
     if (rc) return rc;
   }
   if (stages & FATHOM_STAGE_SELECT) {
-    rc = launch_select_keys(em.samp, rows, em.samp_cap, kk, r_hi, em.sel, st);
+    rc = launch_select_groups(em.samp, rows, em.samp_cap, kk, r_hi, em.sel, st);
     if (rc) return rc;
   }
   if (stages & FATHOM_STAGE_CANDIDATES) {

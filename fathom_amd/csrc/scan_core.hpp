@@ -551,6 +551,7 @@ struct EmitState {
   uint32_t off[2];     // candidates written so far into the tile's region (per head)
   float gm[2];         // group maxima: running max of the quarter's masked scores
   bool gnan[2];
+  uint32_t gk[2];      // sample pass: running max of the quarter's masked keys
   bool head[2];        // the slot's head is in the row and not skipped
   bool plain;          // no masking anywhere in the tile
   // tile-relative token intervals (wave-uniform): tokens of the scanned range
@@ -666,25 +667,28 @@ __device__ __forceinline__ void store_scores(const Emit &em, const ScanArgs &a, 
   }
 }
 
-// Sampled keys of step group V of quarter qs of list entry L (sink/local
-// masked, 0 beyond the row).
-__device__ __forceinline__ void store_sample(const Emit &em, const ScanArgs &a, const float (&s4)[2][4], int64_t bh,
-                                             int64_t beta0, int64_t L, int qs, int V, int lane) {
+// Sampled keys of step group V of quarter qs of list entry L: each lane keeps
+// the largest key of its 16 tokens of the quarter (sink/local masked to -inf,
+// 0 beyond the row) and writes it once the quarter ends -- 64 group maxima per
+// tile and head, [L][block][quarter].
+__device__ __forceinline__ void store_sample(const Emit &em, const ScanArgs &a, const float (&s4)[2][4], EmitState &es,
+                                             int64_t bh, int64_t beta0, int64_t L, int qs, int V, int lane) {
   const int c = lane & 15, gp = lane >> 4;
   const int64_t t4 = (beta0 + c) * kBlk + 16 * qs + 4 * V;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int h = 2 * gp + i;
     if (h >= a.G) continue;
-    uint32_t key[4];
+    if (V == 3) es.gk[i] = 0u;  // a quarter's step groups come V = 3 first, V = 0 last
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const int64_t tok = t4 + w;
       const bool masked = tok < em.sink || tok >= em.lstart;
-      key[w] = tok < a.n ? (masked ? kKeyNegInf : score_key(s4[i][w])) : 0u;
+      const uint32_t key = tok < a.n ? (masked ? kKeyNegInf : score_key(s4[i][w])) : 0u;
+      es.gk[i] = max(es.gk[i], key);
     }
-    uint32_t *dst = em.samp + (bh * a.G + h) * em.samp_cap + L * kWTok + c * kBlk + 16 * qs + 4 * V;
-    *reinterpret_cast<uint4 *>(dst) = make_uint4(key[0], key[1], key[2], key[3]);
+    if (V == 0)
+      em.samp[(bh * a.G + h) * em.samp_cap + L * (kWTok / kGroupTok) + c * kQS + qs] = es.gk[i];
   }
 }
 
@@ -714,7 +718,7 @@ __device__ __forceinline__ void emit_flush(const Emit &em, const ScanArgs &a, Em
                                            int64_t bh, int64_t beta0, int64_t L, int qs, int V, int lane) {
   if constexpr (MODE == kEmitScores) store_scores<false>(em, a, o.s4, es, bh, beta0, qs, V, lane);
   if constexpr (MODE == kEmitScoresMax) store_scores<true>(em, a, o.s4, es, bh, beta0, qs, V, lane);
-  if constexpr (MODE == kEmitSample) store_sample(em, a, o.s4, bh, beta0, L, qs, V, lane);
+  if constexpr (MODE == kEmitSample) store_sample(em, a, o.s4, es, bh, beta0, L, qs, V, lane);
 }
 
 // ------------------------------------------------------------------ tile loop

@@ -1082,7 +1082,9 @@ __global__ __launch_bounds__(kSelThreads) void select_keys_kernel(const uint32_t
 // safe), and T_hi only falls (more candidates) where a group holds several of
 // the top r_hi keys -- rare when kk is at most a quarter of the groups, the
 // launch's condition.  Ranks 16 times fewer values than select_keys_kernel.
-template <int PER>
+// DIRECT: samp already holds group maxima (the fused scan's sample, samp_cap
+// of them per row), ranked as they are.
+template <int PER, bool DIRECT>
 __global__ __launch_bounds__(kSelThreads) void select_groups_kernel(const uint32_t *__restrict__ samp,
                                                                     int64_t samp_cap, uint32_t kk, uint32_t r_hi,
                                                                     TopkSel s) {
@@ -1090,24 +1092,33 @@ __global__ __launch_bounds__(kSelThreads) void select_groups_kernel(const uint32
   __shared__ uint32_t hist2[kBins];
   __shared__ uint32_t s_sel[4];
   const int64_t row = blockIdx.x;
-  const uint4 *src = reinterpret_cast<const uint4 *>(samp + row * samp_cap);
-  const int ng = (int)(samp_cap / 16);
+  const int ng = (int)(DIRECT ? samp_cap : samp_cap / 16);
   uint32_t g[PER];
+  if constexpr (DIRECT) {
+    const uint32_t *src = samp + row * samp_cap;
 #pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int i = (int)threadIdx.x + u * kSelThreads;
-    uint4 q[4] = {};
-    if (i < ng) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) q[j] = src[4 * i + j];
+    for (int u = 0; u < PER; ++u) {
+      const int i = (int)threadIdx.x + u * kSelThreads;
+      g[u] = i < ng ? src[i] : 0u;
     }
-    uint32_t m = 0u;
+  } else {
+    const uint4 *src = reinterpret_cast<const uint4 *>(samp + row * samp_cap);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) m = max(m, max(max(q[j].x, q[j].y), max(q[j].z, q[j].w)));
-    g[u] = m;
+    for (int u = 0; u < PER; ++u) {
+      const int i = (int)threadIdx.x + u * kSelThreads;
+      uint4 q[4] = {};
+      if (i < ng) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = src[4 * i + j];
+      }
+      uint32_t m = 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m = max(m, max(max(q[j].x, q[j].y), max(q[j].z, q[j].w)));
+      g[u] = m;
+    }
   }
-  uint32_t t_lo = 0u, t_hi = 0u;
-  two_bounds<PER>(g, ng, kk, r_hi < kk ? r_hi : kk, sh, hist2, s_sel, t_lo, t_hi);
+  uint32_t t_lo = 0u, t_hi = 0u;  // fewer values than kk: every element is a candidate
+  if (ng >= (int)kk && kk > 0) two_bounds<PER>(g, ng, kk, r_hi < kk ? r_hi : kk, sh, hist2, s_sel, t_lo, t_hi);
   if (threadIdx.x == 0) {
     s.thr[row] = r_hi < kk ? t_hi : t_lo;
     s.thr_lo[row] = t_lo;
@@ -1279,7 +1290,9 @@ size_t topk_layout(int64_t rows, int64_t n, int64_t k, bool regions, char *base,
   const int64_t kk = k > 0 ? k : 0;
   const int64_t tile = regions ? kRegTok : kTileTok;
   const int64_t S = topk_tile_stride(n, kk, tile);
-  const int64_t cap = topk_sample_tiles(n, S, tile) * tile;
+  // the fused scan's sample holds each tile's 64 group maxima, the score-row
+  // top-k's every sampled key
+  const int64_t cap = topk_sample_tiles(n, S, tile) * (regions ? kRegTok / kGroupTok : tile);
   const size_t samp_b = ws_align((size_t)rows * (size_t)cap * 4);
   if (samp) *samp = reinterpret_cast<uint32_t *>(base);
   if (samp_cap) *samp_cap = cap;
@@ -1296,11 +1309,11 @@ int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int
   const int64_t ng = samp_cap / 16;
   if (samp_cap % 16 == 0 && ng >= 4 * kk && kk > 0) {  // 16-key group maxima (see select_groups_kernel)
     if (ng <= kSelThreads)
-      select_groups_kernel<1><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+      select_groups_kernel<1, false><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
     else if (ng <= 2 * kSelThreads)
-      select_groups_kernel<2><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+      select_groups_kernel<2, false><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
     else
-      select_groups_kernel<4><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
+      select_groups_kernel<4, false><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
     return launch_status("select_groups_kernel");
   }
   if (samp_cap <= 8 * kSelThreads)
@@ -1312,6 +1325,20 @@ int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int
   else
     select_keys_kernel<kSelPer><<<g, kSelThreads, 0, st>>>(samp, samp_cap, ukk, urh, s);
   return launch_status("select_keys_kernel");
+}
+
+int launch_select_groups(const uint32_t *gmax, int64_t rows, int64_t ng, int64_t kk, int64_t r_hi, TopkSel s,
+                         hipStream_t st) {
+  if (ng > 4 * kSelThreads) return fail(FATHOM_ERR_INVALID, "select: %lld group maxima exceed %d", (long long)ng, 4 * kSelThreads);
+  const unsigned g = (unsigned)rows;
+  const uint32_t ukk = (uint32_t)kk, urh = (uint32_t)r_hi;
+  if (ng <= kSelThreads)
+    select_groups_kernel<1, true><<<g, kSelThreads, 0, st>>>(gmax, ng, ukk, urh, s);
+  else if (ng <= 2 * kSelThreads)
+    select_groups_kernel<2, true><<<g, kSelThreads, 0, st>>>(gmax, ng, ukk, urh, s);
+  else
+    select_groups_kernel<4, true><<<g, kSelThreads, 0, st>>>(gmax, ng, ukk, urh, s);
+  return launch_status("select_groups_kernel");
 }
 
 int launch_sample_scores(const float *scores, int64_t rows, int64_t n, int64_t S, int64_t sink, int64_t lstart,

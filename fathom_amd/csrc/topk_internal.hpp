@@ -78,6 +78,11 @@ struct TopkSel {
 inline int64_t topk_tile_stride(int64_t n, int64_t kk, int64_t tile) {
   const int64_t ntiles = cdiv(n, tile);
   int64_t want = tile == kRegTok ? 32 : cdiv(8 * kTileTok, tile);
+  // the fused scan's sample keeps 64 group maxima per tile: at least 2 kk of them
+  if (tile == kRegTok && kk > 0) {
+    const int64_t g = cdiv(2 * kk, kRegTok / kGroupTok);
+    want = g > want ? g : want;
+  }
   if (kk > 0) {
     const int64_t a = cdiv(2 * kk, tile), b = cdiv(32 * n, kAlphaX2 * kk * tile);
     want = a > want ? a : want;
@@ -121,6 +126,10 @@ size_t topk_layout(int64_t rows, int64_t n, int64_t k, bool regions, char *base,
 // T_lo (rank kk) and T_hi (rank r_hi <= kk) of every row's sample; clears the counters.
 int launch_select_keys(const uint32_t *samp, int64_t rows, int64_t samp_cap, int64_t kk, int64_t r_hi, TopkSel s,
                        hipStream_t st);
+// Thresholds of the fused scan's rows from their sample's group maxima
+// (ng <= 4096 per row).
+int launch_select_groups(const uint32_t *gmax, int64_t rows, int64_t ng, int64_t kk, int64_t r_hi, TopkSel s,
+                         hipStream_t st);
 int launch_sample_scores(const float *scores, int64_t rows, int64_t n, int64_t S, int64_t sink, int64_t lstart,
                          uint32_t *samp, int64_t samp_cap, hipStream_t st);
 // First pass (fallback = false) or fallback pass (rows whose first pass found fewer than kk).
