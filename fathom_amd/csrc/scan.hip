@@ -26,12 +26,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
   plan_tables(sh, a, bh, NSMAX * kSlice);
-  if (MODE == kEmitSample || (MODE != kEmitFilter && split)) {
+  if (MODE == kEmitSample || (MODE != kEmitFilter && split == 4)) {
     // few tiles (the sample pass, short rows): four waves per tile, one
     // quarter each; the candidate pass keeps whole tiles (a region per tile)
     static_assert(kWaves == kQS, "a wave per quarter of a tile");
     tile_pass<MODE, ACC, false, NSMAX>(a, em, sh, bh, lane, (int64_t)blockIdx.x, (int64_t)gridDim.x, a.nwt,
                                        wave, wave + 1, 0u);
+  } else if (MODE != kEmitFilter && split == 2) {
+    // short rows on the two-waves-per-SIMD kernels: two tiles per workgroup,
+    // two quarters per wave (every wave of the launch resident at once)
+    const int q0 = (wave & 1) * 2;
+    tile_pass<MODE, ACC, false, NSMAX>(a, em, sh, bh, lane, (int64_t)blockIdx.x * 2 + (wave >> 1),
+                                       (int64_t)gridDim.x * 2, a.nwt, q0, q0 + 2, 0u);
   } else {
     // the candidate pass also writes the (zero) counts of the padding regions past the row
     constexpr bool kCand = MODE == kEmitFilter;
@@ -51,16 +57,18 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int
   a.nwt = nwt;
   int64_t wgs;
   int split = 0;
+  const int64_t nsl = cdiv(units_max, kSlice);
   if (MODE == kEmitSample || (MODE != kEmitFilter && nwt * BH < kTargetWaves)) {
-    wgs = nwt;  // four waves per tile, a quarter each
-    split = 1;
+    // fewer tiles than wave slots: waves split the tiles' quarters, four per
+    // tile, or two (two quarters each) on the two-waves-per-SIMD kernel
+    split = (MODE != kEmitSample && nsl > kGS) ? 2 : 4;
+    wgs = split == 4 ? nwt : cdiv(nwt, 2);
   } else {
     // enough waves to fill the chip, each taking a whole number of tiles
     const int64_t per = cdiv(nwt * BH, kTargetWaves);
     wgs = cdiv(cdiv(nwt, per), kWaves);
   }
   const dim3 grid((unsigned)wgs, (unsigned)BH);
-  const int64_t nsl = cdiv(units_max, kSlice);
   if (nsl > kGS)
     scan_wave_kernel<MODE, kGS, 4><<<grid, kThreads, 0, st>>>(a, em, split);
   else if (nsl == 4)
