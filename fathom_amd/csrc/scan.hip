@@ -25,7 +25,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
-  plan_tables(sh, a, bh, NSMAX * kSlice);
+  // the candidate pass starts from the tables its sample pass left, every
+  // other launch builds them
+  if (MODE != kEmitFilter || !em.tab || !load_tables(sh, a, em.tab + bh, NSMAX * kSlice))
+    plan_tables(sh, a, bh, NSMAX * kSlice);
+  if (MODE == kEmitSample && em.tab && blockIdx.x == 0) save_tables(sh, em.tab + bh, NSMAX * kSlice);
   if (MODE == kEmitSample || (MODE != kEmitFilter && split == 4)) {
     // few tiles (the sample pass, short rows): four waves per tile, one
     // quarter each; the candidate pass keeps whole tiles (a region per tile)
@@ -157,10 +161,12 @@ extern "C" int fathom_scan_planes(const float *q, int64_t BH, int64_t G, int64_t
 namespace fathom {
 // Workspace of the fused scan + top-k: rows up to kRowSelectMax keep their
 // scores ([rows, n] fp32) for one row-select launch; longer rows the sampled
-// keys and the candidate regions.
+// keys, the candidate regions and the plan tables (one per row: at least one
+// per (batch, KV head)).
 size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k) {
   if (n <= kRowSelectMax) return ws_align((size_t)rows * (size_t)n * 4) + ws_align((size_t)rows * cdiv(n, kGroupTok) * 4);
-  return topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr);
+  return topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr) +
+         ws_align((size_t)rows * sizeof(sc::PlanTab));
 }
 }  // namespace fathom
 
@@ -214,7 +220,8 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   }
   Emit em{};
   int64_t S = 1;
-  topk_layout(rows, n, k, true, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
+  const size_t tab_at = topk_layout(rows, n, k, true, static_cast<char *>(workspace), &em.samp, &em.samp_cap, &em.sel, &S);
+  em.tab = reinterpret_cast<sc::PlanTab *>(static_cast<char *>(workspace) + tab_at);
   em.sel.kk = (uint32_t)kk;
   const int64_t r_hi = topk_hi_rank(n, S, kk, kRegTok);
   em.sink = sink;

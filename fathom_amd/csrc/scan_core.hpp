@@ -80,6 +80,8 @@ struct ScanArgs {
   int D, G, bmax, ncls;    // classes 1..ncls are scanned (ncls = min(bmax, 4))
 };
 
+struct PlanTab;
+
 struct Emit {
   float *out;        // scores [BH, G, n]
   uint32_t *gmax;    // kEmitScoresMax: [BH * G, ceil(n / 16)] each 16-token group's largest masked key
@@ -87,6 +89,7 @@ struct Emit {
   int64_t samp_cap;
   TopkSel sel;       // thresholds + candidate regions
   int64_t sink, lstart;
+  PlanTab *tab;      // [BH] plan tables: the sample pass writes them, the candidate pass reads them (null: none)
 };
 
 // Wave-uniform loads through the constant address space (scalar loads).
@@ -135,6 +138,19 @@ struct Shared {
   int U;                                 // units, padded to whole slices
   int ureal;                             // units of the plan
 };
+
+// The plan tables of one row, as the fused scan + top-k's sample pass leaves
+// them for its candidate pass (plans of at most kTabUnits units): the
+// candidate pass then starts from one copy instead of rebuilding them from the
+// queries and class lists.
+constexpr int kTabUnits = kGS * kSlice;
+struct PlanTab {
+  int32_t U, ureal, pad[2];
+  int32_t sig[kMaxG];
+  uint32_t uoff[kTabUnits], soff[kTabUnits];
+  _Float16 qa[kRows][kTabUnits], ca[kRows][kTabUnits];
+};
+static_assert(sizeof(PlanTab) % 16 == 0, "tables copy as 16-byte vectors");
 
 // Orders a wave's LDS accesses: every lane's writes before any lane's reads.
 __device__ __forceinline__ void wave_lds_sync() {
@@ -267,6 +283,59 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
   for (int v = ureal + tid; v < UP; v += (int)blockDim.x) sh.uoff[v] = sh.soff[v] = 0u;
   __syncthreads();
   return U;
+}
+
+// Writes the workgroup's plan tables (built by plan_tables, padded to nu
+// units) to t.  A plan of more units writes only its header: the candidate
+// pass then builds its own tables.
+__device__ __forceinline__ void save_tables(const Shared &sh, PlanTab *t, int nu) {
+  const int tid = threadIdx.x, nthr = (int)blockDim.x;
+  const int U = sh.U;
+  if (tid == 0) {
+    t->U = U;
+    t->ureal = sh.ureal;
+  }
+  if (U > nu) return;  // uniform
+  if (tid < kMaxG) t->sig[tid] = sh.sig[tid];
+  for (int i = tid; i < nu; i += nthr) {
+    t->uoff[i] = sh.uoff[i];
+    t->soff[i] = sh.soff[i];
+  }
+  const int per = nu / 8;  // 8 halves per 16-byte vector
+  for (int i = tid; i < kRows * per; i += nthr) {
+    const int r = i / per, v = (i - r * per) * 8;
+    *reinterpret_cast<uint4 *>(&t->qa[r][v]) = *reinterpret_cast<const uint4 *>(&sh.qa[r][v]);
+    *reinterpret_cast<uint4 *>(&t->ca[r][v]) = *reinterpret_cast<const uint4 *>(&sh.ca[r][v]);
+  }
+}
+
+// Loads the plan tables of t (nu units, as save_tables wrote them) into the
+// workgroup's LDS.  False (nothing loaded) when t holds no tables for nu
+// units.  The offsets are range-checked against the superblock, so tables
+// that no sample pass wrote give wrong scores but no access outside the store.
+__device__ __forceinline__ bool load_tables(Shared &sh, const ScanArgs &a, const PlanTab *t, int nu) {
+  const int tid = threadIdx.x, nthr = (int)blockDim.x;
+  const int U = ld_uniform(&t->U), ureal = ld_uniform(&t->ureal);
+  if (U < 0 || U > nu || U % kSlice != 0 || ureal < 0 || ureal > U) return false;  // uniform
+  const uint32_t lim_u = (uint32_t)a.D * 4u * (uint32_t)a.sub * 8u, lim_s = (uint32_t)a.D * (uint32_t)a.sub * 2u;
+  for (int i = tid; i < nu; i += nthr) {
+    const uint32_t u = t->uoff[i], v = t->soff[i];
+    sh.uoff[i] = u < lim_u ? u : 0u;
+    sh.soff[i] = v < lim_s ? v : 0u;
+  }
+  if (tid < kMaxG) sh.sig[tid] = t->sig[tid];
+  const int per = nu / 8;
+  for (int i = tid; i < kRows * per; i += nthr) {
+    const int r = i / per, v = (i - r * per) * 8;
+    *reinterpret_cast<uint4 *>(&sh.qa[r][v]) = *reinterpret_cast<const uint4 *>(&t->qa[r][v]);
+    *reinterpret_cast<uint4 *>(&sh.ca[r][v]) = *reinterpret_cast<const uint4 *>(&t->ca[r][v]);
+  }
+  if (tid == 0) {
+    sh.U = U;
+    sh.ureal = ureal;
+  }
+  __syncthreads();
+  return true;
 }
 
 // --------------------------------------------------------------------- a tile

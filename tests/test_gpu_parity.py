@@ -583,6 +583,25 @@ def test_scan_topk_fused_equals_unfused(cfg, n, BH, k, sub):
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("umax", [16, 48, 0, None])
+def test_scan_topk_fused_plan_tables(umax):
+    """Long rows: the candidate pass starts from the plan tables the sample
+    pass left for rows whose plan fits the kernel's register layout, and builds
+    its own for the others (a units bound below a row's plan, or per-row
+    budgets of 24, 48 and 100 bits under one launch).  Equal to scan + top-k
+    in every case."""
+    print(f"[fused-tables] umax={umax}", flush=True)
+    budget = torch.tensor([24.0, 48.0, 100.0], device=DEV) if umax is None else None
+    x, st, plan = _scan_case(2, 70000, 3, budget=budget)
+    if umax is not None:
+        plan = dict(plan, units_max=umax)
+    q = x["q"].to(DEV)
+    ref = bp.sink_local_topk(st.scan(q, plan), 512, 4, 64)
+    for _ in range(2):  # a repeated call (its workspace may hold the first call's tables)
+        got = st.scan_topk(q, plan, 512, 4, 64)
+        torch.testing.assert_close(got, ref, rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("n,k", [(600000, 40), (1000000, 64)])
 def test_scan_topk_fused_small_k_long_rows(n, k):
     """The fused call with kk = k - 36 small against n (4 of 600000, 28 of
