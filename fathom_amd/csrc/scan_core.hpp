@@ -62,6 +62,7 @@ static_assert(kR == kGroupTok, "a lane's quarter is one group of the group maxim
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 enum : int { kEmitScores = 0, kEmitSample = 1, kEmitFilter = 2, kEmitScoresMax = 3 };
@@ -537,13 +538,14 @@ __device__ __forceinline__ void rescale(uint32_t (&ap)[NS][2], int sx) {
 // listed scale gives s_c (a' < 2^13); C of every head comes from the matrix
 // instruction (B = raw scale pairs, A = the C rows), chained over the plan's
 // slices like the scores.
-template <int NS, bool FIRST>
+// STK (stacked step classes): rows 8..15 repeat the C rows of rows 0..7.
+template <int NS, bool FIRST, bool STK = false>
 __device__ __forceinline__ void scale_group(uint32_t (&raw)[NS][2], float &amax, f4 &dc, const Shared &sh,
                                             const TileAddr &ta, int s0, int lane, int ureal) {
   const int c = lane & 15, g = lane >> 4;
   uint32_t cr[NS][2];
   load_scales<NS>(raw, sh, ta, s0, g);
-  load_arows<NS>(cr, sh.ca, s0, c, g);
+  load_arows<NS>(cr, sh.ca, s0, STK ? (c & 7) : c, g);
   mask_pad_scales<NS>(raw, s0, g, ureal);
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -553,9 +555,11 @@ __device__ __forceinline__ void scale_group(uint32_t (&raw)[NS][2], float &amax,
   dc = chain<NS, FIRST>(dc, cr, raw);
 }
 
-// s_c and the lane's C and exponents from the block maximum and the C sums.
+// s_c and the lane's C and exponents from the block maximum and the C sums
+// (STK: lanes 32..63 hold the heads of lanes 0..31).
+template <bool STK = false>
 __device__ __forceinline__ TileK scale_finish(float amax, const f4 &dc, const Shared &sh, const ScanArgs &a, int lane) {
-  const int g = lane >> 4;
+  const int g = STK ? (lane >> 4) & 1 : lane >> 4;
   amax = rows_max(amax);
   TileK k;
   k.sx = amax > 0.0f ? __builtin_amdgcn_frexp_expf(amax) - 13 : 0;
@@ -616,6 +620,7 @@ __device__ __forceinline__ float hi_threshold(float X, int fe, int w, float M) {
 struct EmitState {
   float T[2][4];       // candidate prefilter thresholds per slot and step class, accumulator
                        // units (NaN: every token takes the exact path; +inf: none does)
+  float Ts[2][2];      // stacked step classes: the lane's T of pair p (class p + 2 (lane >= 32))
   float thr[2];        // row thresholds as floats
   uint32_t off[2];     // candidates written so far into the tile's region (per head)
   float gm[2];         // group maxima: running max of the quarter's masked scores
@@ -800,12 +805,12 @@ struct RowK {
 };
 
 __device__ __forceinline__ RowK row_consts(const Emit &em, const ScanArgs &a, int64_t bh, int lane, bool fb,
-                                           uint32_t skipm) {
+                                           uint32_t skipm, bool stk) {
   RowK r;
   const uint32_t *thr = fb ? em.sel.thr_lo : em.sel.thr;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int h = 2 * (lane >> 4) + i;
+    const int h = 2 * (stk ? (lane >> 4) & 1 : lane >> 4) + i;
     r.head[i] = h < a.G && !((skipm >> h) & 1u);
     r.thr[i] = r.head[i] ? threshold_value(thr[bh * a.G + h]) : INFINITY;
   }
@@ -815,9 +820,9 @@ __device__ __forceinline__ RowK row_consts(const Emit &em, const ScanArgs &a, in
 // Per-mode state set up once a tile's scale pass is done; M: the bound of
 // the low rows' accumulators per unit 2^e_w (zero where the prefilter
 // compares both rows).
-template <int MODE>
+template <int MODE, bool STK = false>
 __device__ __forceinline__ void tile_setup(EmitState &es, const Emit &em, const ScanArgs &a, const TileK &k,
-                                           int64_t beta0, const RowK &rk, const float (&M)[2]) {
+                                           int64_t beta0, const RowK &rk, const float (&M)[2], int lane) {
   const int64_t t0 = beta0 * kBlk, t1 = t0 + kWTok;
   es.plain = beta0 >= a.blk0 && beta0 + kWB <= a.blk_end && t1 <= a.n && t0 >= em.sink && t1 <= em.lstart;
   es.off[0] = es.off[1] = 0u;
@@ -848,6 +853,10 @@ __device__ __forceinline__ void tile_setup(EmitState &es, const Emit &em, const 
       es.T[i][0] = hi_threshold(X, k.fe[i], 0, M[i]);
 #pragma unroll
       for (int w = 1; w < 4; ++w) es.T[i][w] = es.T[i][0] * (float)(1 << (bit_exp(w) - bit_exp(0)));
+      if constexpr (STK) {
+        es.Ts[i][0] = lane >= 32 ? es.T[i][2] : es.T[i][0];
+        es.Ts[i][1] = lane >= 32 ? es.T[i][3] : es.T[i][1];
+      }
     }
   }
 }
@@ -949,6 +958,225 @@ __device__ __forceinline__ void step_group_emit(const uint32_t (&qa)[NS][2], con
   emit_flush<MODE>(em, a, es, o, bh, beta0, L, qs, V, lane);
 }
 
+// ------------------------------------------------------ stacked step classes
+// Rows of at most four heads (G <= 4) leave rows 8..15 of the matrix tile
+// free.  A step group then runs as two pairs of step classes, (0, 2) and
+// (1, 3), each pair in one accumulator: the first class in rows 0..7, the
+// second in rows 8..15.  A slice pair of the first class is one instruction
+// with the A rows in rows 0..7 (zero below), the same slice pair of the second
+// class one with the A rows moved to rows 8..15 (zero above); each adds exact
+// zeros to the other half.  An odd last slice takes both classes in one
+// instruction: the first class's units in the lower four of each lane's eight
+// k values, the second's in the upper four.  Each class's rows see the same
+// nonzero products in the same order as the unstacked chain, so the scores
+// are the same bit for bit; a pair costs one instruction fewer for an odd
+// slice count, and one compare per head covers two classes.  Lane l of a pair
+// accumulator holds rows 4 (l / 16) .. + 3: heads 2 ((l / 16) & 1) + i of class
+// p (lanes 0..31) or p + 2 (lanes 32..63).
+
+// The A rows of rows 0..7 moved to rows 8..15 (zero in rows 0..7).
+template <int NS>
+__device__ __forceinline__ void load_arows_hi(uint32_t (&qhi)[NS][2], const _Float16 (*tab)[kMaxUnits], int s0,
+                                              int lane) {
+  const int r = lane & 15;
+  load_arows<NS>(qhi, tab, s0, r & 7, lane >> 4);
+  const uint32_t keep = r >= 8 ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    qhi[s][0] &= keep;
+    qhi[s][1] &= keep;
+  }
+}
+
+__device__ __forceinline__ f4 mfma4(const uint32_t (&av)[4], const uint32_t (&bv)[4], f4 c) {
+  h8 A, B;
+  __builtin_memcpy(&A, av, sizeof(A));
+  __builtin_memcpy(&B, bv, sizeof(B));
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, c, 0, 0, 0);
+}
+
+// The chain of one pair of step classes from zero: ba the first class's B
+// operands (rows 0..7), bb the second's (rows 8..15).
+template <int NS>
+__device__ __forceinline__ f4 chain_stk(const uint32_t (&qlo)[NS][2], const uint32_t (&qhi)[NS][2],
+                                        const uint32_t (&ba)[NS][2], const uint32_t (&bb)[NS][2]) {
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < NS; s += 2) {
+    if (s + 1 < NS) {
+      const int t = s + 1 < NS ? s + 1 : s;
+      const uint32_t a0[4] = {qlo[s][0], qlo[s][1], qlo[t][0], qlo[t][1]};
+      const uint32_t b0[4] = {ba[s][0], ba[s][1], ba[t][0], ba[t][1]};
+      const uint32_t a1[4] = {qhi[s][0], qhi[s][1], qhi[t][0], qhi[t][1]};
+      const uint32_t b1[4] = {bb[s][0], bb[s][1], bb[t][0], bb[t][1]};
+      acc = mfma4(a0, b0, s == 0 ? f4{0.0f, 0.0f, 0.0f, 0.0f} : acc);
+      acc = mfma4(a1, b1, acc);
+    } else {
+      const uint32_t a0[4] = {qlo[s][0], qlo[s][1], qhi[s][0], qhi[s][1]};
+      const uint32_t b0[4] = {ba[s][0], ba[s][1], bb[s][0], bb[s][1]};
+      acc = mfma4(a0, b0, s == 0 ? f4{0.0f, 0.0f, 0.0f, 0.0f} : acc);
+    }
+  }
+  return acc;
+}
+
+// The candidates of pair P whose prefilter some lane passed (filter_hit for
+// stacked classes): a head's candidates come from lane groups (g & 1) and
+// (g & 1) + 2, ranked over both by one ballot.
+template <int P>
+__device__ __forceinline__ void filter_hit_stk(const Emit &em, const ScanArgs &a, float xa, float xb, bool pa, bool pb,
+                                               const TileK &k, EmitState &es, int64_t bh, int64_t beta0, int qs, int V,
+                                               int lane) {
+  const int c = lane & 15, gh = (lane >> 4) & 1, up = lane >> 5;
+  const int ew = up ? bit_exp(P + 2) : bit_exp(P);
+  const uint32_t tt = (uint32_t)(c * kBlk) + (uint32_t)(16 * qs + 4 * V + P + 2 * up);
+  const uint32_t tok = (uint32_t)(beta0 * kBlk) + tt;
+  const bool inr = tt - es.vlo < es.vlen, um = tt - es.mlo < es.mlen;
+  constexpr uint64_t kH0 = 0x0000FFFF0000FFFFull;  // lane groups 0 and 2
+  const uint64_t hm = gh ? ~kH0 : kH0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float v = fmaf(i == 0 ? xa : xb, ldexpf(1.0f, k.fe[i] - ew), k.C[i]);
+    const float vm = um ? v : -INFINITY;  // score_key(-inf) is kKeyNegInf
+    const bool pass = es.head[i] && inr && (i == 0 ? pa : pb) && !(vm < es.thr[i]);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(pass);
+    if (m == 0ull) continue;  // uniform
+    const uint32_t n0 = (uint32_t)__builtin_popcountll(m & kH0), n1 = (uint32_t)__builtin_popcountll(m & ~kH0);
+    if (pass) {
+      const uint64_t mh = m & hm;
+      const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(mh >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mh, 0u));
+      uint64_t *dst = em.sel.cand + (bh * a.G + 2 * gh + i) * em.sel.cand_cap + beta0 * kBlk;
+      dst[es.off[i] + before] = k64_of(score_key(vm), tok);
+    }
+    es.off[i] += gh ? n1 : n0;
+  }
+}
+
+// Scores of a step group's two pairs (score modes): s[slot][p].
+struct StepOut2 {
+  float s[2][2];
+};
+
+template <int MODE, int P>
+__device__ __forceinline__ void emit_pair(const Emit &em, const ScanArgs &a, const f4 &acc, const TileK &k,
+                                          EmitState &es, StepOut2 &o, int64_t bh, int64_t beta0, int qs, int V,
+                                          int lane) {
+  if constexpr (MODE == kEmitFilter) {
+    const bool pa = !(acc[0] < es.Ts[0][P]);
+    const bool pb = !(acc[2] < es.Ts[1][P]);
+    if (__builtin_amdgcn_ballot_w64(pa || pb) == 0ull) return;  // uniform
+    filter_hit_stk<P>(em, a, acc[0] + acc[1], acc[2] + acc[3], pa, pb, k, es, bh, beta0, qs, V, lane);
+  } else {
+    const int up = lane >> 5;
+    const int ew = up ? bit_exp(P + 2) : bit_exp(P);
+    o.s[0][P] = fmaf(acc[0] + acc[1], ldexpf(1.0f, k.fe[0] - ew), k.C[0]);
+    o.s[1][P] = fmaf(acc[2] + acc[3], ldexpf(1.0f, k.fe[1] - ew), k.C[1]);
+  }
+}
+
+// store_scores for stacked classes: each lane stores its block's two
+// consecutive tokens 4V + 2 (lane >= 32) + {0, 1} per head; a quarter's group
+// maximum joins the halves of lanes l and l ^ 32.
+template <bool GMAX>
+__device__ __forceinline__ void store_scores_stk(const Emit &em, const ScanArgs &a, const float (&s2)[2][2],
+                                                 EmitState &es, int64_t bh, int64_t beta0, int qs, int V, int lane) {
+  const int c = lane & 15, gh = (lane >> 4) & 1, up = lane >> 5;
+  const int64_t blk = beta0 + c;
+  const bool inr = blk >= a.blk0 && blk < a.blk_end;
+  const int64_t tq = blk * kBlk + 16 * qs;  // the quarter's first token
+  const int64_t t2 = tq + 4 * V + 2 * up;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int h = 2 * gh + i;
+    const bool on = h < a.G && inr && tq < a.n;
+    if (on) {
+      float *dst = em.out + (bh * a.G + h) * a.n + t2;
+      if (t2 + 2 <= a.n && (a.n & 1) == 0) {
+        *reinterpret_cast<f2 *>(dst) = f2{s2[i][0], s2[i][1]};
+      } else {
+        if (t2 < a.n) dst[0] = s2[i][0];
+        if (t2 + 1 < a.n) dst[1] = s2[i][1];
+      }
+    }
+    if constexpr (GMAX) {  // a quarter's step groups come V = 3 first, V = 0 last
+      if (V == 3) {
+        es.gm[i] = -INFINITY;
+        es.gnan[i] = false;
+      }
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const int64_t tok = t2 + w;
+        const float v = (es.plain || (tok < a.n && tok >= em.sink && tok < em.lstart)) ? s2[i][w] : -INFINITY;
+        es.gm[i] = fmaxf(es.gm[i], v);
+        es.gnan[i] = es.gnan[i] || (v != v);
+      }
+      if (V == 0) {
+        const float og = __shfl_xor(es.gm[i], 32, 64);
+        const int on2 = __shfl_xor((int)es.gnan[i], 32, 64);
+        const bool gnan = es.gnan[i] || on2 != 0;
+        const float gm = fmaxf(es.gm[i], og);
+        if (on && up == 0) {
+          const int64_t ngrp = (a.n + kR - 1) / kR;
+          em.gmax[(bh * a.G + h) * ngrp + blk * 4 + qs] = gnan ? 0xFFFFFFFFu : score_key(gm);
+        }
+      }
+    }
+  }
+}
+
+// store_sample for stacked classes.
+__device__ __forceinline__ void store_sample_stk(const Emit &em, const ScanArgs &a, const float (&s2)[2][2],
+                                                 EmitState &es, int64_t bh, int64_t beta0, int64_t L, int qs, int V,
+                                                 int lane) {
+  const int c = lane & 15, gh = (lane >> 4) & 1, up = lane >> 5;
+  const int64_t t2 = (beta0 + c) * kBlk + 16 * qs + 4 * V + 2 * up;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int h = 2 * gh + i;
+    if (V == 3) es.gk[i] = 0u;  // a quarter's step groups come V = 3 first, V = 0 last
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const int64_t tok = t2 + w;
+      const bool masked = tok < em.sink || tok >= em.lstart;
+      const uint32_t key = tok < a.n ? (masked ? kKeyNegInf : score_key(s2[i][w])) : 0u;
+      es.gk[i] = max(es.gk[i], key);
+    }
+    if (V == 0) {
+      const uint32_t gk = max(es.gk[i], (uint32_t)__shfl_xor((int)es.gk[i], 32, 64));
+      if (h < a.G && up == 0)
+        em.samp[(bh * a.G + h) * em.samp_cap + L * (kWTok / kGroupTok) + c * kQS + qs] = gk;
+    }
+  }
+}
+
+// One step group of stacked classes (step_group_emit for G <= 4).
+template <int MODE, int NS>
+__device__ __forceinline__ void step_group_stk(const uint32_t (&qlo)[NS][2], const uint32_t (&qhi)[NS][2],
+                                               const uint32_t (&ap)[NS][2], const uint32_t (&Y)[NS][2],
+                                               const Emit &em, const ScanArgs &a, const TileK &k, EmitState &es,
+                                               int64_t bh, int64_t beta0, int64_t L, int qs, int V, int lane) {
+  StepOut2 o;
+  f4 p0, p1;
+  {
+    uint32_t ba[NS][2], bb[NS][2];
+    b_operands<NS, 0>(ba, Y, ap);
+    b_operands<NS, 2>(bb, Y, ap);
+    p0 = chain_stk<NS>(qlo, qhi, ba, bb);
+  }
+  {
+    uint32_t ba[NS][2], bb[NS][2];
+    b_operands<NS, 1>(ba, Y, ap);
+    b_operands<NS, 3>(bb, Y, ap);
+    p1 = chain_stk<NS>(qlo, qhi, ba, bb);
+  }
+  emit_pair<MODE, 0>(em, a, p0, k, es, o, bh, beta0, qs, V, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  emit_pair<MODE, 1>(em, a, p1, k, es, o, bh, beta0, qs, V, lane);
+  if constexpr (MODE == kEmitScores) store_scores_stk<false>(em, a, o.s, es, bh, beta0, qs, V, lane);
+  if constexpr (MODE == kEmitScoresMax) store_scores_stk<true>(em, a, o.s, es, bh, beta0, qs, V, lane);
+  if constexpr (MODE == kEmitSample) store_sample_stk(em, a, o.s, es, bh, beta0, L, qs, V, lane);
+}
+
 // The work of one wave on one tile: wave-tile beta0 (blocks beta0 .. beta0 +
 // 15 of row bh), quarters [qa0, qa1) (all four but in the sample pass), list
 // entry L; fb / skipm: the candidate pass's fallback rescan and the heads it
@@ -979,21 +1207,37 @@ __device__ __forceinline__ void lo_bound(float (&M)[2], const uint32_t (&qreg)[N
   M[1] = d[3];
 }
 
+// lo_bound for stacked classes: rows 8..15 of |A| repeat rows 0..7.
+template <int NS>
+__device__ __forceinline__ void lo_bound_stk(float (&M)[2], const uint32_t (&qlo)[NS][2], const uint32_t (&qhi)[NS][2],
+                                             const uint32_t (&ap)[NS][2]) {
+  uint32_t aq[NS][2];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    aq[s][0] = qlo[s][0] | qhi[s][0];
+    aq[s][1] = qlo[s][1] | qhi[s][1];
+  }
+  lo_bound<NS>(M, aq, ap);
+}
+
 // The four step groups of quarter qs, V = 3 down to 0, on the quarter's halves
 // Y (consumed).  Each dword turns as a whole: right by one for V = 3, then left
 // by four per step group, so the half bits 4V..4V+3 sit on bits 11..14 of each
 // half at step group V.  No bit is lost; the bits that wrap from one half into
 // the other land on bits 0..10 or 15 of a half, which no mask selects.
-template <int MODE, int NS>
-__device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], const uint32_t (&ap)[NS][2],
-                                             uint32_t (&Y)[NS][2], const Emit &em, const ScanArgs &a,
-                                             const TileK &k, EmitState &es, const TileJob &j, int qs) {
+// STK: stacked step classes (qhi: the A rows in rows 8..15).
+template <int MODE, int NS, bool STK>
+__device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], const uint32_t (&qhi)[NS][2],
+                                             const uint32_t (&ap)[NS][2], uint32_t (&Y)[NS][2], const Emit &em,
+                                             const ScanArgs &a, const TileK &k, EmitState &es, const TileJob &j,
+                                             int qs) {
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     Y[s][0] = __builtin_rotateright32(Y[s][0], 1);
     Y[s][1] = __builtin_rotateright32(Y[s][1], 1);
   }
-  step_group_emit<MODE, NS>(qreg, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, 3, j.lane);
+  if constexpr (STK) step_group_stk<MODE, NS>(qreg, qhi, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, 3, j.lane);
+  else step_group_emit<MODE, NS>(qreg, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, 3, j.lane);
 #pragma unroll 1
   for (int V = 2; V >= 0; --V) {
 #pragma unroll
@@ -1001,7 +1245,8 @@ __device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], cons
       Y[s][0] = __builtin_rotateleft32(Y[s][0], 4);
       Y[s][1] = __builtin_rotateleft32(Y[s][1], 4);
     }
-    step_group_emit<MODE, NS>(qreg, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, V, j.lane);
+    if constexpr (STK) step_group_stk<MODE, NS>(qreg, qhi, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, V, j.lane);
+    else step_group_emit<MODE, NS>(qreg, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, V, j.lane);
   }
 }
 
@@ -1009,9 +1254,10 @@ __device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], cons
 // and the A rows (qreg) for every tile.  Both quarters' halves are taken from a
 // quarter pair's plane dwords at once; the next pair's dwords load while the
 // second quarter computes.
-template <int MODE, int NS>
+template <int MODE, int NS, bool STK>
 __device__ __forceinline__ void tile_fast(const ScanArgs &a, const Emit &em, const Shared &sh,
-                                          const uint32_t (&qreg)[NS][2], const TileJob &j) {
+                                          const uint32_t (&qreg)[NS][2], const uint32_t (&qhi)[NS][2],
+                                          const TileJob &j) {
   const int c = j.lane & 15, g = j.lane >> 4;
   const TileAddr ta = tile_addr(a, j.bh, j.beta0, c);
   const int qp0 = j.qa0 >> 1, qp1 = (j.qa1 + 1) >> 1;
@@ -1020,21 +1266,24 @@ __device__ __forceinline__ void tile_fast(const ScanArgs &a, const Emit &em, con
   uint32_t ap[NS][2];
   float amax = 0.0f;
   f4 dc;
-  scale_group<NS, true>(ap, amax, dc, sh, ta, 0, j.lane, j.ureal);
-  const TileK k = scale_finish(amax, dc, sh, a, j.lane);
+  scale_group<NS, true, STK>(ap, amax, dc, sh, ta, 0, j.lane, j.ureal);
+  const TileK k = scale_finish<STK>(amax, dc, sh, a, j.lane);
   rescale<NS>(ap, k.sx);
   float M[2] = {0.0f, 0.0f};
-  if constexpr (MODE == kEmitFilter) lo_bound<NS>(M, qreg, ap);
+  if constexpr (MODE == kEmitFilter) {
+    if constexpr (STK) lo_bound_stk<NS>(M, qreg, qhi, ap);
+    else lo_bound<NS>(M, qreg, ap);
+  }
   EmitState es;
-  tile_setup<MODE>(es, em, a, k, j.beta0, j.rk, M);
+  tile_setup<MODE, STK>(es, em, a, k, j.beta0, j.rk, M, j.lane);
 #pragma unroll 1
   for (int qp = qp0; qp < qp1; ++qp) {
     uint32_t X0[NS][2], X1[NS][2];
     quarter_halves<NS, 0>(X0, d);
     quarter_halves<NS, 1>(X1, d);
-    if (2 * qp >= j.qa0) quarter_fast<MODE, NS>(qreg, ap, X0, em, a, k, es, j, 2 * qp);
+    if (2 * qp >= j.qa0) quarter_fast<MODE, NS, STK>(qreg, qhi, ap, X0, em, a, k, es, j, 2 * qp);
     if (qp + 1 < qp1) load_planes<NS>(d, sh, ta, 0, g, qp + 1);  // in flight during the second quarter
-    if (2 * qp + 1 < j.qa1) quarter_fast<MODE, NS>(qreg, ap, X1, em, a, k, es, j, 2 * qp + 1);
+    if (2 * qp + 1 < j.qa1) quarter_fast<MODE, NS, STK>(qreg, qhi, ap, X1, em, a, k, es, j, 2 * qp + 1);
   }
   if constexpr (MODE == kEmitFilter) tile_counts(em, a, es, j.bh, j.beta0, j.lane, j.fb, j.skipm);
 }
@@ -1081,7 +1330,7 @@ __device__ __forceinline__ void tile_grouped(const ScanArgs &a, const Emit &em, 
   const TileK k = scale_finish(amax, dc, sh, a, j.lane);
   const float M[2] = {0.0f, 0.0f};  // the grouped path compares both rows
   EmitState es;
-  tile_setup<MODE>(es, em, a, k, j.beta0, j.rk, M);
+  tile_setup<MODE>(es, em, a, k, j.beta0, j.rk, M, j.lane);
 #pragma unroll 1
   for (int qs = j.qa0; qs < j.qa1; ++qs) {
 #pragma unroll 1
@@ -1105,17 +1354,19 @@ __device__ __forceinline__ void tile_grouped(const ScanArgs &a, const Emit &em, 
 // nlist, quarters [qa0, qa1).  FB: the candidate pass's fallback rescan (T_lo,
 // second count array; heads in skipm emit nothing).  The candidate pass's
 // entries past the row's tiles (padding regions) get zero counts.
-template <int MODE, int NSK, int ACC, bool FB, int GS>
+template <int MODE, int NSK, int ACC, bool FB, int GS, bool STK = false>
 __device__ __forceinline__ void tile_loop(const ScanArgs &a, const Emit &em, const Shared &sh, int64_t bh, int lane,
                                           int64_t L0, int64_t Ls, int64_t nlist, int qa0, int qa1, uint32_t skipm,
                                           int nsl, int ureal) {
   constexpr bool kCand = MODE == kEmitFilter;
   constexpr int NQ = NSK > 0 ? NSK : 1;
+  static_assert(!STK || NSK > 0, "stacked step classes on the register-held path");
   uint32_t *rcp = FB ? em.sel.rc2 : em.sel.rc1;
-  uint32_t qreg[NQ][2];
+  uint32_t qreg[NQ][2], qhi[NQ][2];
   if constexpr (NSK > 0) load_arows<NQ>(qreg, sh.qa, 0, lane & 15, lane >> 4);
+  if constexpr (STK) load_arows_hi<NQ>(qhi, sh.qa, 0, lane);
   RowK rk{};
-  if constexpr (kCand) rk = row_consts(em, a, bh, lane, FB, skipm);
+  if constexpr (kCand) rk = row_consts(em, a, bh, lane, FB, skipm, STK);
   int64_t left = L0 < nlist ? (nlist - 1 - L0) / Ls : 0;  // the wave's entries after the current one
 #pragma unroll 1
   for (int64_t L = L0; L < nlist; L += Ls, --left) {
@@ -1127,17 +1378,17 @@ __device__ __forceinline__ void tile_loop(const ScanArgs &a, const Emit &em, con
     if (beta0 >= a.blk_end || beta0 + kWB <= a.blk0) continue;  // uniform per wave
     set_priority_by_tiles_left(left);
     const TileJob j{bh, beta0, L, qa0, qa1, lane, ureal, FB, skipm, rk};
-    if constexpr (NSK > 0) tile_fast<MODE, NQ>(a, em, sh, qreg, j);
+    if constexpr (NSK > 0) tile_fast<MODE, NQ, STK>(a, em, sh, qreg, qhi, j);
     else tile_grouped<MODE, ACC, GS>(a, em, sh, nsl, j);
   }
 }
 
 // Every tile of a wave.  A plan of up to NSMAX slices (the workgroup's tables
-// padded to NSMAX slices by plan_tables) runs with everything in registers;
-// a larger one in register groups (a kernel picked for small plans still
-// scans any plan correctly, only slower).  Zero units add exact zeros to
-// every chain (a chain from zero is never -0), so the scores do not depend on
-// the padding.
+// padded to NSMAX slices by plan_tables) runs with everything in registers,
+// rows of at most four heads with stacked step classes; a larger plan in
+// register groups (a kernel picked for small plans still scans any plan
+// correctly, only slower).  Zero units add exact zeros to every chain (a
+// chain from zero is never -0), so the scores do not depend on the padding.
 template <int MODE, int ACC, bool FB, int NSMAX>
 __device__ __forceinline__ void tile_pass(const ScanArgs &a, const Emit &em, const Shared &sh, int64_t bh, int lane,
                                           int64_t L0, int64_t Ls, int64_t nlist, int qa0, int qa1, uint32_t skipm) {
@@ -1145,7 +1396,9 @@ __device__ __forceinline__ void tile_pass(const ScanArgs &a, const Emit &em, con
   constexpr int GS = ACC == 4 ? kGS : 2;  // the register groups of a kernel tuned for small plans stay small
   const int nsl = __builtin_amdgcn_readfirstlane(sh.U) / kSlice;
   const int ureal = __builtin_amdgcn_readfirstlane(sh.ureal);
-  if (nsl <= NSMAX)
+  if (nsl <= NSMAX && a.G <= kMaxG / 2)
+    tile_loop<MODE, NSMAX, ACC, FB, GS, true>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal);
+  else if (nsl <= NSMAX)
     tile_loop<MODE, NSMAX, ACC, FB, GS>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal);
   else
     tile_loop<MODE, -1, ACC, FB, GS>(a, em, sh, bh, lane, L0, Ls, nlist, qa0, qa1, skipm, nsl, ureal);

@@ -177,6 +177,34 @@ def test_scan_matches_oracle(cfg, n, BH, sub):
     _scores_close(scores, ref)
 
 
+@pytest.mark.parametrize("budget,umax", [(16.0, None), (24.0, None), (40.0, None), (48.0, None), (48.0, 64),
+                                         (48.0, 16), (64.0, None), (100.0, None), (100.0, 64)])
+def test_scan_stacked_classes_equal_unstacked(budget, umax):
+    """Rows of at most four heads run stacked step classes (two classes per
+    accumulator, an odd last slice of both classes in one instruction); rows of
+    more heads do not.  Heads 0..3 scanned in a G = 4 call equal the same heads
+    scanned in a G = 8 call (heads 4..7 a copy) bit for bit, for plans of 1 to
+    7 slices, kernels picked for smaller or larger plans included; so do the
+    fused top-k indices (long rows, the candidate pass and its sample)."""
+    print(f"[stacked] budget={budget} umax={umax}", flush=True)
+    x = W.config_inputs(2, n=40000, BH=2)
+    st = bp.PlaneStore(x["K"].to(DEV))
+    plan = bp.make_plan(x["g"].to(DEV), budget)
+    if umax is not None:
+        plan = dict(plan, units_max=umax)
+    q4 = x["q"].to(DEV)
+    assert q4.shape[1] == 4
+    q8 = torch.cat([q4, q4], 1).contiguous()
+    s4, s8 = st.scan(q4, plan), st.scan(q8, plan)
+    torch.testing.assert_close(s4, s8[:, :4], rtol=0, atol=0)
+    torch.testing.assert_close(s8[:, 4:], s8[:, :4], rtol=0, atol=0)
+    i4, i8 = st.scan_topk(q4, plan, 512, 4, 64), st.scan_topk(q8, plan, 512, 4, 64)
+    torch.testing.assert_close(i4, i8[:, :4], rtol=0, atol=0)
+    torch.testing.assert_close(i4, bp.sink_local_topk(s4, 512, 4, 64), rtol=0, atol=0)
+    for G in (1, 2, 3):  # fewer heads: rows 2G..7 of each half are zero
+        torch.testing.assert_close(st.scan(q4[:, :G].contiguous(), plan), s4[:, :G], rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("G,n", [(2, 40000), (3, 20000), (5, 40000), (6, 20000), (8, 40000), (8, 20000)])
 def test_scan_and_fused_topk_every_group_size(G, n):
     """The scan is instantiated per head count G (1-8) and the configurations
