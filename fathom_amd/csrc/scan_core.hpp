@@ -1225,7 +1225,19 @@ __device__ __forceinline__ void lo_bound_stk(float (&M)[2], const uint32_t (&qlo
 // by four per step group, so the half bits 4V..4V+3 sit on bits 11..14 of each
 // half at step group V.  No bit is lost; the bits that wrap from one half into
 // the other land on bits 0..10 or 15 of a half, which no mask selects.
-// STK: stacked step classes (qhi: the A rows in rows 8..15).
+// The chain of pair P of stacked step classes (P, P + 2) of the halves Y.
+template <int NS, int P>
+__device__ __forceinline__ f4 pair_chain(const uint32_t (&qlo)[NS][2], const uint32_t (&qhi)[NS][2],
+                                         const uint32_t (&ap)[NS][2], const uint32_t (&Y)[NS][2]) {
+  uint32_t ba[NS][2], bb[NS][2];
+  b_operands<NS, P>(ba, Y, ap);
+  b_operands<NS, P + 2>(bb, Y, ap);
+  return chain_stk<NS>(qlo, qhi, ba, bb);
+}
+
+// STK: stacked step classes (qhi: the A rows in rows 8..15).  The candidate
+// pass compares pair 1 of a step group after pair 0 of the next one is
+// issued, so no compare waits on the chain just issued.
 template <int MODE, int NS, bool STK>
 __device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], const uint32_t (&qhi)[NS][2],
                                              const uint32_t (&ap)[NS][2], uint32_t (&Y)[NS][2], const Emit &em,
@@ -1235,6 +1247,29 @@ __device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], cons
   for (int s = 0; s < NS; ++s) {
     Y[s][0] = __builtin_rotateright32(Y[s][0], 1);
     Y[s][1] = __builtin_rotateright32(Y[s][1], 1);
+  }
+  if constexpr (STK && MODE == kEmitFilter) {
+    StepOut2 o;  // unused by the candidate emission
+    f4 p0 = pair_chain<NS, 0>(qreg, qhi, ap, Y);
+    f4 p1 = pair_chain<NS, 1>(qreg, qhi, ap, Y);
+    emit_pair<MODE, 0>(em, a, p0, k, es, o, j.bh, j.beta0, qs, 3, j.lane);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 1
+    for (int V = 2; V >= 0; --V) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        Y[s][0] = __builtin_rotateleft32(Y[s][0], 4);
+        Y[s][1] = __builtin_rotateleft32(Y[s][1], 4);
+      }
+      p0 = pair_chain<NS, 0>(qreg, qhi, ap, Y);
+      emit_pair<MODE, 1>(em, a, p1, k, es, o, j.bh, j.beta0, qs, V + 1, j.lane);
+      __builtin_amdgcn_sched_barrier(0);
+      p1 = pair_chain<NS, 1>(qreg, qhi, ap, Y);
+      emit_pair<MODE, 0>(em, a, p0, k, es, o, j.bh, j.beta0, qs, V, j.lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    emit_pair<MODE, 1>(em, a, p1, k, es, o, j.bh, j.beta0, qs, 0, j.lane);
+    return;
   }
   if constexpr (STK) step_group_stk<MODE, NS>(qreg, qhi, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, 3, j.lane);
   else step_group_emit<MODE, NS>(qreg, ap, Y, em, a, k, es, j.bh, j.beta0, j.L, qs, 3, j.lane);
