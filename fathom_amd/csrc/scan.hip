@@ -1,5 +1,7 @@
 // Partial-depth bit-plane scan (PlaneStore.scan) and the fused scan + top-k:
 // the kernels and launches over the wave-tile machinery of scan_core.hpp.
+#include <type_traits>
+
 #include "scan_core.hpp"
 #include "scan_internal.hpp"
 
@@ -17,11 +19,15 @@ using namespace sc;
 // NSMAX (1..4): the plan slices (16 units each) held in registers; ACC (1 or
 // 4): step groups whose accumulators a larger plan keeps over its register
 // groups (4: fewer reloads, more registers).  The scores are the same for any
-// choice; the launch picks them from the plan's units bound.
-template <int MODE, int NSMAX, int ACC>
+// choice; the launch picks them from the plan's units bound.  HOST (the
+// candidate pass over a store in mapped host memory, superblocks of a
+// multiple of 64 blocks): workgroups stage groups of four wave-tiles in LDS
+// (two workgroups per CU).
+template <int MODE, int NSMAX, int ACC, bool HOST = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
-    ACC == 4 ? 2 : 4))) void scan_wave_kernel(ScanArgs a, Emit em, int split) {
+    ACC == 4 || HOST ? 2 : 4))) void scan_wave_kernel(ScanArgs a, Emit em, int split) {
   __shared__ Shared sh;
+  __shared__ std::conditional_t<HOST, HostStage, char> hst;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t bh = blockIdx.y;
@@ -46,6 +52,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
     // the candidate pass also writes the (zero) counts of the padding regions past the row
     constexpr bool kCand = MODE == kEmitFilter;
     const int64_t nlist = kCand && em.sel.nreg > a.nwt ? em.sel.nreg : a.nwt;
+    if constexpr (HOST) {
+      static_assert(kCand, "staged host tiles in the candidate pass");
+      const int nsl = __builtin_amdgcn_readfirstlane(sh.U) / kSlice;
+      const int ureal = __builtin_amdgcn_readfirstlane(sh.ureal);
+      if (nsl <= NSMAX) {  // uniform; larger plans read the store directly
+        if (a.G <= kMaxG / 2)
+          host_tile_loop<MODE, NSMAX, false, true>(a, em, sh, hst, bh, lane, wave, nlist, 0u, nsl, ureal);
+        else
+          host_tile_loop<MODE, NSMAX, false, false>(a, em, sh, hst, bh, lane, wave, nlist, 0u, nsl, ureal);
+        return;
+      }
+    }
     const int64_t L0 = (int64_t)blockIdx.x * kWaves + wave, Ls = (int64_t)gridDim.x * kWaves;
     tile_pass<MODE, ACC, false, NSMAX>(a, em, sh, bh, lane, L0, Ls, nlist, 0, kQS, 0u);
   }
@@ -71,6 +89,25 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int
     // enough waves to fill the chip, each taking a whole number of tiles
     const int64_t per = cdiv(nwt * BH, kTargetWaves);
     wgs = cdiv(cdiv(nwt, per), kWaves);
+  }
+  // the layout of stores in mapped host memory (superblocks of a multiple of
+  // 64 blocks, shorter than the row; 16-byte aligned): the candidate pass
+  // stages its tiles, two workgroups per CU.  The whole-row layout of the
+  // copy-index staging store (in HBM) reads directly.
+  const bool host = MODE == kEmitFilter && nsl <= kGS && a.sub % kHostBlk == 0 && a.sub < cdiv(a.n, kBlk) &&
+                    (reinterpret_cast<uintptr_t>(a.planes) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.scales) & 15) == 0;
+  if (host) {
+    const int64_t per = cdiv(nwt * BH, kTargetWaves / 2);
+    const dim3 hgrid((unsigned)cdiv(cdiv(nwt, per), kWaves), (unsigned)BH);
+    if (MODE == kEmitFilter) {
+      if (nsl == 4)
+        scan_wave_kernel<kEmitFilter, 4, 1, true><<<hgrid, kThreads, 0, st>>>(a, em, split);
+      else if (nsl == 3)
+        scan_wave_kernel<kEmitFilter, 3, 1, true><<<hgrid, kThreads, 0, st>>>(a, em, split);
+      else
+        scan_wave_kernel<kEmitFilter, 2, 1, true><<<hgrid, kThreads, 0, st>>>(a, em, split);
+    }
+    return launch_status("scan_wave_kernel");
   }
   const dim3 grid((unsigned)wgs, (unsigned)BH);
   if (nsl > kGS)

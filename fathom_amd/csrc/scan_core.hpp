@@ -348,6 +348,27 @@ __device__ __forceinline__ bool load_tables(Shared &sh, const ScanArgs &a, const
 struct TileAddr {
   __amdgpu_buffer_rsrc_t pr, sr;
   uint32_t pl, sl;
+  const struct HostStage *hs;  // staged tiles (host stores): the workgroup's stage, hb its first block
+  int hb;
+};
+
+// ------------------------------------------------------------- host staging
+// A store in mapped host memory is read over PCIe, where the request size
+// sets the rate.  In superblocks of a multiple of 64 blocks the four
+// wave-tiles of a workgroup step are 64 consecutive blocks of one superblock:
+// each (channel, plane) unit of the plan is one 512-byte run and each active
+// channel's scales one 128-byte run.  The workgroup copies them into LDS with
+// 16-byte loads (plans of at most kHostUnits units), then each wave scans its
+// tile from there.
+constexpr int kHostUnits = 64;
+constexpr int kHostBlk = 4 * kWB;     // blocks per workgroup step (four wave-tiles)
+constexpr int kHostRow = 2 * kHostBlk + 4;  // a unit's plane dwords, padded (16-byte rows)
+struct HostStage {
+  uint32_t pw[kHostUnits][kHostRow];   // unit -> plane dwords of the 64 blocks (two per block)
+  uint16_t sc[kHostUnits][kHostBlk];   // channel slot -> scales of the 64 blocks
+  uint32_t soff1[kHostUnits];          // channel slot -> scale byte offset in the superblock
+  uint8_t uslot[kHostUnits];           // unit -> channel slot
+  int nch;                             // channel slots
 };
 
 constexpr int kBufFlags = 0x00020000;  // raw 32-bit buffer (gfx9 resource word 3)
@@ -368,6 +389,8 @@ __device__ __forceinline__ TileAddr tile_addr(const ScanArgs &a, int64_t bh, int
   ta.pr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(pb), (short)0, 0x7FFFFFFF, kBufFlags);
   ta.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(sbp), (short)0, 0x7FFFFFFF, kBufFlags);
   ta.pl = ta.sl = 0u;
+  ta.hs = nullptr;
+  ta.hb = 0;
   if ((int64_t)sb0 + dq < a.nsb) {
     ta.pl = ((dq * D * 4u) * sub + off) * 8u;
     ta.sl = ((dq * D) * sub + off) * 2u;
@@ -386,9 +409,17 @@ struct TileK {
 
 // Quarter-pair planes of NS slices from slice s0: dwords of units 4g + m
 // (m < 4), quarters 2 qp, 2 qp + 1 of the lane's block.
-template <int NS>
+template <int NS, bool HOST = false>
 __device__ __forceinline__ void load_planes(uint32_t (&d)[NS][4], const Shared &sh, const TileAddr &ta, int s0, int g,
                                             int qp) {
+  if constexpr (HOST) {
+    const int col = (ta.hb + (int)(threadIdx.x & 15)) * 2 + qp;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) d[s][m] = ta.hs->pw[(s0 + s) * kSlice + 4 * g + m][col];
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const uint4 uo = *reinterpret_cast<const uint4 *>(&sh.uoff[(s0 + s) * kSlice + 4 * g]);
@@ -401,8 +432,20 @@ __device__ __forceinline__ void load_planes(uint32_t (&d)[NS][4], const Shared &
 
 // Raw scales of NS slices from slice s0: pairs (units 4g, 4g + 1),
 // (4g + 2, 4g + 3) per slice.
-template <int NS>
+template <int NS, bool HOST = false>
 __device__ __forceinline__ void load_scales(uint32_t (&ap)[NS][2], const Shared &sh, const TileAddr &ta, int s0, int g) {
+  if constexpr (HOST) {
+    const int col = ta.hb + (int)(threadIdx.x & 15);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      uint32_t v[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) v[m] = ta.hs->sc[ta.hs->uslot[(s0 + s) * kSlice + 4 * g + m]][col];
+      ap[s][0] = v[0] | (v[1] << 16);
+      ap[s][1] = v[2] | (v[3] << 16);
+    }
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const uint4 so = *reinterpret_cast<const uint4 *>(&sh.soff[(s0 + s) * kSlice + 4 * g]);
@@ -539,12 +582,13 @@ __device__ __forceinline__ void rescale(uint32_t (&ap)[NS][2], int sx) {
 // instruction (B = raw scale pairs, A = the C rows), chained over the plan's
 // slices like the scores.
 // STK (stacked step classes): rows 8..15 repeat the C rows of rows 0..7.
-template <int NS, bool FIRST, bool STK = false>
+// HOST: the scales come from the workgroup's stage.
+template <int NS, bool FIRST, bool STK = false, bool HOST = false>
 __device__ __forceinline__ void scale_group(uint32_t (&raw)[NS][2], float &amax, f4 &dc, const Shared &sh,
                                             const TileAddr &ta, int s0, int lane, int ureal) {
   const int c = lane & 15, g = lane >> 4;
   uint32_t cr[NS][2];
-  load_scales<NS>(raw, sh, ta, s0, g);
+  load_scales<NS, HOST>(raw, sh, ta, s0, g);
   load_arows<NS>(cr, sh.ca, s0, STK ? (c & 7) : c, g);
   mask_pad_scales<NS>(raw, s0, g, ureal);
 #pragma unroll
@@ -1187,6 +1231,8 @@ struct TileJob {
   bool fb;
   uint32_t skipm;
   RowK rk;
+  const HostStage *hs = nullptr;  // staged tiles: the workgroup's stage and the tile's first block in it
+  int hb = 0;
 };
 
 // The bound M of the low rows' accumulators of the lane's heads per unit
@@ -1289,19 +1335,25 @@ __device__ __forceinline__ void quarter_fast(const uint32_t (&qreg)[NS][2], cons
 // and the A rows (qreg) for every tile.  Both quarters' halves are taken from a
 // quarter pair's plane dwords at once; the next pair's dwords load while the
 // second quarter computes.
-template <int MODE, int NS, bool STK>
+template <int MODE, int NS, bool STK, bool HOST = false>
 __device__ __forceinline__ void tile_fast(const ScanArgs &a, const Emit &em, const Shared &sh,
                                           const uint32_t (&qreg)[NS][2], const uint32_t (&qhi)[NS][2],
                                           const TileJob &j) {
   const int c = j.lane & 15, g = j.lane >> 4;
-  const TileAddr ta = tile_addr(a, j.bh, j.beta0, c);
+  TileAddr ta;
+  if constexpr (HOST) {
+    ta.hs = j.hs;
+    ta.hb = j.hb;
+  } else {
+    ta = tile_addr(a, j.bh, j.beta0, c);
+  }
   const int qp0 = j.qa0 >> 1, qp1 = (j.qa1 + 1) >> 1;
   uint32_t d[NS][4];
-  load_planes<NS>(d, sh, ta, 0, g, qp0);
+  load_planes<NS, HOST>(d, sh, ta, 0, g, qp0);
   uint32_t ap[NS][2];
   float amax = 0.0f;
   f4 dc;
-  scale_group<NS, true, STK>(ap, amax, dc, sh, ta, 0, j.lane, j.ureal);
+  scale_group<NS, true, STK, HOST>(ap, amax, dc, sh, ta, 0, j.lane, j.ureal);
   const TileK k = scale_finish<STK>(amax, dc, sh, a, j.lane);
   rescale<NS>(ap, k.sx);
   float M[2] = {0.0f, 0.0f};
@@ -1317,7 +1369,7 @@ __device__ __forceinline__ void tile_fast(const ScanArgs &a, const Emit &em, con
     quarter_halves<NS, 0>(X0, d);
     quarter_halves<NS, 1>(X1, d);
     if (2 * qp >= j.qa0) quarter_fast<MODE, NS, STK>(qreg, qhi, ap, X0, em, a, k, es, j, 2 * qp);
-    if (qp + 1 < qp1) load_planes<NS>(d, sh, ta, 0, g, qp + 1);  // in flight during the second quarter
+    if (qp + 1 < qp1) load_planes<NS, HOST>(d, sh, ta, 0, g, qp + 1);  // in flight during the second quarter
     if (2 * qp + 1 < j.qa1) quarter_fast<MODE, NS, STK>(qreg, qhi, ap, X1, em, a, k, es, j, 2 * qp + 1);
   }
   if constexpr (MODE == kEmitFilter) tile_counts(em, a, es, j.bh, j.beta0, j.lane, j.fb, j.skipm);
@@ -1415,6 +1467,93 @@ __device__ __forceinline__ void tile_loop(const ScanArgs &a, const Emit &em, con
     const TileJob j{bh, beta0, L, qa0, qa1, lane, ureal, FB, skipm, rk};
     if constexpr (NSK > 0) tile_fast<MODE, NQ, STK>(a, em, sh, qreg, qhi, j);
     else tile_grouped<MODE, ACC, GS>(a, em, sh, nsl, j);
+  }
+}
+
+// The workgroup's unit -> channel slot map of the stage (units of one channel
+// are consecutive and share a scale offset) and the slots' scale offsets.
+__device__ __forceinline__ void host_slots(HostStage &hs, const Shared &sh, int ureal) {
+  const int tid = threadIdx.x;
+  if (tid < kWave) {
+    const int u = tid;
+    const bool first = u < ureal && (u == 0 || sh.soff[u] != sh.soff[u - 1]);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(first);
+    const uint64_t le = u == kWave - 1 ? ~0ull : (2ull << u) - 1ull;  // lanes <= u
+    const int slot = (int)__builtin_popcountll(m & le) - 1;
+    hs.uslot[u] = (uint8_t)(u < ureal && slot >= 0 ? slot : 0);
+    if (first) hs.soff1[slot] = sh.soff[u];
+    if (u == 0) hs.nch = (int)__builtin_popcountll(m);
+  }
+}
+
+// Copies the plan's plane runs (U units) and scale runs (nch channels) of
+// blocks 16 L4 .. 16 L4 + 63 of row bh into the stage: 16-byte loads, all
+// issued before the first LDS write.
+__device__ __forceinline__ void host_stage(HostStage &hs, const ScanArgs &a, const Shared &sh, int64_t bh, int64_t L4,
+                                           int U, int nch) {
+  const int tid = threadIdx.x, nthr = (int)blockDim.x;
+  const uint32_t sub = (uint32_t)a.sub, b0 = (uint32_t)(L4 * kWB);
+  const uint32_t sb = b0 / sub, off0 = b0 - sb * sub;
+  const char *pb = reinterpret_cast<const char *>(a.planes + ((bh * a.nsb + sb) * a.D * 4) * a.sub * 2) + off0 * 8u;
+  const char *sbp = reinterpret_cast<const char *>(a.scales + ((bh * a.nsb + sb) * a.D) * a.sub) + off0 * 2u;
+  constexpr int kRunQ = kHostBlk * 8 / 16;  // 16-byte pieces of a unit's run
+  constexpr int kScQ = kHostBlk * 2 / 16;   // 16-byte pieces of a channel's scales
+  constexpr int kPer = kHostUnits * kRunQ / kThreads, kPerS = kHostUnits * kScQ / kThreads;
+  uint4 v[kPer], w[kPerS];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int i = tid + r * nthr;
+    if (i < U * kRunQ) v[r] = *reinterpret_cast<const uint4 *>(pb + sh.uoff[i / kRunQ] + (i % kRunQ) * 16);
+  }
+#pragma unroll
+  for (int r = 0; r < kPerS; ++r) {
+    const int i = tid + r * nthr;
+    if (i < nch * kScQ) w[r] = *reinterpret_cast<const uint4 *>(sbp + hs.soff1[i / kScQ] + (i % kScQ) * 16);
+  }
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int i = tid + r * nthr;
+    if (i < U * kRunQ) *reinterpret_cast<uint4 *>(&hs.pw[i / kRunQ][(i % kRunQ) * 4]) = v[r];
+  }
+#pragma unroll
+  for (int r = 0; r < kPerS; ++r) {
+    const int i = tid + r * nthr;
+    if (i < nch * kScQ) *reinterpret_cast<uint4 *>(&hs.sc[i / kScQ][(i % kScQ) * 8]) = w[r];
+  }
+}
+
+// tile_loop for stores in mapped host memory (the candidate pass, plans held
+// in registers): the workgroup steps through groups of four consecutive
+// wave-tiles in lockstep, stages each group, then each wave scans its tile
+// from the stage.
+template <int MODE, int NSK, bool FB, bool STK>
+__device__ __forceinline__ void host_tile_loop(const ScanArgs &a, const Emit &em, const Shared &sh, HostStage &hs,
+                                               int64_t bh, int lane, int wave, int64_t nlist, uint32_t skipm, int nsl,
+                                               int ureal) {
+  static_assert(MODE == kEmitFilter && NSK > 0 && NSK * kSlice <= kHostUnits, "staged candidate pass");
+  uint32_t *rcp = FB ? em.sel.rc2 : em.sel.rc1;
+  host_slots(hs, sh, ureal);
+  __syncthreads();
+  const int nch = __builtin_amdgcn_readfirstlane(hs.nch);
+  uint32_t qreg[NSK][2], qhi[NSK][2];
+  load_arows<NSK>(qreg, sh.qa, 0, lane & 15, lane >> 4);
+  if constexpr (STK) load_arows_hi<NSK>(qhi, sh.qa, 0, lane);
+  const RowK rk = row_consts(em, a, bh, lane, FB, skipm, STK);
+  const int64_t step = (int64_t)gridDim.x * kWaves;
+#pragma unroll 1
+  for (int64_t L4 = (int64_t)blockIdx.x * kWaves; L4 < nlist; L4 += step) {
+    const int64_t L = L4 + wave;
+    if (L4 < a.nwt) host_stage(hs, a, sh, bh, L4, nsl * kSlice, nch);  // uniform
+    __syncthreads();
+    if (L < nlist && L >= a.nwt) {
+      if (lane < a.G && !((skipm >> lane) & 1u)) rcp[(bh * a.G + lane) * em.sel.nreg + L] = 0u;
+    } else if (L < nlist) {
+      TileJob j{bh, L * kWB, L, 0, kQS, lane, ureal, FB, skipm, rk};
+      j.hs = &hs;
+      j.hb = wave * kWB;
+      tile_fast<MODE, NSK, STK, true>(a, em, sh, qreg, qhi, j);
+    }
+    __syncthreads();
   }
 }
 

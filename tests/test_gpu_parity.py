@@ -662,11 +662,13 @@ def test_scan_topk_fused_host_resident():
                                          (3, 100000, 64, None), (2, 40000, "whole", None), (1, 50000, 32, None),
                                          (2, 50000, 32, 8), (2, 20000, 64, None), (3, 4097, 32, None)])
 def test_scan_host_resident_paired_tiles(cfg, n, sub, G):
-    """Host-mapped stores with superblocks of a multiple of 32 blocks take the
-    paired-tile first pass (256-byte reads; G <= 4 only): scores and the fused
-    top-k equal the HBM store's bit for bit, for odd and even tile counts (the
-    odd count's last pair has no second tile) and for G = 8, which keeps the
-    single-tile pass."""
+    """Stores with superblocks of a multiple of 64 blocks (meant for mapped
+    host memory) take the staged candidate pass (each workgroup copies four
+    wave-tiles' 512-byte plane runs into LDS), 32-block superblocks the direct
+    one: in host memory the scores and the fused top-k equal the HBM store's
+    bit for bit, and the fused top-k equals the scores' top-k, for tile counts
+    that are and are not a multiple of four, G = 8 and the whole-sequence
+    layout."""
     print(f"[paired-host] cfg={cfg} n={n} sub={sub} G={G}", flush=True)
     s = math.ceil(n / 64) if sub == "whole" else sub
     x, st, plan = _scan_case(cfg, n, 2, sub=s)
@@ -685,13 +687,14 @@ def test_scan_host_resident_paired_tiles(cfg, n, sub, G):
         torch.cuda.synchronize()
         torch.testing.assert_close(got_s, ref_s, rtol=0, atol=0)
         torch.testing.assert_close(got_i, ref_i, rtol=0, atol=0)
+        torch.testing.assert_close(got_i, bp.sink_local_topk(ref_s, k, 4, 32), rtol=0, atol=0)
     finally:
         off.free_host(hp1)
         off.free_host(hp2)
 
 
 def test_scan_topk_fallback_pass_host_paired():
-    """The fallback pass (single tiles) after a paired first pass: a falling
+    """The fallback pass (direct tiles) after a staged first pass: a falling
     row in a host-mapped store of 64-block superblocks."""
     BH, d, n = 2, 128, 90000
     K = torch.zeros(BH, n, d)
