@@ -910,12 +910,14 @@ __device__ __forceinline__ void tile_counts(const Emit &em, const ScanArgs &a, c
                                             int64_t beta0, int lane, bool fb, uint32_t skipm) {
   const int c = lane & 15, gp = lane >> 4;
   if (c != 0) return;
-  uint32_t *rc = fb ? em.sel.rc2 : em.sel.rc1;
-  const int64_t region = beta0 / kWB;
+  // the row's base is wave-uniform; a head's offset in it fits 32 bits
+  // (nreg <= 2^21 regions)
+  uint32_t *rc = (fb ? em.sel.rc2 : em.sel.rc1) + bh * a.G * em.sel.nreg;
+  const uint32_t region = (uint32_t)(beta0 / kWB);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int h = 2 * gp + i;
-    if (h < a.G && !((skipm >> h) & 1u)) rc[(bh * a.G + h) * em.sel.nreg + region] = es.off[i];
+    if (h < a.G && !((skipm >> h) & 1u)) rc[(uint32_t)h * (uint32_t)em.sel.nreg + region] = es.off[i];
   }
 }
 
@@ -1499,16 +1501,18 @@ __device__ __forceinline__ void host_stage(HostStage &hs, const ScanArgs &a, con
   constexpr int kRunQ = kHostBlk * 8 / 16;  // 16-byte pieces of a unit's run
   constexpr int kScQ = kHostBlk * 2 / 16;   // 16-byte pieces of a channel's scales
   constexpr int kPer = kHostUnits * kRunQ / kThreads, kPerS = kHostUnits * kScQ / kThreads;
+  // every load is issued (pieces past the plan re-read piece 0), so the
+  // pieces stay in registers
   uint4 v[kPer], w[kPerS];
 #pragma unroll
   for (int r = 0; r < kPer; ++r) {
-    const int i = tid + r * nthr;
-    if (i < U * kRunQ) v[r] = *reinterpret_cast<const uint4 *>(pb + sh.uoff[i / kRunQ] + (i % kRunQ) * 16);
+    const int i0 = tid + r * nthr, i = i0 < U * kRunQ ? i0 : 0;
+    v[r] = *reinterpret_cast<const uint4 *>(pb + sh.uoff[i / kRunQ] + (i % kRunQ) * 16);
   }
 #pragma unroll
   for (int r = 0; r < kPerS; ++r) {
-    const int i = tid + r * nthr;
-    if (i < nch * kScQ) w[r] = *reinterpret_cast<const uint4 *>(sbp + hs.soff1[i / kScQ] + (i % kScQ) * 16);
+    const int i0 = tid + r * nthr, i = i0 < nch * kScQ ? i0 : 0;
+    w[r] = *reinterpret_cast<const uint4 *>(sbp + hs.soff1[i / kScQ] + (i % kScQ) * 16);
   }
 #pragma unroll
   for (int r = 0; r < kPer; ++r) {
