@@ -39,7 +39,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
 PCIE_PEAK_GBPS = 64.0         # PCIe 5.0 x16, per direction
-HOST_SUB = 64                 # superblock of the host-resident store (a multiple of 32 blocks)
+HOST_SUB = 64                 # superblock of the host-resident store (a multiple of 64 blocks)
 SIMDS = 256 * 4               # MI355X: 256 CUs x 4 SIMDs
 CLOCK_HZ = 2.4e9              # MI355X peak engine clock
 VALU_CYCLES = 4               # a wave64 VALU instruction occupies a 16-lane SIMD 4 cycles
@@ -650,9 +650,10 @@ def main():
     if not a.no_host and not a.stages_only:
         hps = []
         try:
-            # the host store in 64-block superblocks: the scan's first pass then
-            # reads two wave-tiles per load instruction (256 contiguous bytes),
-            # the request size zero-copy reads need to reach the link's rate
+            # the host store in 64-block superblocks: the candidate pass then
+            # stages four wave-tiles per workgroup, each unit one 512-byte run
+            # in 16-byte pieces, the request size zero-copy reads need to
+            # reach the link's rate
             bp.SUB = HOST_SUB
             try:
                 hsrc = bp.PlaneStore(x["K"], keep_code=False)

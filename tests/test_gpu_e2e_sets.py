@@ -7,7 +7,7 @@ selection boundary, within twice the row's measured score error (criterion in
 tests/fullsize_oracle.py).
 
 Cases: config 2; config 3 (n = 2^20) from HBM and from mapped host memory in
-64-block superblocks (the paired-tile first pass of the host-resident
+64-block superblocks (the staged candidate pass of the host-resident
 regime); config 4 at budgets 40, 48 and 80 bits; config 5 at its first and
 last layer.
 """
@@ -66,9 +66,9 @@ def test_c3_fused_sets_vs_float64_oracle(c3):
 
 
 def test_c3_host_paired_tiles_equal_hbm(c3):
-    """The host-resident regime's first pass (two wave-tiles per 256-byte load,
-    64-block superblocks in mapped pinned memory) at full size selects the
-    HBM path's indices bit for bit."""
+    """The host-resident regime's candidate pass (four wave-tiles staged in
+    LDS per workgroup from 64-block superblocks in mapped pinned memory) at
+    full size selects the HBM path's indices bit for bit."""
     print("[e2e] config 3: 64-block superblocks in mapped host memory", flush=True)
     x, plan = c3["x"], c3["plan"]
     bp.SUB = 64
