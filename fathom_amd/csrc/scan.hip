@@ -81,9 +81,10 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int
   int split = 0;
   const int64_t nsl = cdiv(units_max, kSlice);
   if (MODE == kEmitSample || (MODE != kEmitFilter && nwt * BH < kTargetWaves)) {
-    // fewer tiles than wave slots: waves split the tiles' quarters, four per
-    // tile, or two (two quarters each) on the two-waves-per-SIMD kernel
-    split = (MODE != kEmitSample && nsl > kGS) ? 2 : 4;
+    // fewer tiles than wave slots: waves split the tiles' quarters, two
+    // quarters (one quarter pair of the plane dwords) per wave in the score
+    // modes, one per wave in the sample pass
+    split = MODE != kEmitSample ? 2 : 4;
     wgs = split == 4 ? nwt : cdiv(nwt, 2);
   } else {
     // enough waves to fill the chip, each taking a whole number of tiles
