@@ -49,8 +49,8 @@ def cand_kernel(units_max):
     """The candidate pass's kernel for a plan bound (scan.hip launch_scan)."""
     nsl = -(-int(units_max) // 16)
     if units_max <= 0 or nsl > 4:
-        return "scan_wave_kernel<2, 4, 4>"
-    return f"scan_wave_kernel<2, {max(nsl, 2)}, 1>"
+        return "scan_wave_kernel<2, 6, 4, false>"
+    return f"scan_wave_kernel<2, {max(nsl, 2)}, 1, false>"
 
 
 def parse():

@@ -16,9 +16,10 @@ using namespace sc;
 // that found fewer than kk candidates for a row is completed by the row's
 // finalize workgroup (launch_finalize_fused).  The sample pass gives each of
 // its tiles four waves, one quarter of every block each.
-// NSMAX (1..4): the plan slices (16 units each) held in registers; ACC (1 or
-// 4): step groups whose accumulators a larger plan keeps over its register
-// groups (4: fewer reloads, more registers).  The scores are the same for any
+// NSMAX (2..4 at four waves per SIMD, 6 at two): the plan slices (16 units
+// each) held in registers; ACC (1 or 4): step groups whose accumulators a
+// larger plan keeps over its register groups (4: fewer reloads, more
+// registers).  The scores are the same for any
 // choice; the launch picks them from the plan's units bound.  HOST (the
 // candidate pass over a store in mapped host memory, superblocks of a
 // multiple of 64 blocks): workgroups stage groups of four wave-tiles in LDS
@@ -112,7 +113,7 @@ int launch_scan(const ScanArgs &a0, int64_t nwt, int64_t BH, const Emit &em, int
   }
   const dim3 grid((unsigned)wgs, (unsigned)BH);
   if (nsl > kGS)
-    scan_wave_kernel<MODE, kGS, 4><<<grid, kThreads, 0, st>>>(a, em, split);
+    scan_wave_kernel<MODE, kMaxNS, 4><<<grid, kThreads, 0, st>>>(a, em, split);
   else if (nsl == 4)
     scan_wave_kernel<MODE, 4, 1><<<grid, kThreads, 0, st>>>(a, em, split);
   else if (nsl == 3)

@@ -144,7 +144,8 @@ struct Shared {
 // them for its candidate pass (plans of at most kTabUnits units): the
 // candidate pass then starts from one copy instead of rebuilding them from the
 // queries and class lists.
-constexpr int kTabUnits = kGS * kSlice;
+constexpr int kMaxNS = 6;              // slices a kernel holds in registers (96 units)
+constexpr int kTabUnits = kMaxNS * kSlice;
 struct PlanTab {
   int32_t U, ureal, pad[2];
   int32_t sig[kMaxG];
@@ -1570,7 +1571,7 @@ __device__ __forceinline__ void host_tile_loop(const ScanArgs &a, const Emit &em
 template <int MODE, int ACC, bool FB, int NSMAX>
 __device__ __forceinline__ void tile_pass(const ScanArgs &a, const Emit &em, const Shared &sh, int64_t bh, int lane,
                                           int64_t L0, int64_t Ls, int64_t nlist, int qa0, int qa1, uint32_t skipm) {
-  static_assert(NSMAX >= 1 && NSMAX <= kGS, "one to four slices held in registers");
+  static_assert(NSMAX >= 1 && NSMAX <= kMaxNS, "one to six slices held in registers");
   constexpr int GS = ACC == 4 ? kGS : 2;  // the register groups of a kernel tuned for small plans stay small
   const int nsl = __builtin_amdgcn_readfirstlane(sh.U) / kSlice;
   const int ureal = __builtin_amdgcn_readfirstlane(sh.ureal);

@@ -178,14 +178,16 @@ def test_scan_matches_oracle(cfg, n, BH, sub):
 
 
 @pytest.mark.parametrize("budget,umax", [(16.0, None), (24.0, None), (40.0, None), (48.0, None), (48.0, 64),
-                                         (48.0, 16), (64.0, None), (100.0, None), (100.0, 64)])
+                                         (48.0, 16), (64.0, None), (80.0, None), (90.0, None), (90.0, 200),
+                                         (100.0, None), (100.0, 64)])
 def test_scan_stacked_classes_equal_unstacked(budget, umax):
     """Rows of at most four heads run stacked step classes (two classes per
     accumulator, an odd last slice of both classes in one instruction); rows of
     more heads do not.  Heads 0..3 scanned in a G = 4 call equal the same heads
     scanned in a G = 8 call (heads 4..7 a copy) bit for bit, for plans of 1 to
-    7 slices, kernels picked for smaller or larger plans included; so do the
-    fused top-k indices (long rows, the candidate pass and its sample)."""
+    7 slices (up to 6 held in registers), kernels picked for smaller or larger
+    plans included; so do the fused top-k indices (long rows, the candidate
+    pass and its sample)."""
     print(f"[stacked] budget={budget} umax={umax}", flush=True)
     x = W.config_inputs(2, n=40000, BH=2)
     st = bp.PlaneStore(x["K"].to(DEV))
