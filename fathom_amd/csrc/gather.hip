@@ -552,6 +552,65 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void attn_head_kernel(const flo
   if (tid < kAttnD) out[(bh * G + g) * kAttnD + tid] = runO[tid] / runL;
 }
 
+// Attention of one query head split over its positions (no union, rows in
+// device memory, n_unique not asked for): workgroup (split s, head g, row bh)
+// of NW waves takes positions [16 NW s, 16 NW (s + 1)) of head g, each with a
+// count of one, and writes its (M, sum, weighted V) triple for
+// attn_merge_kernel.  More workgroups than heads spread a row's gathers over
+// the chip.
+template <int NW>
+__global__ __launch_bounds__(NW * kWave) void attn_split_kernel(const float *__restrict__ q,
+                                                                const int64_t *__restrict__ idx, int64_t G, int64_t k,
+                                                                RowSrc rs, float scale, float *__restrict__ part,
+                                                                int64_t nsplit) {
+  __shared__ AttnShared<1, NW, 1> sh;
+  constexpr int T = 16 * NW;
+  const int tid = threadIdx.x;
+  const int64_t s = blockIdx.x, g = blockIdx.y, bh = blockIdx.z;
+  const float *qg = q + (bh * G + g) * kAttnD;
+  const int64_t *ig = idx + (bh * G + g) * k;
+  if (tid < kAttnD) sh.q[0][tid] = qg[tid];
+  if (tid < T) {
+    const int64_t j = s * T + tid;
+    uint4 cn = make_uint4(0u, 0u, 0u, 0u);
+    uint64_t ka = 0ull, va = 0ull;
+    if (j < k) {
+      cn.x = 1u;  // head 0 of the workgroup, selected once at this position
+      bool rec;
+      const int64_t row = rs.locate(tok_key(ig[j]), bh, rec);
+      if (row >= 0) {
+        ka = reinterpret_cast<uint64_t>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
+        va = reinterpret_cast<uint64_t>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes);
+      }
+    }
+    sh.kaddr[tid] = ka;
+    sh.vaddr[tid] = va;
+    sh.cnt[tid] = cn;
+  }
+  __syncthreads();
+  AttnRows r;
+  attn_load(sh, 0, reinterpret_cast<uint64_t>(qg), r);
+  attn_compute(sh, 0, r, scale);
+  __syncthreads();
+  float *pb = part + ((bh * nsplit + s) * G + g) * kPartStride;
+  if (tid < kAttnD) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) acc += sh.o[v][0][tid];
+    pb[2 + tid] = acc;
+  }
+  if (tid == 0) {
+    float Mg = -INFINITY, Lg = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      Mg = fmaxf(Mg, sh.wm[v][0]);
+      Lg += sh.wl[v][0];
+    }
+    pb[0] = Mg;
+    pb[1] = Lg;
+  }
+}
+
 // out[bh, g, d] = sum_s O_s e^(M_s - M) / sum_s L_s e^(M_s - M) over the
 // row's splits, by every thread for its own dimension d with no barrier:
 // M = max_s M_s first, then the weighted sums in split order, kB splits per
@@ -691,7 +750,18 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
   const RowSrc rs{(const char *)Ksrc, (const char *)Vsrc, (const char *)Krec, (const char *)Vrec,
                   cap, nrec, n, (int64_t)kAttnD * 2};
   int rc;
-  if (!n_unique) {
+  if (!n_unique && k > kHeadGroups * kHeadTok) {
+    // more positions than one round of the per-head kernel (C4: k = 2048):
+    // each query head's positions split over workgroups of 64, then the merge
+    constexpr int NW = kAttnWaves;
+    const int64_t ns = cdiv(k, (int64_t)(16 * NW));
+    attn_split_kernel<NW><<<dim3((unsigned)ns, (unsigned)G, (unsigned)BH), NW * kWave, 0, st>>>(q, idx, G, k, rs, scale,
+                                                                                               part, ns);
+    rc = launch_status("attn_split_kernel");
+    if (rc) return rc;
+    attn_merge_kernel<<<(unsigned)(BH * G), kAttnD, 0, st>>>(part, G, ns, out);
+    return launch_status("attn_merge_kernel");
+  } else if (!n_unique) {
     // one workgroup per query head over its own positions, no union, no merge
     attn_head_kernel<<<dim3((unsigned)G, (unsigned)BH), kHeadWaves * kWave, 0, st>>>(q, idx, G, k, rs, scale, out);
     return launch_status("attn_head_kernel");
