@@ -465,149 +465,144 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(const float 
   }
 }
 
-// Attention of one query head per workgroup (no union, rows in device memory,
-// n_unique not asked for): workgroup (g, bh) of kHeadWaves waves takes head
-// g's k selected positions 16 kHeadWaves at a time, each with a count of one
-// (a row selected twice counts twice), folds every group into a running (M,
-// sum, weighted V) with the usual rescaling, and writes out[bh, g] itself --
-// one launch, no partial triples.  Positions are placed kHeadGroups groups at
-// a time, and all of their K/V rows are requested before the first group is
-// computed, so the groups' load latencies overlap.
-constexpr int kHeadWaves = 16;
-constexpr int kHeadTok = 16 * kHeadWaves;
-constexpr int kHeadGroups = 2;
-
-__global__ __launch_bounds__(kHeadWaves * kWave) void attn_head_kernel(const float *__restrict__ q,
-                                                                       const int64_t *__restrict__ idx, int64_t G,
-                                                                       int64_t k, RowSrc rs, float scale,
-                                                                       float *__restrict__ out) {
-  __shared__ AttnShared<1, kHeadWaves, kHeadGroups> sh;
-  __shared__ float runO[kAttnD];
-  __shared__ float runM, runL;
-  const int tid = threadIdx.x;
-  const int64_t g = blockIdx.x, bh = blockIdx.y;
-  const float *qg = q + (bh * G + g) * kAttnD;
-  const int64_t *ig = idx + (bh * G + g) * k;
-  if (tid < kAttnD) {
-    sh.q[0][tid] = qg[tid];
-    runO[tid] = 0.0f;
-  }
-  if (tid == 0) {
-    runM = -INFINITY;
-    runL = 0.0f;
-  }
-  static_assert(kHeadGroups * kHeadTok <= kHeadWaves * kWave, "a thread per position placed");
-  for (int64_t c0 = 0; c0 < k; c0 += kHeadGroups * kHeadTok) {
-    if (tid < kHeadGroups * kHeadTok) {
-      const int64_t j = c0 + tid;
-      uint4 cn = make_uint4(0u, 0u, 0u, 0u);
-      uint64_t ka = 0ull, va = 0ull;
-      if (j < k) {
-        cn.x = 1u;  // head 0 of the workgroup, selected once at this position
-        bool rec;
-        const int64_t row = rs.locate(tok_key(ig[j]), bh, rec);
-        if (row >= 0) {
-          ka = reinterpret_cast<uint64_t>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
-          va = reinterpret_cast<uint64_t>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes);
-        }
-      }
-      sh.kaddr[tid] = ka;
-      sh.vaddr[tid] = va;
-      sh.cnt[tid] = cn;
-    }
-    __syncthreads();
-    const int ng = (int)min((int64_t)kHeadGroups, cdiv(k - c0, (int64_t)kHeadTok));  // uniform
-    AttnRows r[kHeadGroups];
-#pragma unroll
-    for (int gi = 0; gi < kHeadGroups; ++gi)
-      if (gi < ng) attn_load(sh, gi * kHeadTok, reinterpret_cast<uint64_t>(qg), r[gi]);
-#pragma unroll
-    for (int gi = 0; gi < kHeadGroups; ++gi) {
-      if (gi >= ng) break;
-      attn_compute(sh, gi * kHeadTok, r[gi], scale);
-      __syncthreads();
-      // fold the group into the running triple (every thread reads runM first)
-      float mc = -INFINITY;
-#pragma unroll
-      for (int v = 0; v < kHeadWaves; ++v) mc = fmaxf(mc, sh.wm[v][0]);
-      const float Mo = runM, Mn = fmaxf(Mo, mc);
-      const float eo = Mo == -INFINITY ? 0.0f : expf(Mo - Mn), ec = mc == -INFINITY ? 0.0f : expf(mc - Mn);
-      if (tid < kAttnD) {
-        float oc = 0.0f;
-#pragma unroll
-        for (int v = 0; v < kHeadWaves; ++v) oc += sh.o[v][0][tid];
-        runO[tid] = runO[tid] * eo + oc * ec;
-      }
-      __syncthreads();  // every thread has read runM
-      if (tid == 0) {
-        float lc = 0.0f;
-#pragma unroll
-        for (int v = 0; v < kHeadWaves; ++v) lc += sh.wl[v][0];
-        runL = runL * eo + lc * ec;
-        runM = Mn;
-      }
-      __syncthreads();  // sh is rewritten by the next group
-    }
-  }
-  if (tid < kAttnD) out[(bh * G + g) * kAttnD + tid] = runO[tid] / runL;
-}
-
-// Attention of one query head split over its positions (no union, rows in
-// device memory, n_unique not asked for): workgroup (split s, head g, row bh)
-// of NW waves takes positions [16 NW s, 16 NW (s + 1)) of head g, each with a
-// count of one, and writes its (M, sum, weighted V) triple for
-// attn_merge_kernel.  More workgroups than heads spread a row's gathers over
-// the chip.
-template <int NW>
-__global__ __launch_bounds__(NW * kWave) void attn_split_kernel(const float *__restrict__ q,
-                                                                const int64_t *__restrict__ idx, int64_t G, int64_t k,
-                                                                RowSrc rs, float scale, float *__restrict__ part,
-                                                                int64_t nsplit) {
-  __shared__ AttnShared<1, NW, 1> sh;
-  constexpr int T = 16 * NW;
-  const int tid = threadIdx.x;
+// Attention of one query head's positions streamed through registers (no
+// union, rows in device memory, n_unique not asked for): workgroup (split s,
+// head g, row bh) of NW waves takes positions [32 NW s, 32 NW (s + 1)) of head
+// g, each with a count of one (a row selected twice counts twice).  Wave w
+// holds 32 of them: lane l works on dims 8 (l & 15) .. + 7 of the rows of
+// positions 4 t + (l >> 4), t < 8.  Every K and V row piece of the wave is
+// requested before the first score is formed (K first), so the scores follow
+// the K rows as they arrive and the values the V rows.  A position without a
+// row (negative token, beyond the cache) scores 0 and reads kZeroRow, which
+// adds nothing to V.  The wave's softmax is taken against its own maximum, so no
+// barrier is needed until the waves' (M, sum, weighted V) triples are
+// combined.  With one split the workgroup writes out[bh, g]; with more it
+// writes its triple for attn_merge_kernel.
+constexpr int kStreamTok = 32;               // positions per wave
+constexpr uint64_t kRowBytes = 2 * kAttnD;   // a bf16 row
+__device__ const u32x4 kZeroRow[kRowBytes / 16] = {};
+template <int NW, bool REC>
+__global__ __launch_bounds__(NW * kWave) void attn_stream_kernel(const float *__restrict__ q,
+                                                                 const int64_t *__restrict__ idx, int64_t G, int64_t k,
+                                                                 RowSrc rs, float scale, float *__restrict__ out,
+                                                                 float *__restrict__ part, int64_t nsplit) {
+  constexpr int kSteps = kStreamTok / 4;
+  __shared__ float wm[NW], wl[NW];
+  __shared__ float wo[NW][kAttnD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = lane >> 4, ds = lane & 15;
   const int64_t s = blockIdx.x, g = blockIdx.y, bh = blockIdx.z;
   const float *qg = q + (bh * G + g) * kAttnD;
   const int64_t *ig = idx + (bh * G + g) * k;
-  if (tid < kAttnD) sh.q[0][tid] = qg[tid];
-  if (tid < T) {
-    const int64_t j = s * T + tid;
-    uint4 cn = make_uint4(0u, 0u, 0u, 0u);
-    uint64_t ka = 0ull, va = 0ull;
-    if (j < k) {
-      cn.x = 1u;  // head 0 of the workgroup, selected once at this position
-      bool rec;
-      const int64_t row = rs.locate(tok_key(ig[j]), bh, rec);
-      if (row >= 0) {
-        ka = reinterpret_cast<uint64_t>((rec ? rs.Krec : rs.K) + row * rs.row_bytes);
-        va = reinterpret_cast<uint64_t>((rec ? rs.Vrec : rs.V) + row * rs.row_bytes);
-      }
-    }
-    sh.kaddr[tid] = ka;
-    sh.vaddr[tid] = va;
-    sh.cnt[tid] = cn;
-  }
-  __syncthreads();
-  AttnRows r;
-  attn_load(sh, 0, reinterpret_cast<uint64_t>(qg), r);
-  attn_compute(sh, 0, r, scale);
-  __syncthreads();
-  float *pb = part + ((bh * nsplit + s) * G + g) * kPartStride;
-  if (tid < kAttnD) {
-    float acc = 0.0f;
+  const int64_t p0 = (s * NW + wave) * kStreamTok + rg;
+  const float4 qa = *reinterpret_cast<const float4 *>(qg + 8 * ds);
+  const float4 qb = *reinterpret_cast<const float4 *>(qg + 8 * ds + 4);
+  int64_t tk[kSteps];  // positions past k read the last one (and are masked)
 #pragma unroll
-    for (int v = 0; v < NW; ++v) acc += sh.o[v][0][tid];
-    pb[2 + tid] = acc;
+  for (int t = 0; t < kSteps; ++t) {
+    const int64_t j = p0 + 4 * t;
+    tk[t] = ig[j < k ? j : k - 1];
   }
-  if (tid == 0) {
-    float Mg = -INFINITY, Lg = 0.0f;
+  const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+  // RowSrc::locate without branches: a device row (token < min(n, cap)), a
+  // recent row (token >= n, the last one for tokens past nrec) or none
+  const int64_t dlim = rs.n < rs.cap ? rs.n : rs.cap;
+  const uint64_t kdev = reinterpret_cast<uint64_t>(rs.K) + (uint64_t)(bh * rs.cap) * kRowBytes;
+  const uint64_t vdev = reinterpret_cast<uint64_t>(rs.V) + (uint64_t)(bh * rs.cap) * kRowBytes;
+  const uint64_t zero = reinterpret_cast<uint64_t>(kZeroRow);
+  uint64_t ka[kSteps], va[kSteps];
+  bool in[kSteps], has[kSteps];
+#pragma unroll
+  for (int t = 0; t < kSteps; ++t) {
+    in[t] = p0 + 4 * t < k;
+    const uint32_t tok = tok_key(tk[t]);
+    const bool dv = tok != kTokNeg && (int64_t)tok < dlim;
+    has[t] = dv;
+    ka[t] = dv ? kdev + (uint64_t)tok * kRowBytes : zero;
+    va[t] = dv ? vdev + (uint64_t)tok * kRowBytes : zero;
+    if (REC && !dv && tok != kTokNeg && (int64_t)tok >= rs.n) {
+      has[t] = true;
+      const int64_t r = bh * rs.nrec + ((int64_t)tok - rs.n < rs.nrec - 1 ? (int64_t)tok - rs.n : rs.nrec - 1);
+      ka[t] = reinterpret_cast<uint64_t>(rs.Krec) + (uint64_t)r * kRowBytes;
+      va[t] = reinterpret_cast<uint64_t>(rs.Vrec) + (uint64_t)r * kRowBytes;
+    }
+  }
+  u32x4 kv[kSteps], vv[kSteps];
+#pragma unroll
+  for (int t = 0; t < kSteps; ++t) kv[t] = reinterpret_cast<gptr4>(ka[t])[ds];
+  __builtin_amdgcn_sched_barrier(0);  // the K pieces first, in position order
+#pragma unroll
+  for (int t = 0; t < kSteps; ++t) vv[t] = reinterpret_cast<gptr4>(va[t])[ds];
+  __builtin_amdgcn_sched_barrier(0);  // every row piece requested before the first score
+  // ---- scores; a position past k is absent
+  float sc[kSteps];
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < kSteps; ++t) {
+    const uint32_t d4[4] = {kv[t].x, kv[t].y, kv[t].z, kv[t].w};
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t h = d4[e >> 1];
+      a = fmaf(qq[e], __uint_as_float((e & 1) ? (h & 0xFFFF0000u) : (h << 16)), a);
+    }
+    a = row16_reduce<false>(a);
+    sc[t] = in[t] ? (has[t] ? a * scale : 0.0f) : -INFINITY;
+    m = fmaxf(m, sc[t]);
+  }
+  m = across_rows<true>(m);  // the wave's maximum
+  __builtin_amdgcn_sched_barrier(0);  // the V pieces are awaited only from here
+  // ---- the wave's sum and weighted V against its own maximum
+  float l = 0.0f, o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+#pragma unroll
+  for (int t = 0; t < kSteps; ++t) {
+    const float p = in[t] ? expf(sc[t] - m) : 0.0f;
+    l += p;
+    const uint32_t d4[4] = {vv[t].x, vv[t].y, vv[t].z, vv[t].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t h = d4[e >> 1];
+      o[e] = fmaf(p, __uint_as_float((e & 1) ? (h & 0xFFFF0000u) : (h << 16)), o[e]);
+    }
+  }
+  l = across_rows<false>(l);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = across_rows<false>(o[e]);
+  if (rg == 0) {
+    *reinterpret_cast<float4 *>(&wo[wave][8 * ds]) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4 *>(&wo[wave][8 * ds + 4]) = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+  __syncthreads();
+  if (tid < kAttnD) {
+    // lane v < NW: wave v's factor e^(M_v - M); every lane reads them by readlane
+    const float mv = lane < NW ? wm[lane] : -INFINITY;
+    float M = mv;
+#pragma unroll
+    for (int sh = 1; sh < NW; sh <<= 1) M = fmaxf(M, __shfl_xor(M, sh));
+    const float ev = mv == -INFINITY ? 0.0f : expf(mv - M);  // a wave past k adds nothing
+    float L = 0.0f, O = 0.0f;
 #pragma unroll
     for (int v = 0; v < NW; ++v) {
-      Mg = fmaxf(Mg, sh.wm[v][0]);
-      Lg += sh.wl[v][0];
+      const float e = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev), v));
+      L = fmaf(wl[v], e, L);
+      O = fmaf(wo[v][tid], e, O);
     }
-    pb[0] = Mg;
-    pb[1] = Lg;
+    if (nsplit == 1) {
+      out[(bh * G + g) * kAttnD + tid] = O / L;
+    } else {
+      float *pb = part + ((bh * nsplit + s) * G + g) * kPartStride;
+      pb[2 + tid] = O;
+      if (tid == 0) {
+        pb[0] = M;
+        pb[1] = L;
+      }
+    }
   }
 }
 
@@ -750,21 +745,26 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
   const RowSrc rs{(const char *)Ksrc, (const char *)Vsrc, (const char *)Krec, (const char *)Vrec,
                   cap, nrec, n, (int64_t)kAttnD * 2};
   int rc;
-  if (!n_unique && k > kHeadGroups * kHeadTok) {
-    // more positions than one round of the per-head kernel (C4: k = 2048):
-    // each query head's positions split over workgroups of 64, then the merge
-    constexpr int NW = kAttnWaves;
-    const int64_t ns = cdiv(k, (int64_t)(16 * NW));
-    attn_split_kernel<NW><<<dim3((unsigned)ns, (unsigned)G, (unsigned)BH), NW * kWave, 0, st>>>(q, idx, G, k, rs, scale,
-                                                                                               part, ns);
-    rc = launch_status("attn_split_kernel");
-    if (rc) return rc;
+  if (!n_unique) {
+    // rows per selected position, streamed: 16 waves per workgroup (512
+    // positions) when that gives the chip about 128 workgroups or more,
+    // else 4 (128 positions), split heads merged by attn_merge_kernel
+    const bool wide = BH * G * cdiv(k, (int64_t)(kStreamTok * 16)) >= 96;
+    const int64_t ns = cdiv(k, (int64_t)(kStreamTok * (wide ? 16 : 4)));
+    const dim3 grid((unsigned)ns, (unsigned)G, (unsigned)BH);
+    const bool rec = Krec && Vrec && nrec > 0;
+    if (wide && rec)
+      attn_stream_kernel<16, true><<<grid, 16 * kWave, 0, st>>>(q, idx, G, k, rs, scale, out, part, ns);
+    else if (wide)
+      attn_stream_kernel<16, false><<<grid, 16 * kWave, 0, st>>>(q, idx, G, k, rs, scale, out, part, ns);
+    else if (rec)
+      attn_stream_kernel<4, true><<<grid, 4 * kWave, 0, st>>>(q, idx, G, k, rs, scale, out, part, ns);
+    else
+      attn_stream_kernel<4, false><<<grid, 4 * kWave, 0, st>>>(q, idx, G, k, rs, scale, out, part, ns);
+    rc = launch_status("attn_stream_kernel");
+    if (rc || ns == 1) return rc;
     attn_merge_kernel<<<(unsigned)(BH * G), kAttnD, 0, st>>>(part, G, ns, out);
     return launch_status("attn_merge_kernel");
-  } else if (!n_unique) {
-    // one workgroup per query head over its own positions, no union, no merge
-    attn_head_kernel<<<dim3((unsigned)G, (unsigned)BH), kHeadWaves * kWave, 0, st>>>(q, idx, G, k, rs, scale, out);
-    return launch_status("attn_head_kernel");
   } else {
     // the union list (each distinct row read once), then its groups of kAttnTok tokens
     rc = launch_union(idx, BH, GK, k, n, w, n_unique, st);

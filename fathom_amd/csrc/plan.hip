@@ -44,17 +44,22 @@ __device__ float flog2(float x) {
   return (float)r;
 }
 
-// Exact sum of the 64 lanes' integers, in every lane: DPP row sums (quad_perm
-// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the four row sums
-// read out and added -- a dependent chain of four DPP adds, where bit-sliced
-// ballots take a VALU-to-SALU round per bit.
-__device__ __forceinline__ int wave_sum_dpp(int v) {
-  v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
-  v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
-  v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
-  v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false);
-  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
-         __builtin_amdgcn_readlane(v, 48);
+// Sum of the 64 lanes' values in every lane, for small integers held as
+// floats (every partial sum exact, so the order does not matter): DPP row sums
+// (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the four
+// rows added by v_permlane32_swap and v_permlane16_swap -- all VALU, so the
+// bisection's compare needs no round trip through scalar registers.
+__device__ __forceinline__ float wave_total_exact(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true));
+  const uint32_t x = __float_as_uint(v);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+  const uint32_t y = __float_as_uint(v);
+  const auto p16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
+  return __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
 }
 
 template <int CPL>
@@ -76,15 +81,16 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
     lg[k] = (j < D) ? flog2(fmaxf(g[bh * D + j], 1e-30f)) : -INFINITY;
   }
   // depths are integers in [0, bmax]: a lane's sum is below 2^6, the row's
-  // (an exact integer) equals the float sum in any order
+  // (an exact integer below 2^11) equals the float sum in any order
   constexpr int kSumBits = CPL <= 1 ? 4 : CPL <= 2 ? 5 : 6;
   const float Br = budget ? budget[bh] : budget_value;
-  // the row's depth total at water line mid exceeds the budget
+  // the row's depth total at water line mid exceeds the budget; the clamp is
+  // v_med3 (lg is never NaN: NaN g takes the 1e-30 floor)
   auto over = [&](float mid) {
-    int s = 0;
+    float s = __builtin_amdgcn_fmed3f(rintf((lg[0] - mid) * 0.5f), 0.0f, bm);
 #pragma unroll
-    for (int k = 0; k < CPL; ++k) s += (int)fminf(fmaxf(rintf((lg[k] - mid) * 0.5f), 0.0f), bm);
-    return (float)wave_sum_dpp(s) > Br;
+    for (int k = 1; k < CPL; ++k) s += __builtin_amdgcn_fmed3f(rintf((lg[k] - mid) * 0.5f), 0.0f, bm);
+    return wave_total_exact(s) > Br;
   };
   float lo = -60.0f, hi = 60.0f;
   for (int it = 0; it < iters; ++it) {
