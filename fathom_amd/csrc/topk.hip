@@ -37,7 +37,7 @@ struct RangeShared {
   uint32_t wsum[kMaxWaves];
   uint64_t fin[kWave];  // the last few values of a range, selected by one wave
   uint64_t lo, hi, thr;
-  uint32_t need, done, hsel, fcnt;
+  uint32_t need, done, hsel, fcnt, hcnt;
 };
 
 // The two values of lane pair {i & ~J, i | J} (in some order) for a compare-
@@ -891,10 +891,12 @@ __device__ __forceinline__ void bound_round(const uint32_t (&v)[PER], int cnt, u
   if (above < need && above + c0 >= need) {
     sh.hsel = (uint32_t)(kBins - 1 - 2 * tid);
     sh.need = above;
+    sh.hcnt = c0;
   }
   if (above + c0 < need && above + c >= need) {
     sh.hsel = (uint32_t)(kBins - 2 - 2 * tid);
     sh.need = above + c0;
+    sh.hcnt = c1;
   }
   sh.hist[tid] = 0u;  // for the next round
   sh.hist[tid + kFinThreads] = 0u;
@@ -902,43 +904,51 @@ __device__ __forceinline__ void bound_round(const uint32_t (&v)[PER], int cnt, u
 }
 
 // A lower bound of the need-th largest of the cnt values v (thread t holds
-// values t + 1024 u; need <= cnt): a 2048-bin histogram over [min, max], then
-// one over the bin that holds the need-th largest; the lower edge of the
-// second round's bin.  At least need values reach it, and it lies within
-// (max - min) / 2^22 of the need-th largest.
+// values t + 1024 u; need <= cnt).  The values at or below kKeyNegInf (group
+// maxima of masked positions) are left out of the range: with fewer than need
+// values above it the bound is 0.  A 2048-bin histogram over [min, max] of the
+// others gives the bin that holds the need-th largest; its lower edge is the
+// bound when at most kBoundFine values share the bin (a few extra candidates),
+// else one more round over that bin refines it to within (max - min) / 2^22.
+constexpr uint32_t kBoundFine = 32;
 template <int PER>
 __device__ __forceinline__ uint32_t kth_bound(const uint32_t (&v)[PER], int cnt, uint32_t need, RangeShared &sh) {
   static_assert(kBins == 2 * kFinThreads, "two bins per thread");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
-  uint32_t mn = ~0u, mx = 0u;
+  uint32_t mn = ~0u, mx = 0u, nv = 0u;
 #pragma unroll
-  for (int u = 0; u < PER; ++u)
-    if (tid + u * kFinThreads < cnt) {
+  for (int u = 0; u < PER; ++u) {
+    const bool on = tid + u * kFinThreads < cnt && v[u] > kKeyNegInf;
+    if (on) {
       mn = min(mn, v[u]);
       mx = max(mx, v[u]);
     }
+    nv += (uint32_t)__popcll(__ballot(on));
+  }
   wave_minmax_u32(mn, mx);
   if (lane == 0) {
     sh.wmin[wave] = mn;
-    sh.wmax[wave] = mx;
+    sh.wmax[wave] = ((uint64_t)nv << 32) | mx;  // the wave's count beside its maximum
   }
   sh.hist[tid] = 0u;
   sh.hist[tid + kFinThreads] = 0u;
   __syncthreads();
-  uint32_t lo = ~0u, hi = 0u;
+  uint32_t lo = ~0u, hi = 0u, nvalid = 0u;
   for (int w = 0; w < nw; ++w) {
     lo = min(lo, (uint32_t)sh.wmin[w]);
     hi = max(hi, (uint32_t)sh.wmax[w]);
+    nvalid += (uint32_t)(sh.wmax[w] >> 32);
   }
+  if (nvalid < need) return 0u;  // uniform
   const uint32_t R = hi - lo;
   const int bl = R ? 32 - __clz((int)R) : 0;
   const int sft = bl > 11 ? bl - 11 : 0;  // (v - lo) >> sft < 2048
   bound_round<PER>(v, cnt, need, lo, sft, -1, 0u, sh);
   const uint32_t b = sh.hsel, base = lo + (b << sft);
-  if (sft == 0) return base;  // one value per bin: base is the need-th largest
+  if (sft == 0 || sh.hcnt <= kBoundFine) return base;  // uniform
   const int sft2 = sft > 11 ? sft - 11 : 0;
   const uint32_t need2 = need - sh.need;
-  __syncthreads();  // every thread has read sh.hsel and sh.need
+  __syncthreads();  // every thread has read sh.hsel, sh.need and sh.hcnt
   bound_round<PER>(v, cnt, need2, base, sft2, sft, 0u, sh);
   return base + (sh.hsel << sft2);
 }
