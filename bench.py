@@ -220,11 +220,15 @@ def run_copy_index(torch, bp, off, x, K_dev, V_dev, steps, warmup):
 
 def run_decode_step(torch, bp, off, W, dev, steps, warmup):
     """Config 5: one decode step of a 36-layer model with every layer's index and
-    K/V rows in HBM -- per layer make_plan (the layer's own budget), fused scan +
+    K/V rows in HBM -- per layer the plan (the layer's own budget), fused scan +
     top-k and exact attention over the selected rows.  As scripts/B_kernel_bench.py
     does, each stage (over all 36 layers) is captured in a HIP graph and timed
-    around graph replays; the eager time per step is reported beside it.  Every
-    replayed output must equal the eager one bit for bit."""
+    around graph replays; the eager time per step is reported beside it.  The
+    step is timed twice: with the plan made in the scan's prologue
+    (PlaneStore.plan_scan_topk, the reported step) and as the three separate
+    calls make_plan, scan_topk, gather_attention ("separate_calls").  Every
+    replayed output must equal the eager one bit for bit, and both forms must
+    select the same indices."""
     c = W.CONFIGS[5]
     layers = []
     for L in range(c["layers"]):
@@ -235,70 +239,92 @@ def run_decode_step(torch, bp, off, W, dev, steps, warmup):
         del x
     torch.cuda.synchronize()
     n, BH, k, sink, local = c["n"], c["BH"], c["k"], c["sink"], c["local"]
-    st = [{} for _ in layers]
+
+    def timed(stages, st):
+        # eager steps: reference outputs and the per-call (launch-bound) time
+        for _ in range(warmup):
+            for _, fn in stages:
+                fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            for _, fn in stages:
+                fn()
+        e1.record()
+        torch.cuda.synchronize()
+        eager_ms = e0.elapsed_time(e1) / steps
+        ref = [(s["idx"].clone(), s["out"].clone()) for s in st]
+        graphs = []
+        for _, fn in stages:
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                fn()
+            graphs.append(gph)
+        torch.cuda.synchronize()
+        ms = {name: 0.0 for name, _ in stages}
+        evs = []
+        for it in range(warmup + steps):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(len(graphs) + 1)]
+            e[0].record()
+            for j, gph in enumerate(graphs):
+                gph.replay()
+                e[j + 1].record()
+            if it >= warmup:
+                evs.append(e)
+        torch.cuda.synchronize()
+        for e in evs:
+            for j, (name, _) in enumerate(stages):
+                ms[name] += e[j].elapsed_time(e[j + 1]) / steps
+        for (ri, ro), s in zip(ref, st):
+            if not (torch.equal(ri, s["idx"]) and torch.equal(ro, s["out"])):
+                raise RuntimeError("decode step: a graph replay differs from the eager step")
+        del graphs
+        return ms, eager_ms
+
+    fu = [{} for _ in layers]  # the plan made inside the scan
+
+    def s_plan_scan_topk():
+        for i, ly in enumerate(layers):
+            fu[i]["idx"] = ly["store"].plan_scan_topk(ly["q"], ly["g"], ly["budget"], k, sink, local)
+
+    def s_attn_fu():
+        for i, ly in enumerate(layers):
+            fu[i]["out"] = off.gather_attention(ly["q"], fu[i]["idx"], n, ly["K"], ly["V"], n)[0]
+
+    sp = [{} for _ in layers]  # the three separate calls
 
     def s_plan():
         for i, ly in enumerate(layers):
-            st[i]["plan"] = bp.make_plan(ly["g"], ly["budget"])
+            sp[i]["plan"] = bp.make_plan(ly["g"], ly["budget"])
 
     def s_scan_topk():
         for i, ly in enumerate(layers):
-            st[i]["idx"] = ly["store"].scan_topk(ly["q"], st[i]["plan"], k, sink, local)
+            sp[i]["idx"] = ly["store"].scan_topk(ly["q"], sp[i]["plan"], k, sink, local)
 
-    def s_attn():
+    def s_attn_sp():
         for i, ly in enumerate(layers):
-            st[i]["out"] = off.gather_attention(ly["q"], st[i]["idx"], n, ly["K"], ly["V"], n)[0]
+            sp[i]["out"] = off.gather_attention(ly["q"], sp[i]["idx"], n, ly["K"], ly["V"], n)[0]
 
-    stages = [("plan", s_plan), ("scan_topk", s_scan_topk), ("attn", s_attn)]
-    # eager steps: reference outputs and the per-call (launch-bound) time
-    for _ in range(warmup):
-        for _, fn in stages:
-            fn()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        for _, fn in stages:
-            fn()
-    e1.record()
-    torch.cuda.synchronize()
-    eager_ms = e0.elapsed_time(e1) / steps
-    ref = [(s["idx"].clone(), s["out"].clone()) for s in st]
-    graphs = []
-    for _, fn in stages:
-        gph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gph):
-            fn()
-        graphs.append(gph)
-    torch.cuda.synchronize()
-    ms = {name: 0.0 for name, _ in stages}
-    evs = []
-    for it in range(warmup + steps):
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(len(graphs) + 1)]
-        e[0].record()
-        for j, gph in enumerate(graphs):
-            gph.replay()
-            e[j + 1].record()
-        if it >= warmup:
-            evs.append(e)
-    torch.cuda.synchronize()
-    for e in evs:
-        for j, (name, _) in enumerate(stages):
-            ms[name] += e[j].elapsed_time(e[j + 1]) / steps
-    for (ri, ro), s in zip(ref, st):
-        if not (torch.equal(ri, s["idx"]) and torch.equal(ro, s["out"])):
-            raise RuntimeError("decode step: a graph replay differs from the eager step")
+    ms, eager_ms = timed([("plan_scan_topk", s_plan_scan_topk), ("attn", s_attn_fu)], fu)
+    ms_sp, eager_sp = timed([("plan", s_plan), ("scan_topk", s_scan_topk), ("attn", s_attn_sp)], sp)
+    for a, b in zip(fu, sp):
+        if not (torch.equal(a["idx"], b["idx"]) and torch.equal(a["out"], b["out"])):
+            raise RuntimeError("decode step: plan_scan_topk differs from make_plan + scan_topk")
     step_ms = sum(ms.values())
-    scan_bytes = sum(bp.bytes_planes(s["plan"]["t"], n) for s in st)
-    del graphs, layers, st
+    scan_bytes = sum(bp.bytes_planes(s["plan"]["t"], n) for s in sp)
+    del layers, fu, sp
     torch.cuda.empty_cache()
     return {"workload": c["name"], "layers": c["layers"], "BH": BH, "n": n, "k": k,
             "budgets": [float(b) for b in W.C5_BUDGETS], "timing": "HIP graph per stage over all layers",
             "ms_per_step": step_ms, "eager_ms_per_step": eager_ms,
             "stage_ms_per_step": {s: round(v, 4) for s, v in ms.items()},
-            "scanned_tokens_per_s": c["layers"] * BH * n / (ms["scan_topk"] * 1e-3),
+            "scanned_tokens_per_s": c["layers"] * BH * n / (ms["plan_scan_topk"] * 1e-3),
             "scan_bytes_per_step": scan_bytes,
-            "scan_topk_GBps": scan_bytes / (ms["scan_topk"] * 1e-3) / 1e9}
+            "scan_topk_GBps": scan_bytes / (ms["plan_scan_topk"] * 1e-3) / 1e9,
+            "separate_calls": {"ms_per_step": sum(ms_sp.values()), "eager_ms_per_step": eager_sp,
+                               "stage_ms_per_step": {s: round(v, 4) for s, v in ms_sp.items()}},
+            "indices_equal_separate_calls": True}
 
 
 def _graph_run(torch, fn, reps=20, warm_ms=30.0, timed=10):

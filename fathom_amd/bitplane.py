@@ -332,6 +332,47 @@ class PlaneStore:
                   _stream(q.device))
         return idx
 
+    def plan_scan_topk(self, q, g, budget, k, sink=4, local=32, m=None, bmax=4, iters=30, return_t=False):
+        """make_plan(g, budget, bmax, iters) then scan_topk(q, plan, k, sink, local, m)
+        in one call (kernels/bitplane.py:83-116, then the scan and top-k): the same
+        indices [BH, G, k].  Rows of at most 32768 tokens are planned inside the
+        scan's prologue, so no plan launch precedes it (the decode chain of
+        scripts/B_kernel_bench.py:74).  return_t=True also returns the plan's
+        depths t [BH, D] int8."""
+        _need_gpu(q, g)
+        BH, G, d = q.shape
+        if BH != self.BH:
+            raise AssertionError(f"q has BH={BH}, store has {self.BH}")
+        if tuple(g.shape) != (BH, d):
+            raise ValueError(f"plan_scan_topk: g {tuple(g.shape)} must be [BH, D] = [{BH}, {d}]")
+        if bmax > 4:
+            raise ValueError("the store holds 4 planes: plan with bmax <= 4")
+        n = self.n
+        m = n if m is None else int(m)
+        sub = int(getattr(self, "sub", SUB))
+        qc = q.contiguous().float()
+        gf = g.contiguous().float()
+        idx = torch.empty(BH, G, int(k), dtype=torch.int64, device=q.device)
+        t = torch.empty(BH, d, dtype=torch.int8, device=q.device) if return_t else None
+        units_max, bptr, bval = 0, None, 0.0
+        if torch.is_tensor(budget):
+            if budget.device.type == "cpu" and budget.numel() > 0:
+                bmx = float(budget.float().max())
+                units_max = int(math.floor(bmx)) if math.isfinite(bmx) else 0
+            bptr = budget.to(device=q.device, dtype=torch.float32).expand(BH).contiguous()
+        else:
+            bval = float(budget)
+            units_max = int(math.floor(bval)) if math.isfinite(bval) else 0
+        units_max = max(0, min(units_max, int(bmax) * d)) if units_max > 0 else 0
+        L = _lib.lib()
+        nbytes = L.fathom_plan_scan_topk_workspace_bytes(BH, G, d, int(bmax), n, int(k), int(sink), int(local))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        _lib.call("fathom_plan_scan_topk", _ptr(qc), _ptr(gf), _ptr(bptr), bval, BH, G, d, int(bmax), int(iters),
+                  units_max, ctypes.c_void_p(self.planes32.data_ptr()), ctypes.c_void_p(self.scales_k.data_ptr()), n,
+                  int(self.nsb), sub, m, int(k), int(sink), int(local), _ptr(idx), _ptr(t), _ptr(ws), nbytes,
+                  _stream(q.device))
+        return (idx, t) if return_t else idx
+
     def scan_topk_stages(self, q, plan, k, stages, ws=None, idx=None, sink=4, local=32, m=None):
         """Stages of scan_topk (bit mask of STAGE_*) on a caller-kept workspace
         (bench.py times the candidate pass alone this way; the reference has no

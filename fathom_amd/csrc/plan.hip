@@ -5,62 +5,11 @@
 // of the integer depths is exact in any order); the compacted lists are built
 // with wave prefix sums so every output array is written in full (zero padded)
 // and no separate clear is needed.
-#include "common.hpp"
+#include "plan_core.hpp"
+#include "scan_internal.hpp"
 
 namespace fathom {
 namespace {
-
-// float32 log2 shared bit-for-bit with the CPU oracle: x = m 2^e with m folded
-// into (1/sqrt2, sqrt2], ln m = 2 atanh(s), s = (m-1)/(m+1), odd series to
-// z^11 (z = s^2) in Horner form, log2 x = e + ln m * log2(e), every step a
-// separate IEEE float64 operation (no contraction), rounded once to float32.
-__device__ float flog2(float x) {
-#pragma clang fp contract(off)
-  if (x != x) return x;
-  if (isinf(x)) return x;
-  const uint32_t bits = __float_as_uint(x);
-  int e = (int)((bits >> 23) & 0xFFu) - 127;
-  double m = (double)(int)((bits & 0x7FFFFFu) | 0x800000u) / 8388608.0;
-  if (m > 1.4142135623730951) {
-    m = m * 0.5;
-    e += 1;
-  }
-  const double s = (m - 1.0) / (m + 1.0);
-  const double z = s * s;
-  double p = 1.0 / 23.0;
-  p = p * z; p = p + 1.0 / 21.0;
-  p = p * z; p = p + 1.0 / 19.0;
-  p = p * z; p = p + 1.0 / 17.0;
-  p = p * z; p = p + 1.0 / 15.0;
-  p = p * z; p = p + 1.0 / 13.0;
-  p = p * z; p = p + 1.0 / 11.0;
-  p = p * z; p = p + 1.0 / 9.0;
-  p = p * z; p = p + 1.0 / 7.0;
-  p = p * z; p = p + 1.0 / 5.0;
-  p = p * z; p = p + 1.0 / 3.0;
-  p = p * z; p = p + 1.0;
-  const double ln_m = (2.0 * s) * p;
-  const double r = (double)e + ln_m * 1.4426950408889634;
-  return (float)r;
-}
-
-// Sum of the 64 lanes' values in every lane, for small integers held as
-// floats (every partial sum exact, so the order does not matter): DPP row sums
-// (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the four
-// rows added by v_permlane32_swap and v_permlane16_swap -- all VALU, so the
-// bisection's compare needs no round trip through scalar registers.
-__device__ __forceinline__ float wave_total_exact(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true));
-  const uint32_t x = __float_as_uint(v);
-  const auto p32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-  v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
-  const uint32_t y = __float_as_uint(v);
-  const auto p16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
-  return __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-}
 
 template <int CPL>
 __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, const float *__restrict__ budget,
@@ -75,34 +24,16 @@ __global__ __launch_bounds__(64) void plan_kernel(const float *__restrict__ g, c
   const float bm = (float)bmax;
   float lg[CPL];
 #pragma unroll
-  for (int k = 0; k < CPL; ++k) {
-    const int j = lane * CPL + k;
-    // kernels/bitplane.py:89: lg = log2(max(g, 1e-30)); NaN g takes the 1e-30 floor.
-    lg[k] = (j < D) ? flog2(fmaxf(g[bh * D + j], 1e-30f)) : -INFINITY;
-  }
-  // depths are integers in [0, bmax]: a lane's sum is below 2^6, the row's
-  // (an exact integer below 2^11) equals the float sum in any order
-  constexpr int kSumBits = CPL <= 1 ? 4 : CPL <= 2 ? 5 : 6;
+  for (int k = 0; k < CPL; ++k) lg[k] = plan::channel_lg(g, bh, D, lane * CPL + k);
+  constexpr int kSumBits = CPL <= 1 ? 4 : CPL <= 2 ? 5 : 6;  // a lane's depth total is below 2^6
   const float Br = budget ? budget[bh] : budget_value;
-  // the row's depth total at water line mid exceeds the budget; the clamp is
-  // v_med3 (lg is never NaN: NaN g takes the 1e-30 floor)
-  auto over = [&](float mid) {
-    float s = __builtin_amdgcn_fmed3f(rintf((lg[0] - mid) * 0.5f), 0.0f, bm);
-#pragma unroll
-    for (int k = 1; k < CPL; ++k) s += __builtin_amdgcn_fmed3f(rintf((lg[k] - mid) * 0.5f), 0.0f, bm);
-    return wave_total_exact(s) > Br;
-  };
-  float lo = -60.0f, hi = 60.0f;
-  for (int it = 0; it < iters; ++it) {
-    const float mid = (lo + hi) * 0.5f;
-    if (over(mid)) lo = mid; else hi = mid;
-  }
+  const float hi = plan::water_line<CPL>(lg, Br, bm, iters);
   int t[CPL];
   int cnt_act = 0, cnt_pairs = 0;
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
     const int j = lane * CPL + k;
-    t[k] = (j < D) ? (int)fminf(fmaxf(rintf((lg[k] - hi) * 0.5f), 0.0f), bm) : 0;
+    t[k] = (j < D) ? plan::depth_at(lg[k], hi, bm) : 0;
     if (j < D) t_out[bh * D + j] = (int8_t)t[k];
     cnt_act += t[k] > 0;
     cnt_pairs += t[k];
@@ -177,7 +108,6 @@ __global__ __launch_bounds__(64) void channel_list_kernel(const uint8_t *__restr
 using namespace fathom;
 
 namespace fathom {
-namespace {
 int make_plan_run(const float *g, const float *budget, float budget_value, int64_t BH, int64_t D, int bmax, int iters,
                   int8_t *t, int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls, int32_t *clsn,
                   void *stream) {
@@ -198,7 +128,6 @@ int make_plan_run(const float *g, const float *budget, float budget_value, int64
     plan_kernel<4><<<(unsigned)BH, 64, 0, st>>>(g, budget, bv, d, bmax, iters, t, pairs, npairs, act, nact, cls, clsn);
   return launch_status("plan_kernel");
 }
-}  // namespace
 }  // namespace fathom
 
 extern "C" int fathom_make_plan(const float *g, const float *budget, int64_t BH, int64_t D, int bmax, int iters,

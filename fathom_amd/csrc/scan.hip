@@ -130,8 +130,10 @@ int64_t units_bound(int64_t units_max, int64_t D, int bmax) {
 }
 
 int check_scan(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,
-               const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, const char *who) {
-  if (!q || !cls || !clsn || !planes_sb || !scales_sb) return fail(FATHOM_ERR_INVALID, "%s: null pointer", who);
+               const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, const char *who,
+               bool own_plan = false) {
+  if (!q || (!own_plan && (!cls || !clsn)) || !planes_sb || !scales_sb)
+    return fail(FATHOM_ERR_INVALID, "%s: null pointer", who);
   if (BH < 1 || BH > 65535) return fail(FATHOM_ERR_INVALID, "%s: BH=%lld outside [1, 65535]", who, (long long)BH);
   if (G < 1 || G > 8) return fail(FATHOM_ERR_INVALID, "%s: G=%lld outside [1, 8]", who, (long long)G);
   if (D < 1 || D > kMaxD) return fail(FATHOM_ERR_INVALID, "%s: D=%lld outside [1, %d]", who, (long long)D, kMaxD);
@@ -303,4 +305,83 @@ extern "C" int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, in
                                        int stages, void *stream) {
   return scan_topk_run(q, BH, G, D, cls, clsn, bmax, units_max, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local, idx,
                        workspace, workspace_bytes, stages, stream);
+}
+
+namespace fathom {
+namespace {
+// make_plan's arrays for plan_scan_topk's long rows, past the scan's workspace.
+size_t plan_arrays_ws(int64_t BH, int64_t D, int bmax) {
+  return ws_align((size_t)(BH * D)) + ws_align((size_t)(BH * D * bmax) * 4) + 2 * ws_align((size_t)BH * 4) +
+         ws_align((size_t)(BH * D) * 4) + ws_align((size_t)(BH * bmax * D) * 4) + ws_align((size_t)(BH * bmax) * 4);
+}
+}  // namespace
+}  // namespace fathom
+
+extern "C" size_t fathom_plan_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t D, int bmax, int64_t n, int64_t k,
+                                                        int64_t sink, int64_t local) {
+  const int64_t kk = k - sink - local;
+  if (BH < 1 || G < 1 || D < 1 || bmax < 1 || n < 1 || kk < 0) return 0;
+  return scan_topk_ws(BH * G, n, k) + plan_arrays_ws(BH, D, bmax);
+}
+
+extern "C" int fathom_plan_scan_topk(const float *q, const float *g, const float *budget, float budget_value, int64_t BH,
+                                     int64_t G, int64_t D, int bmax, int iters, int64_t units_max, const void *planes_sb,
+                                     const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k,
+                                     int64_t sink, int64_t local, int64_t *idx, int8_t *t_out, void *workspace,
+                                     size_t workspace_bytes, void *stream) {
+  if (!g) return fail(FATHOM_ERR_INVALID, "plan_scan_topk: null pointer");
+  if (iters < 0 || iters > 200) return fail(FATHOM_ERR_INVALID, "plan_scan_topk: iters=%d outside [0, 200]", iters);
+  int rc = check_scan(q, BH, G, D, nullptr, nullptr, bmax, planes_sb, scales_sb, n, nsb, sub, "plan_scan_topk", true);
+  if (rc) return rc;
+  if (!idx) return fail(FATHOM_ERR_INVALID, "plan_scan_topk: null output");
+  const int64_t rows = BH * G;
+  rc = check_topk_args(rows, n, m, k, sink, local, "plan_scan_topk");
+  if (rc) return rc;
+  const size_t need = fathom_plan_scan_topk_workspace_bytes(BH, G, D, bmax, n, k, sink, local);
+  if (!workspace || workspace_bytes < need)
+    return fail(FATHOM_ERR_WORKSPACE, "plan_scan_topk: workspace %zu bytes, need %zu", workspace_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t kk = k - sink - local;
+  const size_t sws = scan_topk_ws(rows, n, k);
+  if (n > kRowSelectMax || kk == 0) {
+    // make_plan into the workspace, then the fused scan + top-k
+    char *p = static_cast<char *>(workspace) + sws;
+    int8_t *t = t_out ? t_out : reinterpret_cast<int8_t *>(p);
+    p += ws_align((size_t)(BH * D));
+    int32_t *pairs = reinterpret_cast<int32_t *>(p);
+    p += ws_align((size_t)(BH * D * bmax) * 4);
+    int32_t *npairs = reinterpret_cast<int32_t *>(p);
+    p += ws_align((size_t)BH * 4);
+    int32_t *nact = reinterpret_cast<int32_t *>(p);
+    p += ws_align((size_t)BH * 4);
+    int32_t *act = reinterpret_cast<int32_t *>(p);
+    p += ws_align((size_t)(BH * D) * 4);
+    int32_t *cls = reinterpret_cast<int32_t *>(p);
+    p += ws_align((size_t)(BH * bmax * D) * 4);
+    int32_t *clsn = reinterpret_cast<int32_t *>(p);
+    rc = make_plan_run(g, budget, budget_value, BH, D, bmax, iters, t, pairs, npairs, act, nact, cls, clsn, stream);
+    if (rc) return rc;
+    return scan_topk_run(q, BH, G, D, cls, clsn, bmax, units_max, planes_sb, scales_sb, n, nsb, sub, m, k, sink, local,
+                         idx, workspace, sws, FATHOM_STAGE_ALL, stream);
+  }
+  // short rows: every workgroup of the scan plans its row in the prologue
+  // (the plan kernel's arithmetic), then the rows are selected as in scan_topk
+  const int64_t nblk = cdiv(n, kBlk);
+  ScanArgs a = make_args(q, G, D, nullptr, nullptr, bmax, planes_sb, scales_sb, n, nsb, sub);
+  a.blk0 = 0;
+  a.blk_end = nblk;
+  a.wt0 = 0;
+  a.g = g;
+  a.budget = budget;
+  a.budget_value = budget_value;
+  a.iters = iters;
+  a.t_out = t_out;
+  Emit es{};
+  es.out = static_cast<float *>(workspace);
+  es.gmax = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + ws_align((size_t)rows * (size_t)n * 4));
+  es.sink = sink;
+  es.lstart = (m - local) > 0 ? (m - local) : 0;
+  rc = launch_scan<kEmitScoresMax>(a, cdiv(nblk, kWB), BH, es, units_bound(units_max, D, bmax), st);
+  if (rc) return rc;
+  return launch_rowselect_gmax(es.out, es.gmax, rows, n, m, k, sink, local, idx, st);
 }

@@ -39,6 +39,7 @@
 // mapped host memory give the same scores bit for bit.
 #pragma once
 #include "topk_internal.hpp"
+#include "plan_core.hpp"
 
 namespace fathom {
 namespace sc {
@@ -79,6 +80,14 @@ struct ScanArgs {
   int64_t wt_stride;       // wave-tiles between consecutive list entries
   int64_t nwt;             // list entries per row
   int D, G, bmax, ncls;    // classes 1..ncls are scanned (ncls = min(bmax, 4))
+  // g non-null: the prologue plans its row itself (make_plan of g [BH, D] and
+  // the row's budget, budget[bh] or budget_value, `iters` bisection steps;
+  // cls and clsn unused) and the first workgroup of a row writes the plan's
+  // depths to t_out [BH, D] (if non-null)
+  const float *g, *budget;
+  float budget_value;
+  int iters;
+  int8_t *t_out;
 };
 
 struct PlanTab;
@@ -135,6 +144,7 @@ struct Shared {
   _Float16 qa[kRows][kMaxUnits];         // score A rows: 2h = hi(q_hj 2^-(p + sigma_h)), 2h + 1 = lo
   _Float16 ca[kRows][kMaxUnits];         // C A rows: the split of q_hj 2^-sigma_h (2^-t_j - 1), first units only
   uint16_t schan[kMaxD];                 // channel slot -> channel (prologue)
+  int pnc[4];                            // class sizes of a plan made in the prologue
   int sig[kMaxG];                        // sigma_h: the exponent of the head's largest |q|
   int U;                                 // units, padded to whole slices
   int ureal;                             // units of the plan
@@ -174,32 +184,65 @@ __device__ __forceinline__ void set_priority_by_tiles_left(int64_t left) {
 // f16 truncation (round toward zero) of x.
 __device__ __forceinline__ _Float16 f16_rtz(float x) { return __builtin_amdgcn_cvt_pkrtz(x, 0.0f)[0]; }
 
+// The row's plan made by one wave (a.g set): make_plan's depths of the row's
+// channels (2 per lane, the plan kernel's arithmetic), written to a.t_out by
+// the row's first workgroup, and its class lists -- channels of depth c + 1,
+// ascending, as make_plan's cls -- into sh.schan with their sizes in sh.pnc.
+__device__ __forceinline__ void plan_row(Shared &sh, const ScanArgs &a, int64_t bh, int lane) {
+  static_assert(kMaxD == 2 * kWave, "two channels per lane");
+  const float bm = (float)a.bmax;
+  float lg[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) lg[k] = plan::channel_lg(a.g, bh, a.D, 2 * lane + k);
+  const float Br = a.budget ? a.budget[bh] : a.budget_value;
+  const float hi = plan::water_line<2>(lg, Br, bm, a.iters);
+  int t[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int j = 2 * lane + k;
+    t[k] = j < a.D ? plan::depth_at(lg[k], hi, bm) : 0;
+    if (a.t_out && blockIdx.x == 0 && j < a.D) a.t_out[bh * a.D + j] = (int8_t)t[k];
+  }
+  int s = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int cnt = c < a.ncls ? (t[0] == c + 1) + (t[1] == c + 1) : 0;
+    int pos = s + wave_excl_scan_small<2>(cnt, lane);
+    const int total = wave_sum_small<2>(cnt);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      if (c < a.ncls && t[k] == c + 1) sh.schan[pos++] = (uint16_t)(2 * lane + k);
+    if (lane == 0) sh.pnc[c] = total;
+    s += total;
+  }
+}
+
 // Workgroup prologue: the plan tables in LDS, with zero units from the plan's
 // last up to upad units (at least to a whole slice).  Returns the padded unit
 // count.
 __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_t bh, int upad) {
   const int tid = threadIdx.x;
+  const bool own = a.g != nullptr;  // the row planned here
   int nc[4], SF[4], UE[4];
   int s = 0, u = 0;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    nc[c] = c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
+    nc[c] = !own && c < a.ncls ? min(max(ld_uniform(a.clsn + bh * a.bmax + c), 0), a.D) : 0;
     nc[c] = min(nc[c], a.D - s);  // at most D slots in all
     s += nc[c];
     u += nc[c] * (c + 1);
     SF[c] = s;
     UE[c] = u;
   }
-  const int nact = s, ureal = u;
-  const int U = (ureal + kSlice - 1) / kSlice * kSlice;
-  const int UP = min(max(U, upad), kMaxUnits);
   // the prologue's global loads are issued together: the class lists (every
-  // in-range entry of the bmax x D table) and the queries
+  // in-range entry of the bmax x D table) and the queries; or wave 0 plans the
+  // row while the others load the queries
   {
     static_assert(kMaxD == 2 * kWave, "two channels per lane");
     const int nthr = (int)blockDim.x;
     const int w = tid >> 6, l = tid & 63, nw = nthr >> 6;
-    for (int i0 = tid; i0 < 4 * kMaxD; i0 += 2 * nthr) {
+    if (own && w == 0) plan_row(sh, a, bh, l);
+    for (int i0 = tid; !own && i0 < 4 * kMaxD; i0 += 2 * nthr) {
       int jr[2];
 #pragma unroll
       for (int u2 = 0; u2 < 2; ++u2) {
@@ -236,6 +279,21 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
       }
     }
   }
+  if (own) {  // uniform: the class sizes of the plan made above
+    __syncthreads();
+    s = u = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      nc[c] = sh.pnc[c];
+      s += nc[c];
+      u += nc[c] * (c + 1);
+      SF[c] = s;
+      UE[c] = u;
+    }
+  }
+  const int nact = s, ureal = u;
+  const int U = (ureal + kSlice - 1) / kSlice * kSlice;
+  const int UP = min(max(U, upad), kMaxUnits);
   if (tid == 0) {
     sh.U = U;
     sh.ureal = ureal;

@@ -13,4 +13,9 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
                   int64_t k, int64_t sink, int64_t local, int64_t *idx, void *workspace, size_t workspace_bytes,
                   int stages, void *stream);
 
+// make_plan on the device (budget [BH], or budget_value when budget is null).
+int make_plan_run(const float *g, const float *budget, float budget_value, int64_t BH, int64_t D, int bmax, int iters,
+                  int8_t *t, int32_t *pairs, int32_t *npairs, int32_t *act, int32_t *nact, int32_t *cls, int32_t *clsn,
+                  void *stream);
+
 }  // namespace fathom

@@ -203,6 +203,28 @@ int fathom_scan_topk_stages(const float *q, int64_t BH, int64_t G, int64_t D, co
                             int64_t *idx, void *workspace, size_t workspace_bytes, int stages, void *stream);
 
 /*
+ * make_plan followed by the fused scan + top-k in one call: idx is identical
+ * to fathom_make_plan (budget [BH], or budget_value for every row when budget
+ * is null; bmax, iters as there) then fathom_scan_topk with that plan's cls and
+ * clsn (kernels/bitplane.py:83-116 then :319-338 and :372-378, the plan ->
+ * scan -> top-k stages of scripts/B_kernel_bench.py:74).  For rows of at most
+ * 32768 tokens (D <= 128) every workgroup of the scan makes its row's plan in
+ * its prologue with the plan kernel's arithmetic, so no plan launch and no
+ * plan arrays precede the scan: the decode form of the chain.  Longer rows run
+ * the plan kernel into the workspace first.  t_out [BH, D] int8 (nullable)
+ * receives the plan's depths.  It composes reference stages and has no single
+ * counterpart in the reference.
+ * workspace: fathom_plan_scan_topk_workspace_bytes(BH, G, D, bmax, n, k, sink,
+ * local) bytes.
+ */
+size_t fathom_plan_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_t D, int bmax, int64_t n, int64_t k,
+                                             int64_t sink, int64_t local);
+int fathom_plan_scan_topk(const float *q, const float *g, const float *budget, float budget_value, int64_t BH, int64_t G,
+                          int64_t D, int bmax, int iters, int64_t units_max, const void *planes_sb, const void *scales_sb,
+                          int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
+                          int64_t *idx, int8_t *t_out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * fathom_scan_topk without a workspace argument, for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It has no counterpart in the reference.

@@ -613,6 +613,35 @@ def test_scan_topk_fused_equals_unfused(cfg, n, BH, k, sub):
     torch.testing.assert_close(got, ref, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("cfg,n,BH,k,budget", [(5, 32768, 4, 512, None), (5, 32768, 3, 512, 92.0),
+                                               (2, 16421, 2, 512, "rows"), (1, 16384, None, 128, None),
+                                               (4, 20000, 2, 2048, 40.0), (2, 5000, 3, 300, 17.5), (2, 700, 1, 36, None),
+                                               (2, 40000, 2, 512, "rows")])
+def test_plan_scan_topk_equals_plan_then_scan_topk(cfg, n, BH, k, budget):
+    """make_plan + scan_topk in one call: rows of at most 32768 tokens planned
+    in the scan's prologue (C5 at the config budget and at 92 bits, per-row
+    budgets, G = 1, 4, 7, kk = 0), longer rows through the plan kernel.  The
+    indices and the plan's depths equal the two-call chain's, on two calls in a
+    row."""
+    print(f"[plan-scan-topk] cfg={cfg} n={n} BH={BH} k={k} budget={budget}", flush=True)
+    x = W.config_inputs(cfg, seed=1, n=n, BH=BH)
+    st = bp.PlaneStore(x["K"].to(DEV), keep_code=False)
+    q, g = x["q"].to(DEV), x["g"].to(DEV)
+    bh = q.shape[0]
+    if budget == "rows":
+        budget = torch.linspace(20.0, 100.0, bh, device=DEV)
+    elif budget is None:
+        budget = x["budget"]
+    sink, local = x["sink"], x["local"]
+    plan = bp.make_plan(g, budget)
+    ref = st.scan_topk(q, plan, k, sink, local)
+    for _ in range(2):
+        got, t = st.plan_scan_topk(q, g, budget, k, sink, local, return_t=True)
+        torch.testing.assert_close(got, ref, rtol=0, atol=0)
+        torch.testing.assert_close(t, plan["t"], rtol=0, atol=0)
+    assert torch.equal(st.plan_scan_topk(q, g, budget, k, sink, local), ref)
+
+
 @pytest.mark.parametrize("umax", [16, 48, 0, None])
 def test_scan_topk_fused_plan_tables(umax):
     """Long rows: the candidate pass starts from the plan tables the sample
