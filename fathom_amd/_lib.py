@@ -42,6 +42,10 @@ PROTOTYPES = {
     "fathom_plan_scan_topk_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64]),
     "fathom_plan_scan_topk": (_i32, [_vp, _vp, _vp, ctypes.c_float, _i64, _i64, _i64, _i32, _i32, _i64, _vp, _vp, _i64,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "fathom_plan_scan_topk_attention_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64]),
+    "fathom_plan_scan_topk_attention": (_i32, [_vp, _vp, _vp, ctypes.c_float, _i64, _i64, _i64, _i32, _i32, _i64, _vp,
+                                               _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64,
+                                               ctypes.c_float, _vp, _vp, _sz, _vp]),
     "fathom_scan_topk_noalloc": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                         _i64, _i64, _vp, _vp]),
     "fathom_topk_workspace_bytes": (_sz, [_i64, _i64, _i64]),

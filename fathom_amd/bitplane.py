@@ -332,13 +332,9 @@ class PlaneStore:
                   _stream(q.device))
         return idx
 
-    def plan_scan_topk(self, q, g, budget, k, sink=4, local=32, m=None, bmax=4, iters=30, return_t=False):
-        """make_plan(g, budget, bmax, iters) then scan_topk(q, plan, k, sink, local, m)
-        in one call (kernels/bitplane.py:83-116, then the scan and top-k): the same
-        indices [BH, G, k].  Rows of at most 32768 tokens are planned inside the
-        scan's prologue, so no plan launch precedes it (the decode chain of
-        scripts/B_kernel_bench.py:74).  return_t=True also returns the plan's
-        depths t [BH, D] int8."""
+    def _plan_call_args(self, q, g, budget, bmax):
+        """Shared argument checks of the plan_scan_topk calls: (qc, gf, budget
+        pointer tensor or None, budget value, units bound)."""
         _need_gpu(q, g)
         BH, G, d = q.shape
         if BH != self.BH:
@@ -347,13 +343,6 @@ class PlaneStore:
             raise ValueError(f"plan_scan_topk: g {tuple(g.shape)} must be [BH, D] = [{BH}, {d}]")
         if bmax > 4:
             raise ValueError("the store holds 4 planes: plan with bmax <= 4")
-        n = self.n
-        m = n if m is None else int(m)
-        sub = int(getattr(self, "sub", SUB))
-        qc = q.contiguous().float()
-        gf = g.contiguous().float()
-        idx = torch.empty(BH, G, int(k), dtype=torch.int64, device=q.device)
-        t = torch.empty(BH, d, dtype=torch.int8, device=q.device) if return_t else None
         units_max, bptr, bval = 0, None, 0.0
         if torch.is_tensor(budget):
             if budget.device.type == "cpu" and budget.numel() > 0:
@@ -364,6 +353,55 @@ class PlaneStore:
             bval = float(budget)
             units_max = int(math.floor(bval)) if math.isfinite(bval) else 0
         units_max = max(0, min(units_max, int(bmax) * d)) if units_max > 0 else 0
+        return q.contiguous().float(), g.contiguous().float(), bptr, bval, units_max
+
+    def plan_scan_topk_attention(self, q, g, budget, k, Ksrc, Vsrc, sink=4, local=32, m=None, bmax=4, iters=30,
+                                 scale=None):
+        """plan_scan_topk(q, g, budget, k, ...) then offload.gather_attention over its
+        indices with K/V bf16 rows [BH, cap, 128] in device memory: the decode
+        step's plan -> scan -> top-k -> gather + attention chain
+        (scripts/B_kernel_bench.py:64-101) in one call.  Rows of at most 32768
+        tokens with k <= 512 select and attend in the same workgroups.  Returns
+        (idx [BH, G, k] int64, out [BH, G, 128] fp32), equal to the separate
+        calls'."""
+        _need_gpu(q, g, Ksrc, Vsrc)
+        BH, G, d = q.shape
+        for name, t in (("Ksrc", Ksrc), ("Vsrc", Vsrc)):
+            if t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[0] != BH or t.shape[2] != d or not t.is_contiguous():
+                raise ValueError(f"plan_scan_topk_attention: {name} must be contiguous bf16 [BH, cap, {d}]")
+        if Ksrc.shape != Vsrc.shape:
+            raise ValueError("plan_scan_topk_attention: Ksrc and Vsrc shapes differ")
+        qc, gf, bptr, bval, units_max = self._plan_call_args(q, g, budget, bmax)
+        n = self.n
+        m = n if m is None else int(m)
+        sub = int(getattr(self, "sub", SUB))
+        idx = torch.empty(BH, G, int(k), dtype=torch.int64, device=q.device)
+        out = torch.empty(BH, G, d, dtype=torch.float32, device=q.device)
+        sc = float(d) ** -0.5 if scale is None else float(scale)
+        L = _lib.lib()
+        nbytes = L.fathom_plan_scan_topk_attention_workspace_bytes(BH, G, d, int(bmax), n, int(k), int(sink), int(local))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        _lib.call("fathom_plan_scan_topk_attention", _ptr(qc), _ptr(gf), _ptr(bptr), bval, BH, G, d, int(bmax),
+                  int(iters), units_max, ctypes.c_void_p(self.planes32.data_ptr()),
+                  ctypes.c_void_p(self.scales_k.data_ptr()), n, int(self.nsb), sub, m, int(k), int(sink), int(local),
+                  _ptr(idx), None, ctypes.c_void_p(Ksrc.data_ptr()), ctypes.c_void_p(Vsrc.data_ptr()), int(Ksrc.shape[1]),
+                  sc, _ptr(out), _ptr(ws), nbytes, _stream(q.device))
+        return idx, out
+
+    def plan_scan_topk(self, q, g, budget, k, sink=4, local=32, m=None, bmax=4, iters=30, return_t=False):
+        """make_plan(g, budget, bmax, iters) then scan_topk(q, plan, k, sink, local, m)
+        in one call (kernels/bitplane.py:83-116, then the scan and top-k): the same
+        indices [BH, G, k].  Rows of at most 32768 tokens are planned inside the
+        scan's prologue, so no plan launch precedes it (the decode chain of
+        scripts/B_kernel_bench.py:74).  return_t=True also returns the plan's
+        depths t [BH, D] int8."""
+        qc, gf, bptr, bval, units_max = self._plan_call_args(q, g, budget, bmax)
+        BH, G, d = q.shape
+        n = self.n
+        m = n if m is None else int(m)
+        sub = int(getattr(self, "sub", SUB))
+        idx = torch.empty(BH, G, int(k), dtype=torch.int64, device=q.device)
+        t = torch.empty(BH, d, dtype=torch.int8, device=q.device) if return_t else None
         L = _lib.lib()
         nbytes = L.fathom_plan_scan_topk_workspace_bytes(BH, G, d, int(bmax), n, int(k), int(sink), int(local))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)

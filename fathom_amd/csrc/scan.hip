@@ -4,6 +4,7 @@
 
 #include "scan_core.hpp"
 #include "scan_internal.hpp"
+#include "attn_core.hpp"
 
 namespace fathom {
 namespace {
@@ -324,11 +325,21 @@ extern "C" size_t fathom_plan_scan_topk_workspace_bytes(int64_t BH, int64_t G, i
   return scan_topk_ws(BH * G, n, k) + plan_arrays_ws(BH, D, bmax);
 }
 
-extern "C" int fathom_plan_scan_topk(const float *q, const float *g, const float *budget, float budget_value, int64_t BH,
-                                     int64_t G, int64_t D, int bmax, int iters, int64_t units_max, const void *planes_sb,
-                                     const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k,
-                                     int64_t sink, int64_t local, int64_t *idx, int8_t *t_out, void *workspace,
-                                     size_t workspace_bytes, void *stream) {
+namespace fathom {
+namespace {
+// The attention of fathom_plan_scan_topk_attention (null: none).
+struct AttnOut {
+  const void *K, *V;
+  int64_t cap;
+  float scale;
+  float *out;
+};
+
+int plan_scan_topk_run(const float *q, const float *g, const float *budget, float budget_value, int64_t BH, int64_t G,
+                       int64_t D, int bmax, int iters, int64_t units_max, const void *planes_sb, const void *scales_sb,
+                       int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
+                       int64_t *idx, int8_t *t_out, void *workspace, size_t workspace_bytes, const AttnOut *att,
+                       void *stream) {
   if (!g) return fail(FATHOM_ERR_INVALID, "plan_scan_topk: null pointer");
   if (iters < 0 || iters > 200) return fail(FATHOM_ERR_INVALID, "plan_scan_topk: iters=%d outside [0, 200]", iters);
   int rc = check_scan(q, BH, G, D, nullptr, nullptr, bmax, planes_sb, scales_sb, n, nsb, sub, "plan_scan_topk", true);
@@ -383,5 +394,58 @@ extern "C" int fathom_plan_scan_topk(const float *q, const float *g, const float
   es.lstart = (m - local) > 0 ? (m - local) : 0;
   rc = launch_scan<kEmitScoresMax>(a, cdiv(nblk, kWB), BH, es, units_bound(units_max, D, bmax), st);
   if (rc) return rc;
+  if (att)  // the selection's workgroups go on to their head's attention
+    return launch_rowselect_gmax_attn(es.out, es.gmax, rows, n, m, k, sink, local, idx, q, G, att->K, att->V, att->cap,
+                                      att->scale, att->out, st);
   return launch_rowselect_gmax(es.out, es.gmax, rows, n, m, k, sink, local, idx, st);
+}
+}  // namespace
+}  // namespace fathom
+
+extern "C" int fathom_plan_scan_topk(const float *q, const float *g, const float *budget, float budget_value, int64_t BH,
+                                     int64_t G, int64_t D, int bmax, int iters, int64_t units_max, const void *planes_sb,
+                                     const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k,
+                                     int64_t sink, int64_t local, int64_t *idx, int8_t *t_out, void *workspace,
+                                     size_t workspace_bytes, void *stream) {
+  return plan_scan_topk_run(q, g, budget, budget_value, BH, G, D, bmax, iters, units_max, planes_sb, scales_sb, n, nsb,
+                            sub, m, k, sink, local, idx, t_out, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" size_t fathom_plan_scan_topk_attention_workspace_bytes(int64_t BH, int64_t G, int64_t D, int bmax, int64_t n,
+                                                                  int64_t k, int64_t sink, int64_t local) {
+  const size_t base = fathom_plan_scan_topk_workspace_bytes(BH, G, D, bmax, n, k, sink, local);
+  return base ? base + ws_align(fathom_gather_attention_workspace_bytes(BH, G, k)) : 0;
+}
+
+extern "C" int fathom_plan_scan_topk_attention(const float *q, const float *g, const float *budget, float budget_value,
+                                               int64_t BH, int64_t G, int64_t D, int bmax, int iters, int64_t units_max,
+                                               const void *planes_sb, const void *scales_sb, int64_t n, int64_t nsb,
+                                               int64_t sub, int64_t m, int64_t k, int64_t sink, int64_t local,
+                                               int64_t *idx, int8_t *t_out, const void *Ksrc, const void *Vsrc,
+                                               int64_t cap, float scale, float *out, void *workspace,
+                                               size_t workspace_bytes, void *stream) {
+  if (!Ksrc || !Vsrc || !out) return fail(FATHOM_ERR_INVALID, "plan_scan_topk_attention: null pointer");
+  if (D != 128) return fail(FATHOM_ERR_INVALID, "plan_scan_topk_attention: D=%lld, attention needs 128", (long long)D);
+  if (cap < 0) return fail(FATHOM_ERR_INVALID, "plan_scan_topk_attention: cap=%lld", (long long)cap);
+  const size_t need = fathom_plan_scan_topk_attention_workspace_bytes(BH, G, D, bmax, n, k, sink, local);
+  if (!workspace || workspace_bytes < need)
+    return fail(FATHOM_ERR_WORKSPACE, "plan_scan_topk_attention: workspace %zu bytes, need %zu", workspace_bytes, need);
+  const size_t pws = fathom_plan_scan_topk_workspace_bytes(BH, G, D, bmax, n, k, sink, local);
+  const int64_t kk = k - sink - local;
+  // fused where gather_attention would take one 16-wave split per head, so
+  // the outputs are the two calls' bit for bit
+  const bool fused = n <= kRowSelectMax && kk > 0 && k <= 512 && attn::attn_wide(BH, G, k) &&
+                     ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(Ksrc) |
+                       reinterpret_cast<uintptr_t>(Vsrc)) & 7) == 0;
+  if (fused) {
+    const AttnOut att{Ksrc, Vsrc, cap, scale, out};
+    return plan_scan_topk_run(q, g, budget, budget_value, BH, G, D, bmax, iters, units_max, planes_sb, scales_sb, n, nsb,
+                              sub, m, k, sink, local, idx, t_out, workspace, pws, &att, stream);
+  }
+  // the two calls: the selection, then gather_attention over its indices
+  int rc = plan_scan_topk_run(q, g, budget, budget_value, BH, G, D, bmax, iters, units_max, planes_sb, scales_sb, n, nsb,
+                              sub, m, k, sink, local, idx, t_out, workspace, pws, nullptr, stream);
+  if (rc) return rc;
+  return fathom_gather_attention(q, idx, BH, G, k, n, Ksrc, Vsrc, cap, nullptr, nullptr, 0, scale, out, nullptr,
+                                 static_cast<char *>(workspace) + pws, need - pws, stream);
 }

@@ -16,6 +16,7 @@
 // and a 64-bit K64 needs at most six rounds.
 #include "topk_internal.hpp"
 #include "scan_core.hpp"
+#include "attn_core.hpp"
 
 namespace fathom {
 namespace {
@@ -1148,17 +1149,12 @@ __global__ __launch_bounds__(kSelThreads) void select_groups_kernel(const uint32
 // for spread scores).  Up to 2048 candidates are ranked by one sort; more are
 // selected first; rows whose candidates outgrow the LDS list (ties around T)
 // are selected from the whole row.
-__global__ __launch_bounds__(kFinThreads) void rowselect_gmax_kernel(const float *__restrict__ scores,
-                                                                     const uint32_t *__restrict__ gmax, int64_t n,
-                                                                     int64_t m, int64_t k, int64_t sink, int64_t local,
-                                                                     int64_t *__restrict__ idx) {
-  constexpr int kGroups = (int)(kRowSelectMax / kGroupTok);
-  constexpr int kPer = kGroups / kFinThreads;
-  __shared__ uint64_t cl[kCandLds];
-  __shared__ uint64_t ss[kMaxK];
-  __shared__ RangeShared sh;
-  __shared__ uint16_t glist[kGroups];
-  __shared__ uint32_t s_cnt;
+constexpr int kGmaxGroups = (int)(kRowSelectMax / kGroupTok);
+__device__ __forceinline__ void rowselect_gmax_row(const float *__restrict__ scores, const uint32_t *__restrict__ gmax,
+                                                   int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+                                                   int64_t *__restrict__ idx, uint64_t *cl, uint64_t *ss,
+                                                   RangeShared &sh, uint16_t *glist, uint32_t &s_cnt) {
+  constexpr int kPer = kGmaxGroups / kFinThreads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
   const int64_t row = blockIdx.x;
   const float *rs = scores + row * n;
@@ -1261,6 +1257,43 @@ __global__ __launch_bounds__(kFinThreads) void rowselect_gmax_kernel(const float
     if (rank < got) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x);
   });
   write_fixed(out, got, kk, m, sink, local);
+}
+
+// The selection of rowselect_gmax_row, one workgroup per row.  ATTN (the
+// decode step's selection + attention, k <= 512, rows in device memory): the
+// workgroup then runs the attention of its query head over the k indices it
+// wrote, exactly as gather_attention's attn_stream_kernel does for one split
+// (16 waves of 32 positions), so out equals gather_attention's output.
+struct RowAttn {
+  const float *q;  // [rows, D] fp32 query heads (row = bh * G + g)
+  int64_t G;
+  attn::RowSrc rs;
+  float scale;
+  float *out;      // [rows, D] fp32
+};
+template <bool ATTN>
+__global__ __launch_bounds__(kFinThreads) void rowselect_gmax_kernel(const float *__restrict__ scores,
+                                                                     const uint32_t *__restrict__ gmax, int64_t n,
+                                                                     int64_t m, int64_t k, int64_t sink, int64_t local,
+                                                                     int64_t *__restrict__ idx, RowAttn ra) {
+  __shared__ uint64_t cl[kCandLds];
+  __shared__ uint64_t ss[kMaxK];
+  __shared__ RangeShared sh;
+  __shared__ uint16_t glist[kGmaxGroups];
+  __shared__ uint32_t s_cnt;
+  rowselect_gmax_row(scores, gmax, n, m, k, sink, local, idx, cl, ss, sh, glist, s_cnt);
+  if constexpr (ATTN) {
+    constexpr int NW = kFinThreads / kWave;
+    static_assert(NW == 16, "one attention split of 16 waves");
+    static_assert(sizeof(float) * (2 * NW + NW * attn::kAttnD) <= sizeof(cl), "the attention's LDS in cl");
+    __syncthreads();  // the row's indices are written (and cl is free)
+    const int64_t row = blockIdx.x, bh = row / ra.G;
+    const int64_t *ig = idx + row * k;
+    float *wm = reinterpret_cast<float *>(cl), *wl = wm + NW;
+    auto wo = reinterpret_cast<float(*)[attn::kAttnD]>(wl + NW);
+    attn::attn_stream_block<NW, false>(ra.q + row * attn::kAttnD, [&](int64_t j) { return ig[j]; }, k, 0, bh, ra.rs,
+                                       ra.scale, wm, wl, wo, ra.out + row * attn::kAttnD, nullptr, true);
+  }
 }
 
 __global__ __launch_bounds__(256) void fixed_only_kernel(int64_t rows, int64_t m, int64_t k, int64_t sink,
@@ -1388,7 +1421,17 @@ int launch_rowselect(const float *scores, int64_t rows, int64_t n, int64_t m, in
 
 int launch_rowselect_gmax(const float *scores, const uint32_t *gmax, int64_t rows, int64_t n, int64_t m, int64_t k,
                           int64_t sink, int64_t local, int64_t *idx, hipStream_t st) {
-  rowselect_gmax_kernel<<<(unsigned)rows, kFinThreads, 0, st>>>(scores, gmax, n, m, k, sink, local, idx);
+  rowselect_gmax_kernel<false><<<(unsigned)rows, kFinThreads, 0, st>>>(scores, gmax, n, m, k, sink, local, idx, RowAttn{});
+  return launch_status("rowselect_gmax_kernel");
+}
+
+int launch_rowselect_gmax_attn(const float *scores, const uint32_t *gmax, int64_t rows, int64_t n, int64_t m, int64_t k,
+                               int64_t sink, int64_t local, int64_t *idx, const float *q, int64_t G, const void *K,
+                               const void *V, int64_t cap, float scale, float *out, hipStream_t st) {
+  if (k > kFinThreads / 2) return fail(FATHOM_ERR_INVALID, "rowselect_gmax_attn: k=%lld exceeds 512", (long long)k);
+  RowAttn ra{q, G, attn::RowSrc{(const char *)K, (const char *)V, nullptr, nullptr, cap, 0, n, 2 * attn::kAttnD}, scale,
+             out};
+  rowselect_gmax_kernel<true><<<(unsigned)rows, kFinThreads, 0, st>>>(scores, gmax, n, m, k, sink, local, idx, ra);
   return launch_status("rowselect_gmax_kernel");
 }
 

@@ -145,6 +145,13 @@ int launch_rowselect(const float *scores, int64_t rows, int64_t n, int64_t m, in
 // largest masked keys): only the groups that can hold a top-kk key are read.
 int launch_rowselect_gmax(const float *scores, const uint32_t *gmax, int64_t rows, int64_t n, int64_t m, int64_t k,
                           int64_t sink, int64_t local, int64_t *idx, hipStream_t st);
+// launch_rowselect_gmax, then in the same workgroup the attention of each row's
+// query head (row = bh * G + g) over its k <= 512 selected positions: K, V
+// bf16 rows [BH, cap, D = 128] in device memory, out [rows, D] fp32, equal to
+// gather_attention's output for those indices.
+int launch_rowselect_gmax_attn(const float *scores, const uint32_t *gmax, int64_t rows, int64_t n, int64_t m, int64_t k,
+                               int64_t sink, int64_t local, int64_t *idx, const float *q, int64_t G, const void *K,
+                               const void *V, int64_t cap, float scale, float *out, hipStream_t st);
 // kk == 0: only the sink and local positions are written.
 int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st);
 // Shape checks shared by the top-k entry points (FATHOM_OK or an error status).

@@ -225,6 +225,27 @@ int fathom_plan_scan_topk(const float *q, const float *g, const float *budget, f
                           int64_t *idx, int8_t *t_out, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * fathom_plan_scan_topk followed by fathom_gather_attention over its indices
+ * (rows in device memory: Ksrc, Vsrc bf16 [BH, cap, 128], no recent rows),
+ * the decode step's plan -> scan -> top-k -> gather + attention chain of
+ * scripts/B_kernel_bench.py:64-101 in one call.  For rows of at most 32768
+ * tokens and k <= 512 each selection workgroup goes on to its query head's
+ * attention over the indices it wrote (the arithmetic of gather_attention), so
+ * idx and out equal the two calls'.  Other shapes run the two calls.  It
+ * composes reference stages and has no single counterpart in the reference.
+ * workspace: fathom_plan_scan_topk_attention_workspace_bytes(BH, G, D, bmax,
+ * n, k, sink, local) bytes.
+ */
+size_t fathom_plan_scan_topk_attention_workspace_bytes(int64_t BH, int64_t G, int64_t D, int bmax, int64_t n, int64_t k,
+                                                       int64_t sink, int64_t local);
+int fathom_plan_scan_topk_attention(const float *q, const float *g, const float *budget, float budget_value, int64_t BH,
+                                    int64_t G, int64_t D, int bmax, int iters, int64_t units_max, const void *planes_sb,
+                                    const void *scales_sb, int64_t n, int64_t nsb, int64_t sub, int64_t m, int64_t k,
+                                    int64_t sink, int64_t local, int64_t *idx, int8_t *t_out, const void *Ksrc,
+                                    const void *Vsrc, int64_t cap, float scale, float *out, void *workspace,
+                                    size_t workspace_bytes, void *stream);
+
+/*
  * fathom_scan_topk without a workspace argument, for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It has no counterpart in the reference.

@@ -642,6 +642,38 @@ def test_plan_scan_topk_equals_plan_then_scan_topk(cfg, n, BH, k, budget):
     assert torch.equal(st.plan_scan_topk(q, g, budget, k, sink, local), ref)
 
 
+@pytest.mark.parametrize("cfg,n,BH,k,budget", [(5, 32768, 32, 512, None), (5, 32768, 24, 512, 92.0),
+                                               (2, 16421, 24, 300, "rows"), (5, 32768, 4, 512, None),
+                                               (1, 16384, None, 128, None), (4, 20000, 2, 2048, 40.0),
+                                               (2, 700, 1, 36, None), (2, 40000, 2, 512, None)])
+def test_plan_scan_topk_attention_equals_separate_calls(cfg, n, BH, k, budget):
+    """Selection + attention in one call: the same workgroups for rows of at
+    most 32768 tokens, k <= 512 and at least 96 query heads (C5's 128, 96 at 92
+    bits and per-row budgets); the two calls otherwise (16 heads, G = 1,
+    k = 2048, kk = 0, long rows).  The indices equal plan_scan_topk's and the
+    outputs equal gather_attention's over them bit for bit, on two calls in a
+    row."""
+    print(f"[plan-scan-topk-attn] cfg={cfg} n={n} BH={BH} k={k} budget={budget}", flush=True)
+    x = W.config_inputs(cfg, seed=2, n=n, BH=BH)
+    K = x["K"].to(DEV)
+    st = bp.PlaneStore(K, keep_code=False)
+    q, g = x["q"].to(DEV), x["g"].to(DEV)
+    bh = q.shape[0]
+    if budget == "rows":
+        budget = torch.linspace(24.0, 90.0, bh, device=DEV)
+    elif budget is None:
+        budget = x["budget"]
+    sink, local = x["sink"], x["local"]
+    Kb = K.to(torch.bfloat16).contiguous()
+    V = W.synth_values(bh, n, seed=5, device=DEV)
+    ref_idx = st.plan_scan_topk(q, g, budget, k, sink, local)
+    ref_out = off.gather_attention(q, ref_idx, n, Kb, V, n)[0]
+    for _ in range(2):
+        idx, out = st.plan_scan_topk_attention(q, g, budget, k, Kb, V, sink, local)
+        assert torch.equal(idx, ref_idx)
+        assert torch.equal(out, ref_out)
+
+
 @pytest.mark.parametrize("umax", [16, 48, 0, None])
 def test_scan_topk_fused_plan_tables(umax):
     """Long rows: the candidate pass starts from the plan tables the sample
