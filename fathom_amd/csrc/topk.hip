@@ -997,28 +997,36 @@ __device__ __forceinline__ void two_bins(const uint32_t *hist, uint32_t na, uint
 template <int PER>
 __device__ __forceinline__ void two_bounds(const uint32_t (&v)[PER], int cnt, uint32_t na, uint32_t nb,
                                            RangeShared &sh, uint32_t *hist2, uint32_t *s_sel, uint32_t &ta,
-                                           uint32_t &tb, uint32_t floor = 0u) {
+                                           uint32_t &tb, uint32_t floor = 0u, bool coarse_ok = false) {
   static_assert(kBins == 2 * kFinThreads, "two bins per thread");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
-  uint32_t mn = ~0u, mx = 0u;
+  uint32_t mn = ~0u, mx = 0u, nv = 0u;
 #pragma unroll
-  for (int u = 0; u < PER; ++u)
-    if (tid + u * kFinThreads < cnt && v[u] >= floor) {
+  for (int u = 0; u < PER; ++u) {
+    const bool on = tid + u * kFinThreads < cnt && v[u] >= floor;
+    if (on) {
       mn = min(mn, v[u]);
       mx = max(mx, v[u]);
     }
+    nv += (uint32_t)__popcll(__ballot(on));
+  }
   wave_minmax_u32(mn, mx);
   if (lane == 0) {
     sh.wmin[wave] = mn;
-    sh.wmax[wave] = mx;
+    sh.wmax[wave] = ((uint64_t)nv << 32) | mx;  // the wave's count beside its maximum
   }
   sh.hist[tid] = sh.hist[tid + kFinThreads] = 0u;
   hist2[tid] = hist2[tid + kFinThreads] = 0u;
   __syncthreads();
-  uint32_t lo = ~0u, hi = 0u;
+  uint32_t lo = ~0u, hi = 0u, nvalid = 0u;
   for (int w = 0; w < nw; ++w) {
     lo = min(lo, (uint32_t)sh.wmin[w]);
     hi = max(hi, (uint32_t)sh.wmax[w]);
+    nvalid += (uint32_t)(sh.wmax[w] >> 32);
+  }
+  if (nvalid < na || nvalid < nb) {  // uniform: fewer values at or above floor than a rank
+    ta = tb = 0u;
+    return;
   }
   const uint32_t R = hi - lo;
   const int bl = R ? 32 - __clz((int)R) : 0;
@@ -1030,7 +1038,14 @@ __device__ __forceinline__ void two_bounds(const uint32_t (&v)[PER], int cnt, ui
   uint32_t sel[2], above[2];
   two_bins(sh.hist, na, nb, sh, sel, above, s_sel);
   const uint32_t base_a = lo + (sel[0] << sft), base_b = lo + (sel[1] << sft);
-  if (sft == 0) {  // one value per bin: the bins' values are the ranks' values
+  bool coarse = false;
+  if (coarse_ok) {  // uniform: both bins hold at most kBoundFine values
+    coarse = sh.hist[sel[0]] <= kBoundFine && sh.hist[sel[1]] <= kBoundFine;
+    __syncthreads();  // every thread has read the counts before the clear below
+  }
+  // one value per bin: the bins' values are the ranks' values; coarse: the
+  // bins' lower edges
+  if (sft == 0 || coarse) {  // uniform
     ta = base_a;
     tb = base_b;
     return;
@@ -1129,7 +1144,10 @@ __global__ __launch_bounds__(kSelThreads) void select_groups_kernel(const uint32
     }
   }
   uint32_t t_lo = 0u, t_hi = 0u;  // fewer values than kk: every element is a candidate
-  if (ng >= (int)kk && kk > 0) two_bounds<PER>(g, ng, kk, r_hi < kk ? r_hi : kk, sh, hist2, s_sel, t_lo, t_hi);
+  // the range leaves out the groups of masked positions (keys at or below
+  // -inf); lower bounds from one round where the ranks' bins are sparse
+  if (ng >= (int)kk && kk > 0)
+    two_bounds<PER>(g, ng, kk, r_hi < kk ? r_hi : kk, sh, hist2, s_sel, t_lo, t_hi, kKeyNegInf + 1u, true);
   if (threadIdx.x == 0) {
     s.thr[row] = r_hi < kk ? t_hi : t_lo;
     s.thr_lo[row] = t_lo;
