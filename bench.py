@@ -66,6 +66,9 @@ def parse():
     ap.add_argument("--stages-only", action="store_true", help="scan + top-k only (for profiling runs)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only config 5's 36-layer decode step (for rocprofv3 kernel traces of its stages)")
+    ap.add_argument("--decode-form", choices=["all", "one"], default="all",
+                    help="decode step forms timed: all three (default), or only the one-call form (for a kernel "
+                         "trace of exactly the reported step)")
     ap.add_argument("--host-scan-only", action="store_true",
                     help="only the fused scan + top-k over the host-mapped store, --steps calls after --warmup "
                          "(for rocprofv3 --pmc runs of the zero-copy scan); raises if its indices differ from "
@@ -218,7 +221,7 @@ def run_copy_index(torch, bp, off, x, K_dev, V_dev, steps, warmup):
             off.free_host(h)
 
 
-def run_decode_step(torch, bp, off, W, dev, steps, warmup):
+def run_decode_step(torch, bp, off, W, dev, steps, warmup, forms="all"):
     """Config 5: one decode step of a 36-layer model with every layer's index and
     K/V rows in HBM -- per layer the plan (the layer's own budget), fused scan +
     top-k and exact attention over the selected rows.  As scripts/B_kernel_bench.py
@@ -316,21 +319,24 @@ def run_decode_step(torch, bp, off, W, dev, steps, warmup):
             sp[i]["out"] = off.gather_attention(ly["q"], sp[i]["idx"], n, ly["K"], ly["V"], n)[0]
 
     ms, eager_ms = timed([("plan_scan_topk_attention", s_decode)], fa)
+    scan_bytes = sum(bp.bytes_planes(bp.make_plan(ly["g"], ly["budget"])["t"], n) for ly in layers)
+    base = {"workload": c["name"], "layers": c["layers"], "BH": BH, "n": n, "k": k,
+            "budgets": [float(b) for b in W.C5_BUDGETS], "timing": "HIP graph per stage over all layers",
+            "ms_per_step": sum(ms.values()), "eager_ms_per_step": eager_ms,
+            "form": "PlaneStore.plan_scan_topk_attention: one call per layer", "scan_bytes_per_step": scan_bytes}
+    if forms == "one":
+        del layers, fa
+        torch.cuda.empty_cache()
+        return base
     ms_fu, eager_fu = timed([("plan_scan_topk", s_plan_scan_topk), ("attn", s_attn_fu)], fu)
     ms_sp, eager_sp = timed([("plan", s_plan), ("scan_topk", s_scan_topk), ("attn", s_attn_sp)], sp)
     for a, b, c2 in zip(fa, fu, sp):
         if not all(torch.equal(a[key], b[key]) and torch.equal(a[key], c2[key]) for key in ("idx", "out")):
             raise RuntimeError("decode step: the one-call, two-call and three-call forms differ")
-    step_ms = sum(ms.values())
-    scan_bytes = sum(bp.bytes_planes(s["plan"]["t"], n) for s in sp)
     del layers, fa, fu, sp
     torch.cuda.empty_cache()
-    return {"workload": c["name"], "layers": c["layers"], "BH": BH, "n": n, "k": k,
-            "budgets": [float(b) for b in W.C5_BUDGETS], "timing": "HIP graph per stage over all layers",
-            "ms_per_step": step_ms, "eager_ms_per_step": eager_ms,
-            "form": "PlaneStore.plan_scan_topk_attention: one call per layer",
+    return {**base,
             "scanned_tokens_per_s": c["layers"] * BH * n / (ms_fu["plan_scan_topk"] * 1e-3),
-            "scan_bytes_per_step": scan_bytes,
             "scan_topk_GBps": scan_bytes / (ms_fu["plan_scan_topk"] * 1e-3) / 1e9,
             "two_calls": {"ms_per_step": sum(ms_fu.values()), "eager_ms_per_step": eager_fu,
                           "stage_ms_per_step": {s: round(v, 4) for s, v in ms_fu.items()}},
@@ -646,7 +652,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if a.decode_only:
-        decode = run_decode_step(torch, bp, off, W, dev, max(3, a.steps // 2), 2)
+        decode = run_decode_step(torch, bp, off, W, dev, max(3, a.steps // 2), 2, a.decode_form)
         log(f"[bench] decode step (config 5): {json.dumps(decode)}")
         return
     t0 = time.perf_counter()
@@ -782,7 +788,7 @@ def main():
     if not a.no_decode and not a.stages_only and a.n is None:
         del store
         torch.cuda.empty_cache()
-        decode = run_decode_step(torch, bp, off, W, dev, max(3, a.steps // 2), 2)
+        decode = run_decode_step(torch, bp, off, W, dev, max(3, a.steps // 2), 2, a.decode_form)
         log(f"[bench] decode step (config 5): {json.dumps(decode)}")
 
     cpu = None
