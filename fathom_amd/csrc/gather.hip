@@ -543,10 +543,19 @@ extern "C" int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, i
   return launch_status("union_fetch_kernel");
 }
 
+// The union path (distinct rows, counts per head) holds a row's G * k
+// positions in one workgroup's LDS and its counts per head in 16-bit fields
+// of 8; rows per selected position have neither limit.
+static bool union_fits(int64_t G, int64_t k) { return G <= kMaxHeads && G * k <= kMaxGK; }
+
 extern "C" size_t fathom_gather_attention_workspace_bytes(int64_t BH, int64_t G, int64_t k) {
   if (BH < 1 || G < 1 || k < 1) return 0;
+  // per-position partials: at most one split per 128 positions of a head
+  const size_t stream = (size_t)BH * cdiv(k, (int64_t)(4 * kStreamTok)) * G * kPartStride * sizeof(float);
+  if (!union_fits(G, k)) return stream;
   const int64_t GK = G * k, nsplit = cdiv(GK, kAttnTok);
-  return union_ws_layout(BH, GK, nullptr, nullptr) + (size_t)BH * nsplit * G * kPartStride * sizeof(float);
+  const size_t uni = (size_t)BH * nsplit * G * kPartStride * sizeof(float);
+  return union_ws_layout(BH, GK, nullptr, nullptr) + (uni > stream ? uni : stream);
 }
 
 extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64_t BH, int64_t G, int64_t k, int64_t n,
@@ -555,9 +564,10 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
                                        void *workspace, size_t workspace_bytes, void *stream) {
   if (!q || !idx || !Ksrc || !Vsrc || !out) return fail(FATHOM_ERR_INVALID, "gather_attention: null pointer");
   if (BH < 1 || BH > 65535) return fail(FATHOM_ERR_INVALID, "gather_attention: BH=%lld outside [1, 65535]", (long long)BH);
-  if (G < 1 || G > kMaxHeads) return fail(FATHOM_ERR_INVALID, "gather_attention: G=%lld outside [1, %d]", (long long)G, kMaxHeads);
-  if (k < 1 || G * k > kMaxGK)
-    return fail(FATHOM_ERR_INVALID, "gather_attention: G*k=%lld outside [1, %d]", (long long)(G * k), kMaxGK);
+  if (G < 1 || G > 65535 || k < 1) return fail(FATHOM_ERR_INVALID, "gather_attention: G=%lld k=%lld", (long long)G, (long long)k);
+  if (n_unique && !union_fits(G, k))
+    return fail(FATHOM_ERR_INVALID, "gather_attention: distinct-row counts need G <= %d and G*k <= %d (G=%lld k=%lld)",
+                kMaxHeads, kMaxGK, (long long)G, (long long)k);
   if (n < 0 || cap < 0 || nrec < 0) return fail(FATHOM_ERR_INVALID, "gather_attention: bad n/cap/nrec");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(Ksrc) | reinterpret_cast<uintptr_t>(Vsrc)) & 7)
     return fail(FATHOM_ERR_INVALID, "gather_attention: q, K and V must be 8-byte aligned");
@@ -566,8 +576,8 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
     return fail(FATHOM_ERR_WORKSPACE, "gather_attention: workspace %zu bytes, need %zu", workspace_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   const int64_t GK = G * k, nsplit = cdiv(GK, kAttnTok);
-  UnionWs w;
-  const size_t off = union_ws_layout(BH, GK, static_cast<char *>(workspace), &w);
+  UnionWs w{};
+  const size_t off = union_fits(G, k) ? union_ws_layout(BH, GK, static_cast<char *>(workspace), &w) : 0;
   float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + off);
   const RowSrc rs{(const char *)Ksrc, (const char *)Vsrc, (const char *)Krec, (const char *)Vrec,
                   cap, nrec, n, (int64_t)kAttnD * 2};

@@ -270,7 +270,9 @@ def gather_attention(q, idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, scale=Non
     union first, so each distinct token is read once, and returns its size;
     unique=False reads the rows per selected position with one launch fewer (for
     rows in device memory) and returns n_unique None; the default is True for
-    mapped host rows (DevPtr) and False for tensors.  scale defaults to D ** -0.5.
+    mapped host rows (DevPtr) and False for tensors.  The union holds at most
+    G <= 8 and G * k <= 16384 positions per row; the per-position path has no
+    such limit (and is the default beyond it).  scale defaults to D ** -0.5.
     Returns (out [BH, G, D] fp32, n_unique [BH] int32 or None)."""
     _need_gpu(q, idx)
     BH, G, k = idx.shape
@@ -284,7 +286,7 @@ def gather_attention(q, idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, scale=Non
     flat = idx.contiguous().to(torch.int64)
     out = torch.empty(BH, G, D, device=dev, dtype=torch.float32)
     if unique is None:
-        unique = isinstance(Ksrc, DevPtr)
+        unique = isinstance(Ksrc, DevPtr) and G <= 8 and G * k <= 16384
     nu = torch.empty(BH, device=dev, dtype=torch.int32) if unique else None
     nbytes = _lib.lib().fathom_gather_attention_workspace_bytes(BH, G, k)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)

@@ -982,6 +982,40 @@ def test_gather_attention_matches_oracle(host, G, k):
             off.free_host(h)
 
 
+@pytest.mark.parametrize("G,k", [(12, 2048), (16, 1100)])
+def test_gather_attention_beyond_the_union_limits(G, k):
+    """Per-position rows (device and mapped host) need neither G <= 8 nor
+    G * k <= 16384 (12 x 2048 = 24576 positions, 16 query heads): the output
+    is within tolerance of the float64 oracle, and asking for the distinct-row
+    counts there is refused."""
+    print(f"[gather_attention-big] G={G} k={k}", flush=True)
+    rng = np.random.default_rng(5 + G)
+    BH, n = 2, 9000
+    K = torch.randn(BH, n, 128).to(torch.bfloat16)
+    V = torch.randn(BH, n, 128).to(torch.bfloat16)
+    q = torch.randn(BH, G, 128)
+    idx = rng.integers(-1, n, size=(BH, G, k))
+    ref, _ = O.gather_attention(q.numpy(), idx, n, K.float().numpy(), V.float().numpy())
+    it = torch.from_numpy(idx).to(DEV)
+    out, nu = off.gather_attention(q.to(DEV), it, n, K.to(DEV), V.to(DEV), n)
+    assert nu is None
+    _attn_close(out.cpu().numpy(), ref)
+    hps = []
+    try:
+        _, Ksrc, h1 = off.host_mapped(K)
+        _, Vsrc, h2 = off.host_mapped(V)
+        hps = [h1, h2]
+        out2, nu2 = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n)  # default: per position here
+        torch.cuda.synchronize()
+        assert nu2 is None
+        _attn_close(out2.cpu().numpy(), ref)
+        with pytest.raises(ValueError):
+            off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, unique=True)
+    finally:
+        for h in hps:
+            off.free_host(h)
+
+
 def test_gather_attn_dropin_equals_torch_formula():
     """gather_attn(q, Kc, Vc, idx) against the reference formula in torch fp32."""
     BH, G, n, k = 4, 4, 9000, 512
