@@ -40,6 +40,11 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
 PCIE_PEAK_GBPS = 64.0         # PCIe 5.0 x16, per direction
 HOST_SUB = 64                 # superblock of the host-resident store (a multiple of 64 blocks)
+# The HBM store of the headline: the whole-sequence superblock layout (one
+# superblock per row, SUB = n / 64 blocks), the layout of the reference's own
+# 1M-token HBM scan benchmark (scripts/bench_scan_cfg.py:10).  Each active
+# channel's scales are then one contiguous run, so the four wave-tiles of a
+# candidate-pass workgroup share each 128-byte scale line.
 SIMDS = 256 * 4               # MI355X: 256 CUs x 4 SIMDs
 CLOCK_HZ = 2.4e9              # MI355X peak engine clock
 VALU_CYCLES = 4               # a wave64 VALU instruction occupies a 16-lane SIMD 4 cycles
@@ -658,7 +663,11 @@ def main():
     t0 = time.perf_counter()
     x = W.config_inputs(a.config, device=dev, n=a.n)
     V = W.synth_values(x["BH"], x["n"], device=dev)
-    store = bp.PlaneStore(x["K"], keep_code=False)
+    bp.SUB = -(-x["n"] // bp.BLK)  # the whole-sequence layout (above)
+    try:
+        store = bp.PlaneStore(x["K"], keep_code=False)
+    finally:
+        bp.SUB = 16
     torch.cuda.synchronize()
     log(f"[bench] inputs + store built in {time.perf_counter() - t0:.1f} s: {W.CONFIGS[a.config]['name']}"
         f" n={x['n']}")
@@ -817,7 +826,8 @@ def main():
         "data": "synthetic (seeded lognormal-scaled keys, planted keys; no model weights)",
         "config": {"workload": W.CONFIGS[a.config]["name"] + ", index + rows in HBM", "BH": BH, "G": x["G"],
                    "n": n, "budget_bits": x["budget"], "k": x["k"], "sink": x["sink"], "local": x["local"],
-                   "bits_per_token": round(hbm["bits_per_token"], 3), "parallelism": "single GPU"},
+                   "bits_per_token": round(hbm["bits_per_token"], 3), "parallelism": "single GPU",
+                   "store_layout": "whole-sequence superblock (SUB = n/64), as the reference's 1M scan benchmark"},
         "stage_ms": {k: round(v, 4) for k, v in st.items()},
         "scan_topk_ms": scan_topk_ms,
         "scan_topk_timing": "20 fused calls captured in one HIP graph, 10 replays after 30 ms of warm-up replays (eager per-stage time: stage_ms)",
