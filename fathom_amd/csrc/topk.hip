@@ -1168,10 +1168,14 @@ __global__ __launch_bounds__(kSelThreads) void select_groups_kernel(const uint32
 // selected first; rows whose candidates outgrow the LDS list (ties around T)
 // are selected from the whole row.
 constexpr int kGmaxGroups = (int)(kRowSelectMax / kGroupTok);
-__device__ __forceinline__ void rowselect_gmax_row(const float *__restrict__ scores, const uint32_t *__restrict__ gmax,
+// ranked (LDS of k int32, past the sort's scratch in cl; null: none): rows of
+// at most 2048 candidates also leave their k output tokens there, and the
+// call returns true.
+__device__ __forceinline__ bool rowselect_gmax_row(const float *__restrict__ scores, const uint32_t *__restrict__ gmax,
                                                    int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
                                                    int64_t *__restrict__ idx, uint64_t *cl, uint64_t *ss,
-                                                   RangeShared &sh, uint16_t *glist, uint32_t &s_cnt) {
+                                                   RangeShared &sh, uint16_t *glist, uint32_t &s_cnt,
+                                                   int32_t *ranked = nullptr) {
   constexpr int kPer = kGmaxGroups / kFinThreads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = kFinThreads >> 6;
   const int64_t row = blockIdx.x;
@@ -1257,11 +1261,11 @@ __device__ __forceinline__ void rowselect_gmax_row(const float *__restrict__ sco
   if (cnt > (uint32_t)kCandLds) {  // uniform: ties around T
     const auto src = index_src([&](int64_t i) { return k64_of(masked_key(rs, i, sink, lstart), i); }, n);
     select_sorted(src, n, kk, m, sink, local, out, cl, ss, sh, s_cnt, true);
-    return;
+    return false;
   }
   if (cnt > (uint32_t)(2 * kFinThreads)) {
     select_sorted(ArraySrc{cl, (int64_t)cnt}, cnt, kk, m, sink, local, out, cl, ss, sh, s_cnt, false);
-    return;
+    return false;
   }
   // at most 2048 candidates: one sort ranks them, the first kk are written
   uint64_t v2[2];
@@ -1272,9 +1276,19 @@ __device__ __forceinline__ void rowselect_gmax_row(const float *__restrict__ sco
   while (nlim < (int)cnt) nlim <<= 1;
   const int got = (int64_t)cnt < kk ? (int)cnt : (int)kk;
   bin_rank_desc<2>(v2, (int)cnt, cl, sh, nlim, [&](int rank, uint64_t x) {
-    if (rank < got) out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x);
+    if (rank < got) {
+      const uint32_t tok = 0xFFFFFFFFu - (uint32_t)x;
+      out[rank] = (int64_t)tok;
+      if (ranked) ranked[rank] = (int32_t)tok;
+    }
   });
   write_fixed(out, got, kk, m, sink, local);
+  if (ranked) {  // the same tokens as write_fixed's
+    for (int i = got + tid; i < (int)kk; i += kFinThreads) ranked[i] = 0;
+    for (int i = tid; i < (int)(sink + local); i += kFinThreads)
+      ranked[kk + i] = (int32_t)((i < sink) ? (int64_t)i : (m - local + (i - sink)));
+  }
+  return ranked != nullptr;
 }
 
 // The selection of rowselect_gmax_row, one workgroup per row.  ATTN (the
@@ -1299,18 +1313,30 @@ __global__ __launch_bounds__(kFinThreads) void rowselect_gmax_kernel(const float
   __shared__ RangeShared sh;
   __shared__ uint16_t glist[kGmaxGroups];
   __shared__ uint32_t s_cnt;
-  rowselect_gmax_row(scores, gmax, n, m, k, sink, local, idx, cl, ss, sh, glist, s_cnt);
+  // ATTN: the ranked tokens also in LDS, in cl's upper half (past the sort's
+  // scratch and the attention's triples)
+  int32_t *ranked = ATTN ? reinterpret_cast<int32_t *>(cl + kCandLds / 2) : nullptr;
+  static_assert(kCandLds / 2 >= 2 * 2 * kFinThreads + kBins && 2 * (kCandLds / 2) >= kMaxK + kFinThreads,
+                "the ranked tokens lie past the sort's scratch and hold k of them");
+  const bool in_lds = rowselect_gmax_row(scores, gmax, n, m, k, sink, local, idx, cl, ss, sh, glist, s_cnt, ranked);
   if constexpr (ATTN) {
     constexpr int NW = kFinThreads / kWave;
     static_assert(NW == 16, "one attention split of 16 waves");
-    static_assert(sizeof(float) * (2 * NW + NW * attn::kAttnD) <= sizeof(cl), "the attention's LDS in cl");
-    __syncthreads();  // the row's indices are written (and cl is free)
+    static_assert(sizeof(float) * (2 * NW + NW * attn::kAttnD) <= sizeof(uint64_t) * (kCandLds / 2),
+                  "the attention's LDS in cl's lower half");
+    __syncthreads();  // the row's indices are written (and cl's lower half is free)
     const int64_t row = blockIdx.x, bh = row / ra.G;
     const int64_t *ig = idx + row * k;
     float *wm = reinterpret_cast<float *>(cl), *wl = wm + NW;
     auto wo = reinterpret_cast<float(*)[attn::kAttnD]>(wl + NW);
-    attn::attn_stream_block<NW, false>(ra.q + row * attn::kAttnD, [&](int64_t j) { return ig[j]; }, k, 0, bh, ra.rs,
-                                       ra.scale, wm, wl, wo, ra.out + row * attn::kAttnD, nullptr, true);
+    const float *qr = ra.q + row * attn::kAttnD;
+    float *orow = ra.out + row * attn::kAttnD;
+    if (in_lds)  // uniform: the tokens from LDS, else from the index list just written
+      attn::attn_stream_block<NW, false>(qr, [&](int64_t j) { return (int64_t)ranked[j]; }, k, 0, bh, ra.rs, ra.scale,
+                                         wm, wl, wo, orow, nullptr, true);
+    else
+      attn::attn_stream_block<NW, false>(qr, [&](int64_t j) { return ig[j]; }, k, 0, bh, ra.rs, ra.scale, wm, wl, wo,
+                                         orow, nullptr, true);
   }
 }
 
