@@ -16,6 +16,9 @@
 //           recent-token device buffer, or a zero row for negative tokens) and
 //           writes it to every position of its chain, so each distinct host
 //           row crosses PCIe exactly once;
+//   wide    rows of more than 16384 positions (and distinct-row counts over
+//           more than 8 query heads) keep the table in global memory instead:
+//           the same rows and counts, no shape limit;
 //   attend  (gather_attention) the K and V rows are read 16 lanes per 256-byte
 //           row, so every load instruction reads whole rows, and form the
 //           softmax numerators of the query heads, weighted by the times a
@@ -208,6 +211,131 @@ __global__ __launch_bounds__(256) void union_fetch_kernel(UnionWs w, int64_t GK,
       q = nxt[q];
     }
   }
+}
+
+// ------------------------------------------------------------------ wide union
+// Rows of more than kMaxGK positions, or distinct-row counts over more than
+// kMaxHeads query heads: the same semantics from a hash table in global memory
+// (2^hbits >= 2 GK slots per row, so a probe always ends at its token's slot).
+// The lowest position holding a token (an atomic minimum per slot) fetches its
+// row once; the token's other positions copy it from there afterwards.
+struct WideUnionWs {
+  uint32_t *key;   // [BH, S] token key + 1 (0: empty)
+  int32_t *first;  // [BH, S] lowest position holding the slot's token
+  int32_t *slot;   // [BH, GK] slot of each position's token
+  int64_t S;
+  int hbits;
+};
+
+size_t wide_union_layout(int64_t BH, int64_t GK, char *base, WideUnionWs *w) {
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  int hb = 6;
+  while ((int64_t(1) << hb) < 2 * GK) ++hb;
+  const int64_t S = int64_t(1) << hb;
+  const size_t o_first = al((size_t)BH * S * 4), o_slot = o_first + al((size_t)BH * S * 4),
+               end = o_slot + al((size_t)BH * GK * 4);
+  if (w) {
+    w->key = reinterpret_cast<uint32_t *>(base);
+    w->first = reinterpret_cast<int32_t *>(base + o_first);
+    w->slot = reinterpret_cast<int32_t *>(base + o_slot);
+    w->S = S;
+    w->hbits = hb;
+  }
+  return end;
+}
+
+__global__ __launch_bounds__(256) void wide_union_clear_kernel(WideUnionWs w, int64_t BH, int32_t *__restrict__ n_unique) {
+  const int64_t total = BH * w.S;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    w.key[i] = 0u;
+    w.first[i] = 0x7FFFFFFF;
+    if (n_unique && i < BH) n_unique[i] = 0;
+  }
+}
+
+__global__ __launch_bounds__(256) void wide_union_insert_kernel(const int64_t *__restrict__ idx, int64_t GK,
+                                                                WideUnionWs w) {
+  const int64_t bh = blockIdx.y;
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= GK) return;
+  const uint32_t t = tok_key(idx[bh * GK + p]);
+  const uint32_t key = t + 1u;  // t <= kTokNeg, so key != 0
+  uint32_t *hk = w.key + bh * w.S;
+  const uint32_t smask = (uint32_t)(w.S - 1);
+  uint32_t s = (uint32_t)(((uint64_t)(t * 2654435761u) << w.hbits) >> 32) & smask;
+  for (int64_t it = 0; it < w.S; ++it) {  // ends at the token's slot: the table is at most half full
+    const uint32_t old = atomicCAS(&hk[s], 0u, key);
+    if (old == 0u || old == key) break;
+    s = (s + 1u) & smask;
+  }
+  atomicMin(&w.first[bh * w.S + s], (int32_t)p);
+  w.slot[bh * GK + p] = (int32_t)s;
+}
+
+// n_unique[bh] += distinct tokens < n (a thread per position, one atomic per workgroup).
+__global__ __launch_bounds__(256) void wide_union_count_kernel(const int64_t *__restrict__ idx, int64_t GK, int64_t n,
+                                                               WideUnionWs w, int32_t *__restrict__ n_unique) {
+  __shared__ int32_t part[256 / kWave];
+  const int64_t bh = blockIdx.y;
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  int c = 0;
+  if (p < GK) {
+    const uint32_t t = tok_key(idx[bh * GK + p]);
+    c = (t != kTokNeg && (int64_t)t < n && w.first[bh * w.S + w.slot[bh * GK + p]] == (int32_t)p) ? 1 : 0;
+  }
+  c = wave_sum_i(c);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int tot = part[0] + part[1] + part[2] + part[3];
+    if (tot) atomicAdd(&n_unique[bh], tot);
+  }
+}
+
+// A wave per position: first positions read their token's row (as
+// union_fetch_kernel), the others copy it from the first position's output
+// row (DUP, launched after the fetch).
+template <bool DUP>
+__global__ __launch_bounds__(256) void wide_union_fetch_kernel(const int64_t *__restrict__ idx, int64_t GK,
+                                                               WideUnionWs w, RowSrc rs, char *__restrict__ Kout,
+                                                               char *__restrict__ Vout) {
+  const int lane = threadIdx.x & 63;
+  const int64_t bh = blockIdx.y;
+  const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (p >= GK) return;
+  const int32_t fp = w.first[bh * w.S + w.slot[bh * GK + p]];
+  if ((fp != (int32_t)p) != DUP) return;
+  const char *ks, *vs;
+  if (DUP) {
+    ks = Kout + (bh * GK + fp) * rs.row_bytes;
+    vs = Vout + (bh * GK + fp) * rs.row_bytes;
+  } else {
+    bool rec;
+    const int64_t row = rs.locate(tok_key(idx[bh * GK + p]), bh, rec);
+    ks = row < 0 ? nullptr : (rec ? rs.Krec : rs.K) + row * rs.row_bytes;
+    vs = row < 0 ? nullptr : (rec ? rs.Vrec : rs.V) + row * rs.row_bytes;
+  }
+  char *kd = Kout + (bh * GK + p) * rs.row_bytes;
+  char *vd = Vout + (bh * GK + p) * rs.row_bytes;
+  for (int64_t o = (int64_t)lane * 4; o < rs.row_bytes; o += kWave * 4) {
+    *reinterpret_cast<uint32_t *>(kd + o) = ks ? *reinterpret_cast<const uint32_t *>(ks + o) : 0u;
+    *reinterpret_cast<uint32_t *>(vd + o) = vs ? *reinterpret_cast<const uint32_t *>(vs + o) : 0u;
+  }
+}
+
+// The table of every row, and n_unique when given.
+int launch_wide_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t n, const WideUnionWs &w, int32_t *n_unique,
+                      hipStream_t st) {
+  const int64_t cells = BH * w.S;
+  wide_union_clear_kernel<<<(unsigned)min(cdiv(cells, 256), (int64_t)16384), 256, 0, st>>>(w, BH, n_unique);
+  int rc = launch_status("wide_union_clear_kernel");
+  if (rc) return rc;
+  const dim3 grid((unsigned)cdiv(GK, 256), (unsigned)BH);
+  wide_union_insert_kernel<<<grid, 256, 0, st>>>(idx, GK, w);
+  rc = launch_status("wide_union_insert_kernel");
+  if (rc || !n_unique) return rc;
+  wide_union_count_kernel<<<grid, 256, 0, st>>>(idx, GK, n, w, n_unique);
+  return launch_status("wide_union_count_kernel");
 }
 
 // ------------------------------------------------------------------ attention
@@ -516,7 +644,7 @@ extern "C" int fathom_gather_rows(const void *src, int64_t cap, const int32_t *i
 
 extern "C" size_t fathom_gather_union_workspace_bytes(int64_t BH, int64_t GK) {
   if (BH < 1 || GK < 1) return 0;
-  return union_ws_layout(BH, GK, nullptr, nullptr);
+  return GK <= kMaxGK ? union_ws_layout(BH, GK, nullptr, nullptr) : wide_union_layout(BH, GK, nullptr, nullptr);
 }
 
 extern "C" int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t n, const void *Ksrc,
@@ -525,19 +653,31 @@ extern "C" int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, i
                                    size_t workspace_bytes, void *stream) {
   if (!idx || !Ksrc || !Vsrc || !Kout || !Vout) return fail(FATHOM_ERR_INVALID, "gather_union: null pointer");
   if (BH < 1 || BH > 65535) return fail(FATHOM_ERR_INVALID, "gather_union: BH=%lld outside [1, 65535]", (long long)BH);
-  if (GK < 1 || GK > kMaxGK) return fail(FATHOM_ERR_INVALID, "gather_union: G*k=%lld outside [1, %d]", (long long)GK, kMaxGK);
+  if (GK < 1 || GK > 0x7FFFFFFF) return fail(FATHOM_ERR_INVALID, "gather_union: G*k=%lld unsupported", (long long)GK);
   if (n < 0 || cap < 0) return fail(FATHOM_ERR_INVALID, "gather_union: bad n/cap");
   if (row_bytes < 4 || row_bytes % 4) return fail(FATHOM_ERR_INVALID, "gather_union: row_bytes=%lld not a multiple of 4", (long long)row_bytes);
   const size_t need = fathom_gather_union_workspace_bytes(BH, GK);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "gather_union: workspace %zu bytes, need %zu", workspace_bytes, need);
   hipStream_t st = (hipStream_t)stream;
+  const RowSrc rs{(const char *)Ksrc, (const char *)Vsrc, (const char *)Krec, (const char *)Vrec,
+                  cap, nrec, n, row_bytes};
+  if (GK > kMaxGK) {  // beyond one workgroup's LDS: the table in the workspace
+    WideUnionWs ww;
+    wide_union_layout(BH, GK, static_cast<char *>(workspace), &ww);
+    int rc = launch_wide_union(idx, BH, GK, n, ww, n_unique, st);
+    if (rc) return rc;
+    const dim3 grid((unsigned)cdiv(GK, 4), (unsigned)BH);
+    wide_union_fetch_kernel<false><<<grid, 256, 0, st>>>(idx, GK, ww, rs, (char *)Kout, (char *)Vout);
+    rc = launch_status("wide_union_fetch_kernel");
+    if (rc) return rc;
+    wide_union_fetch_kernel<true><<<grid, 256, 0, st>>>(idx, GK, ww, rs, (char *)Kout, (char *)Vout);
+    return launch_status("wide_union_fetch_kernel");
+  }
   UnionWs w;
   union_ws_layout(BH, GK, static_cast<char *>(workspace), &w);
   int rc = launch_union(idx, BH, GK, GK, n, w, n_unique, st);
   if (rc) return rc;
-  const RowSrc rs{(const char *)Ksrc, (const char *)Vsrc, (const char *)Krec, (const char *)Vrec,
-                  cap, nrec, n, row_bytes};
   dim3 grid((unsigned)cdiv(GK, 4), (unsigned)BH);
   union_fetch_kernel<<<grid, 256, 0, st>>>(w, GK, rs, (char *)Kout, (char *)Vout);
   return launch_status("union_fetch_kernel");
@@ -552,7 +692,7 @@ extern "C" size_t fathom_gather_attention_workspace_bytes(int64_t BH, int64_t G,
   if (BH < 1 || G < 1 || k < 1) return 0;
   // per-position partials: at most one split per 128 positions of a head
   const size_t stream = (size_t)BH * cdiv(k, (int64_t)(4 * kStreamTok)) * G * kPartStride * sizeof(float);
-  if (!union_fits(G, k)) return stream;
+  if (!union_fits(G, k)) return wide_union_layout(BH, G * k, nullptr, nullptr) + stream;
   const int64_t GK = G * k, nsplit = cdiv(GK, kAttnTok);
   const size_t uni = (size_t)BH * nsplit * G * kPartStride * sizeof(float);
   return union_ws_layout(BH, GK, nullptr, nullptr) + (uni > stream ? uni : stream);
@@ -565,9 +705,7 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
   if (!q || !idx || !Ksrc || !Vsrc || !out) return fail(FATHOM_ERR_INVALID, "gather_attention: null pointer");
   if (BH < 1 || BH > 65535) return fail(FATHOM_ERR_INVALID, "gather_attention: BH=%lld outside [1, 65535]", (long long)BH);
   if (G < 1 || G > 65535 || k < 1) return fail(FATHOM_ERR_INVALID, "gather_attention: G=%lld k=%lld", (long long)G, (long long)k);
-  if (n_unique && !union_fits(G, k))
-    return fail(FATHOM_ERR_INVALID, "gather_attention: distinct-row counts need G <= %d and G*k <= %d (G=%lld k=%lld)",
-                kMaxHeads, kMaxGK, (long long)G, (long long)k);
+  if (G * k > 0x7FFFFFFF) return fail(FATHOM_ERR_INVALID, "gather_attention: G*k=%lld unsupported", (long long)(G * k));
   if (n < 0 || cap < 0 || nrec < 0) return fail(FATHOM_ERR_INVALID, "gather_attention: bad n/cap/nrec");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(Ksrc) | reinterpret_cast<uintptr_t>(Vsrc)) & 7)
     return fail(FATHOM_ERR_INVALID, "gather_attention: q, K and V must be 8-byte aligned");
@@ -577,12 +715,19 @@ extern "C" int fathom_gather_attention(const float *q, const int64_t *idx, int64
   hipStream_t st = (hipStream_t)stream;
   const int64_t GK = G * k, nsplit = cdiv(GK, kAttnTok);
   UnionWs w{};
-  const size_t off = union_fits(G, k) ? union_ws_layout(BH, GK, static_cast<char *>(workspace), &w) : 0;
+  WideUnionWs ww{};
+  const bool fits = union_fits(G, k);
+  const size_t off = fits ? union_ws_layout(BH, GK, static_cast<char *>(workspace), &w)
+                          : wide_union_layout(BH, GK, static_cast<char *>(workspace), &ww);
   float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + off);
   const RowSrc rs{(const char *)Ksrc, (const char *)Vsrc, (const char *)Krec, (const char *)Vrec,
                   cap, nrec, n, (int64_t)kAttnD * 2};
   int rc;
-  if (!n_unique) {
+  if (n_unique && !fits) {  // the distinct-row count from the table in the workspace; rows per position below
+    rc = launch_wide_union(idx, BH, GK, n, ww, n_unique, st);
+    if (rc) return rc;
+  }
+  if (!n_unique || !fits) {
     // rows per selected position, streamed (attn_wide: 16 or 4 waves per
     // workgroup), split heads merged by attn_merge_kernel
     const bool wide = attn_wide(BH, G, k);

@@ -72,7 +72,7 @@ extern "C" int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, i
   if (k - sink - local == 0)
     return scan_topk_run(q, BH, G, D, cls, clsn, bmax, units_max, planes_sb, scales_sb, n, nsb, sub, m, k, sink,
                          local, idx, nullptr, 0, FATHOM_STAGE_ALL, stream);
-  const size_t need = scan_topk_ws(BH * G, n, k);
+  const size_t need = scan_topk_ws(BH * G, n, k, k - sink - local);
   if (need > kScratchBytes)
     return fail(FATHOM_ERR_WORKSPACE,
                 "scan_topk_noalloc: BH=%lld G=%lld n=%lld k=%lld needs %zu bytes of scratch, the static array holds "

@@ -204,8 +204,10 @@ namespace fathom {
 // Workspace of the fused scan + top-k: rows up to kRowSelectMax keep their
 // scores ([rows, n] fp32) for one row-select launch; longer rows the sampled
 // keys, the candidate regions and the plan tables (one per row: at least one
-// per (batch, KV head)).
-size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k) {
+// per (batch, KV head)).  kk above kSelMaxK: the scores and the wide path's
+// selection state.
+size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k, int64_t kk) {
+  if (kk > kSelMaxK) return ws_align((size_t)rows * (size_t)n * 4) + wide_select_bytes(rows, kk);
   if (n <= kRowSelectMax) return ws_align((size_t)rows * (size_t)n * 4) + ws_align((size_t)rows * cdiv(n, kGroupTok) * 4);
   return topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr) +
          ws_align((size_t)rows * sizeof(sc::PlanTab));
@@ -216,7 +218,7 @@ extern "C" size_t fathom_scan_topk_workspace_bytes(int64_t BH, int64_t G, int64_
                                                    int64_t local) {
   const int64_t kk = k - sink - local;
   if (BH < 1 || G < 1 || n < 1 || kk < 0) return 0;
-  return scan_topk_ws(BH * G, n, k);
+  return scan_topk_ws(BH * G, n, k, kk);
 }
 
 namespace fathom {
@@ -234,7 +236,7 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
   if (kk == 0) return (stages & FATHOM_STAGE_FINALIZE) ? launch_fixed_only(rows, m, k, sink, local, idx, st) : FATHOM_OK;
-  const size_t need = scan_topk_ws(rows, n, k);
+  const size_t need = scan_topk_ws(rows, n, k, kk);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "scan_topk: workspace %zu bytes, need %zu", workspace_bytes, need);
   const int64_t nblk = cdiv(n, kBlk);
@@ -244,6 +246,21 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   a.wt0 = 0;
   const int64_t nwt = cdiv(nblk, kWB);
   const int64_t um = units_bound(units_max, D, bmax);
+  if (kk > kSelMaxK) {
+    // kk beyond the LDS-resident selections: the scores in the workspace (the
+    // candidate stage), then the wide path's selection (the finalize stage)
+    Emit es{};
+    es.out = static_cast<float *>(workspace);
+    const size_t sb = ws_align((size_t)rows * (size_t)n * 4);
+    if (stages & FATHOM_STAGE_CANDIDATES) {
+      rc = launch_scan<kEmitScores>(a, nwt, BH, es, um, st);
+      if (rc) return rc;
+    }
+    return (stages & FATHOM_STAGE_FINALIZE)
+               ? wide_select_run(es.out, rows, n, m, k, sink, local, idx, static_cast<char *>(workspace) + sb,
+                                 workspace_bytes - sb, st)
+               : FATHOM_OK;
+  }
   if (n <= kRowSelectMax) {
     // short rows: the scores and their 16-token group maxima in the workspace
     // (the candidate stage), then the rows selected in one launch from the
@@ -322,7 +339,7 @@ extern "C" size_t fathom_plan_scan_topk_workspace_bytes(int64_t BH, int64_t G, i
                                                         int64_t sink, int64_t local) {
   const int64_t kk = k - sink - local;
   if (BH < 1 || G < 1 || D < 1 || bmax < 1 || n < 1 || kk < 0) return 0;
-  return scan_topk_ws(BH * G, n, k) + plan_arrays_ws(BH, D, bmax);
+  return scan_topk_ws(BH * G, n, k, kk) + plan_arrays_ws(BH, D, bmax);
 }
 
 namespace fathom {
@@ -353,8 +370,8 @@ int plan_scan_topk_run(const float *q, const float *g, const float *budget, floa
     return fail(FATHOM_ERR_WORKSPACE, "plan_scan_topk: workspace %zu bytes, need %zu", workspace_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
-  const size_t sws = scan_topk_ws(rows, n, k);
-  if (n > kRowSelectMax || kk == 0) {
+  const size_t sws = scan_topk_ws(rows, n, k, kk);
+  if (n > kRowSelectMax || kk == 0 || kk > kSelMaxK) {
     // make_plan into the workspace, then the fused scan + top-k
     char *p = static_cast<char *>(workspace) + sws;
     int8_t *t = t_out ? t_out : reinterpret_cast<int8_t *>(p);

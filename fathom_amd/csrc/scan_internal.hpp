@@ -4,8 +4,9 @@
 
 namespace fathom {
 
-// Workspace bytes of the fused scan + top-k over rows = BH * G score rows of n tokens.
-size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k);
+// Workspace bytes of the fused scan + top-k over rows = BH * G score rows of n
+// tokens, kk = k - sink - local.
+size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k, int64_t kk);
 
 // The fused scan + top-k (stages: FATHOM_STAGE_* mask) on a caller-provided workspace.
 int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_t *cls, const int32_t *clsn, int bmax,

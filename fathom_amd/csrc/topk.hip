@@ -28,7 +28,7 @@ constexpr int kFilterThreads = 256;
 constexpr int64_t kFilterChunk = 16384;
 constexpr uint32_t kFilterLocal = 2048;  // LDS candidates per filter workgroup
 constexpr int kCandLds = 16384;          // candidates selected in LDS (128 KB)
-constexpr int kMaxK = 2048;              // largest kk
+constexpr int kMaxK = (int)kSelMaxK;      // largest kk of these selections
 constexpr int kBins = 2048;
 constexpr int kMaxWaves = 16;            // waves of a 1024-thread workgroup
 
@@ -1492,7 +1492,6 @@ int check_topk_args(int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink,
   const int64_t kk = k - sink - local;
   if (kk < 0) return fail(FATHOM_ERR_INVALID, "%s: k=%lld < sink+local=%lld", who, (long long)k, (long long)(sink + local));
   if (kk > n) return fail(FATHOM_ERR_INVALID, "%s: k - sink - local = %lld exceeds n=%lld", who, (long long)kk, (long long)n);
-  if (kk > kMaxK) return fail(FATHOM_ERR_INVALID, "%s: k - sink - local = %lld exceeds %d", who, (long long)kk, kMaxK);
   if (sink > n || m < n || local > m)
     return fail(FATHOM_ERR_INVALID, "%s: need sink <= n <= m and local <= m (sink=%lld n=%lld m=%lld local=%lld)", who,
                 (long long)sink, (long long)n, (long long)m, (long long)local);
@@ -1503,9 +1502,22 @@ int check_topk_args(int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink,
 
 using namespace fathom;
 
+namespace fathom {
+namespace {
+// k bounds kk = k - sink - local from above: the chain's layout where kk may
+// exceed kSelMaxK covers the wide path's too.
+size_t topk_ws(int64_t rows, int64_t n, int64_t k) {
+  const size_t chain = topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
+  if (k <= kSelMaxK) return chain;
+  const size_t wide = wide_select_bytes(rows, k < n ? k : n);
+  return chain > wide ? chain : wide;
+}
+}  // namespace
+}  // namespace fathom
+
 extern "C" size_t fathom_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
   if (rows < 1 || n < 1 || k < 0) return 0;
-  return topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
+  return topk_ws(rows, n, k);
 }
 
 extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k,
@@ -1517,6 +1529,7 @@ extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
   if (kk == 0) return launch_fixed_only(rows, m, k, sink, local, idx, st);
+  if (kk > kSelMaxK) return wide_select_run(scores, rows, n, m, k, sink, local, idx, workspace, workspace_bytes, st);
   const size_t need = topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "sink_local_topk: workspace %zu bytes, need %zu", workspace_bytes, need);

@@ -154,6 +154,15 @@ int launch_rowselect_gmax_attn(const float *scores, const uint32_t *gmax, int64_
                                const void *V, int64_t cap, float scale, float *out, hipStream_t st);
 // kk == 0: only the sink and local positions are written.
 int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st);
+// Largest kk of the LDS-resident selections (sample -> select -> filter ->
+// finalize, row-select, the fused scan's chains); larger kk take the wide path.
+constexpr int64_t kSelMaxK = 2048;
+// Workspace and run of the wide path: exact top kk of score rows [rows, n] for
+// any kk <= n by a 64-bit radix select and a bitonic sort (any number of
+// launches, all of data-independent shape).
+size_t wide_select_bytes(int64_t rows, int64_t kk);
+int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+                    int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st);
 // Shape checks shared by the top-k entry points (FATHOM_OK or an error status).
 int check_topk_args(int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local, const char *who);
 

@@ -270,9 +270,10 @@ def gather_attention(q, idx, n, Ksrc, Vsrc, cap, Krec=None, Vrec=None, scale=Non
     union first, so each distinct token is read once, and returns its size;
     unique=False reads the rows per selected position with one launch fewer (for
     rows in device memory) and returns n_unique None; the default is True for
-    mapped host rows (DevPtr) and False for tensors.  The union holds at most
-    G <= 8 and G * k <= 16384 positions per row; the per-position path has no
-    such limit (and is the default beyond it).  scale defaults to D ** -0.5.
+    mapped host rows (DevPtr) and False for tensors, and False beyond G <= 8
+    and G * k <= 16384 positions per row (there unique=True only adds the
+    counts, from a hash table in global memory; the rows are read per
+    position either way).  scale defaults to D ** -0.5.
     Returns (out [BH, G, D] fp32, n_unique [BH] int32 or None)."""
     _need_gpu(q, idx)
     BH, G, k = idx.shape

@@ -272,7 +272,9 @@ int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, int64_t D, c
  * scores [rows, n] float32: mask [0, sink) and [max(m - local, 0), n) to -inf,
  * select the top kk = k - sink - local by (score descending, index ascending;
  * NaN above +inf, -0.0 == +0.0), then append 0..sink-1 and m-local..m-1.
- *   idx [rows, k] int64.  Requires 0 <= kk <= n, sink <= n, local <= m, n <= m.
+ *   idx [rows, k] int64.  Requires 0 <= kk <= n, sink <= n, local <= m, n <= m
+ * (any kk, as torch.topk: kk above 2048 takes an exact 64-bit radix select and
+ * a bitonic sort over the score rows).
  * workspace: fathom_topk_workspace_bytes(rows, n, k) bytes of device memory,
  * contents arbitrary on entry.
  */
@@ -291,7 +293,8 @@ int fathom_gather_rows(const void *src, int64_t cap, const int32_t *idx, int64_t
 
 /*
  * Group-union row gather (scripts/B_e2e_offload_v2.py:228-241): for idx
- * [BH, GK] int64 (GK = G*k <= 16384), fetch every distinct token < n of a row
+ * [BH, GK] int64 (GK = G*k, any size: up to 16384 the dedup runs in one
+ * workgroup's LDS, above in a hash table in the workspace), fetch every distinct token < n of a row
  * once from Ksrc/Vsrc [BH, cap, row_bytes] (usually mapped host memory), tokens
  * >= n from the device buffers Krec/Vrec [BH, nrec, row_bytes] at row
  * clamp(idx - n, 0, nrec - 1), negative tokens as zero rows, and write
@@ -318,7 +321,9 @@ int fathom_gather_union(const int64_t *idx, int64_t BH, int64_t GK, int64_t n, c
  * fathom_gather_union; with n_unique NULL the rows are read per selected
  * position, with no union pass (rows in device memory: one launch fewer).
  * Both give the same attention up to fp32 summation order.  q [BH, G, 128]
- * fp32, idx [BH, G, k] int64, out [BH, G, 128] fp32; G <= 8, G*k <= 16384.
+ * fp32, idx [BH, G, k] int64, out [BH, G, 128] fp32.  With G > 8 or G*k >
+ * 16384 the rows are read per selected position also when n_unique is set,
+ * and n_unique comes from a hash table in the workspace.
  * workspace: fathom_gather_attention_workspace_bytes(BH, G, k) bytes.
  */
 size_t fathom_gather_attention_workspace_bytes(int64_t BH, int64_t G, int64_t k);

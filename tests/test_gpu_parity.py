@@ -300,8 +300,7 @@ def test_topk_edge_k_and_errors():
     _topk_case(rows[..., :40], 50, 4, 32)       # kk = 14, four unmasked tokens
     t = torch.from_numpy(rows).to(DEV)
     for n, k, sink, local in ((1000, 30, 4, 32),     # k < sink + local
-                              (1000, 1037, 4, 32),   # kk > n
-                              (5000, 2049, 0, 0)):   # kk above the largest supported
+                              (1000, 1037, 4, 32)):  # kk > n
         with pytest.raises(ValueError):
             bp.sink_local_topk(t[..., :n].contiguous(), k, sink, local)
     x, st, plan = _scan_case(2, 2000, 2)
@@ -339,6 +338,57 @@ def test_topk_final_ranking_spread_and_crowded(n, k):
     rows[1, n // 3] = 1e30
     rows[2, n // 2] = np.inf
     _topk_case(rows, k, 4, 32)
+
+
+@pytest.mark.parametrize("n,k,sink,local,m", [(5000, 2049, 0, 0, None), (5000, 5000, 0, 0, None),
+                                                (40000, 20036, 4, 32, None), (70000, 40000, 4, 32, 70010),
+                                                (300000, 4100, 4, 32, None), (16385, 16385, 0, 0, None)])
+def test_topk_wide_bitexact(n, k, sink, local, m):
+    """kk above the LDS-resident selections' 2048 (torch.topk has no limit):
+    the 64-bit radix select + bitonic sort.  One LDS sort chunk (P = 4096), the
+    whole row, P = 32768 and 65536 (global merge steps between LDS merges), the
+    local window partly past the row (m > n), a long row, P = 32768 with
+    kk = P / 2 + 1."""
+    print(f"[topk-wide] n={n} k={k} m={m}", flush=True)
+    rng = np.random.default_rng(n + k)
+    rows = rng.standard_normal((2, 2, n)).astype(np.float32)
+    _topk_case(rows, k, sink, local, m=m)
+
+
+def test_topk_wide_ties_nan_inf():
+    """Wide kk over rows of seven distinct values (the index rounds break the
+    ties), NaN, +-inf, -0.0, and more selected than unmasked tokens (the masked
+    -inf keys fill the rest by index)."""
+    rng = np.random.default_rng(11)
+    n = 12000
+    rows = rng.integers(-3, 4, size=(4, n)).astype(np.float32)
+    rows[0, rng.integers(0, n, 20)] = np.nan
+    rows[1, rng.integers(0, n, 20)] = -np.inf
+    rows[1, rng.integers(0, n, 20)] = np.inf
+    rows[2, rng.integers(0, n, 300)] = -0.0
+    rows[3] = 0.0
+    _topk_case(rows, 6000, 4, 32)
+    _topk_case(rows, 2100, 3, 5, m=n + 2)
+    _topk_case(rows, 12004, 0, 5, m=n + 2)  # kk = 11999 of 11997 unmasked
+
+
+@pytest.mark.parametrize("cfg,n,BH,k", [(2, 9000, 2, 4000), (2, 40000, 2, 3000), (5, 32768, 2, 6000)])
+def test_scan_topk_wide_equals_scan_then_topk(cfg, n, BH, k):
+    """The fused entries with kk above 2048: scan_topk and plan_scan_topk (short
+    and long rows) equal sink_local_topk of the scan's scores, which equals the
+    oracle's top-k of those scores."""
+    print(f"[scan-topk-wide] cfg={cfg} n={n} k={k}", flush=True)
+    x = W.config_inputs(cfg, seed=2, n=n, BH=BH)
+    st = bp.PlaneStore(x["K"].to(DEV), keep_code=False)
+    q, g = x["q"].to(DEV), x["g"].to(DEV)
+    sink, local = x["sink"], x["local"]
+    plan = bp.make_plan(g, x["budget"])
+    sc = st.scan(q, plan)
+    ref = bp.sink_local_topk(sc, k, sink, local)
+    np.testing.assert_array_equal(ref.cpu().numpy(), O.sink_local_topk(sc.cpu().numpy(), k, sink, local))
+    for _ in range(2):
+        assert torch.equal(st.scan_topk(q, plan, k, sink, local), ref)
+        assert torch.equal(st.plan_scan_topk(q, g, x["budget"], k, sink, local), ref)
 
 
 def test_topk_huge_tie_bucket_slow_path():
@@ -389,10 +439,13 @@ def test_gather_rows_matches_oracle():
     np.testing.assert_array_equal(got.cpu().view(torch.int16).numpy(), ref)
 
 
-@pytest.mark.parametrize("host", [False, True])
-def test_gather_union_matches_oracle(host):
-    rng = np.random.default_rng(5)
-    BH, n, G, k, nrec = 4, 20000, 7, 2048, 6
+@pytest.mark.parametrize("host,G,k", [(False, 7, 2048), (True, 7, 2048), (False, 12, 2048), (True, 16, 1100)])
+def test_gather_union_matches_oracle(host, G, k):
+    """Rows, order and distinct-row counts of the group union; G * k above
+    16384 positions (12 x 2048, 16 x 1100) takes the table in global memory."""
+    print(f"[gather_union] host={host} G={G} k={k}", flush=True)
+    rng = np.random.default_rng(5 + G)
+    BH, n, nrec = 4, 20000, 6
     K = torch.randn(BH, n, 128).to(torch.bfloat16)
     V = torch.randn(BH, n, 128).to(torch.bfloat16)
     Kr = torch.randn(BH, nrec, 128).to(torch.bfloat16)
@@ -986,8 +1039,8 @@ def test_gather_attention_matches_oracle(host, G, k):
 def test_gather_attention_beyond_the_union_limits(G, k):
     """Per-position rows (device and mapped host) need neither G <= 8 nor
     G * k <= 16384 (12 x 2048 = 24576 positions, 16 query heads): the output
-    is within tolerance of the float64 oracle, and asking for the distinct-row
-    counts there is refused."""
+    is within tolerance of the float64 oracle, and the distinct-row counts
+    (from the table in global memory there) equal the oracle's."""
     print(f"[gather_attention-big] G={G} k={k}", flush=True)
     rng = np.random.default_rng(5 + G)
     BH, n = 2, 9000
@@ -995,7 +1048,7 @@ def test_gather_attention_beyond_the_union_limits(G, k):
     V = torch.randn(BH, n, 128).to(torch.bfloat16)
     q = torch.randn(BH, G, 128)
     idx = rng.integers(-1, n, size=(BH, G, k))
-    ref, _ = O.gather_attention(q.numpy(), idx, n, K.float().numpy(), V.float().numpy())
+    ref, rnu = O.gather_attention(q.numpy(), idx, n, K.float().numpy(), V.float().numpy())
     it = torch.from_numpy(idx).to(DEV)
     out, nu = off.gather_attention(q.to(DEV), it, n, K.to(DEV), V.to(DEV), n)
     assert nu is None
@@ -1009,8 +1062,11 @@ def test_gather_attention_beyond_the_union_limits(G, k):
         torch.cuda.synchronize()
         assert nu2 is None
         _attn_close(out2.cpu().numpy(), ref)
-        with pytest.raises(ValueError):
-            off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, unique=True)
+        for _ in range(2):
+            out3, nu3 = off.gather_attention(q.to(DEV), it, n, Ksrc, Vsrc, n, unique=True)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(nu3.cpu().numpy(), rnu)
+            assert torch.equal(out3, out2)
     finally:
         for h in hps:
             off.free_host(h)
