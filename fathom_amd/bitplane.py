@@ -249,6 +249,16 @@ def _plan_classes(plan, BH, d):
     return cls.to(torch.int32).contiguous(), clsn.to(torch.int32).contiguous()
 
 
+# Query heads per scan launch: a matrix row tile of the scan kernels holds 8
+# heads x {hi, lo} weights.  The store methods run more heads (G > 8) as groups
+# of at most 8 over the same store, one launch each.
+G_CALL = 8
+
+
+def _head_groups(G):
+    return [(g0, min(g0 + G_CALL, G)) for g0 in range(0, G, G_CALL)]
+
+
 class PlaneStore:
     """K [BH, n, D] (any float dtype, on the GPU) -> superblock-ordered bit-plane
     store on the same device (kernels/bitplane.py:310-340).
@@ -297,6 +307,12 @@ class PlaneStore:
         out = torch.empty(BH, G, self.n, device=q.device, dtype=torch.float32) if out is None else out
         if out.dtype != torch.float32 or not out.is_contiguous() or tuple(out.shape) != (BH, G, self.n):
             raise ValueError(f"out must be a contiguous float32 [{BH}, {G}, {self.n}] tensor")
+        if G > G_CALL:
+            for g0, g1 in _head_groups(G):
+                part = out[:, g0:g1].contiguous()
+                PlaneStore.scan(self, q[:, g0:g1], plan, out=part, blocks=blocks)
+                out[:, g0:g1].copy_(part)
+            return out
         nb = math.ceil(self.n / BLK)
         b0, b1 = (0, nb) if blocks is None else (int(blocks[0]), int(blocks[1]))
         sub = int(getattr(self, "sub", SUB))
@@ -317,6 +333,8 @@ class PlaneStore:
             raise AssertionError(f"q has BH={BH}, store has {self.BH}")
         if plan["cls"].shape[1] > 4:
             raise ValueError("the store holds 4 planes: plan with bmax <= 4")
+        if G > G_CALL:
+            return torch.cat([PlaneStore.scan_topk(self, q[:, g0:g1], plan, k, sink, local, m) for g0, g1 in _head_groups(G)], 1)
         n = self.n
         m = n if m is None else int(m)
         sub = int(getattr(self, "sub", SUB))
@@ -371,6 +389,10 @@ class PlaneStore:
                 raise ValueError(f"plan_scan_topk_attention: {name} must be contiguous bf16 [BH, cap, {d}]")
         if Ksrc.shape != Vsrc.shape:
             raise ValueError("plan_scan_topk_attention: Ksrc and Vsrc shapes differ")
+        if G > G_CALL:
+            parts = [PlaneStore.plan_scan_topk_attention(self, q[:, g0:g1], g, budget, k, Ksrc, Vsrc, sink, local, m,
+                                                         bmax, iters, scale) for g0, g1 in _head_groups(G)]
+            return torch.cat([r[0] for r in parts], 1), torch.cat([r[1] for r in parts], 1)
         qc, gf, bptr, bval, units_max = self._plan_call_args(q, g, budget, bmax)
         n = self.n
         m = n if m is None else int(m)
@@ -395,8 +417,13 @@ class PlaneStore:
         scan's prologue, so no plan launch precedes it (the decode chain of
         scripts/B_kernel_bench.py:74).  return_t=True also returns the plan's
         depths t [BH, D] int8."""
-        qc, gf, bptr, bval, units_max = self._plan_call_args(q, g, budget, bmax)
         BH, G, d = q.shape
+        if G > G_CALL:
+            parts = [PlaneStore.plan_scan_topk(self, q[:, g0:g1], g, budget, k, sink, local, m, bmax, iters, True)
+                     for g0, g1 in _head_groups(G)]
+            idx = torch.cat([r[0] for r in parts], 1)
+            return (idx, parts[0][1]) if return_t else idx
+        qc, gf, bptr, bval, units_max = self._plan_call_args(q, g, budget, bmax)
         n = self.n
         m = n if m is None else int(m)
         sub = int(getattr(self, "sub", SUB))
@@ -480,6 +507,12 @@ class Chan4Store:
         out = torch.empty(BH, G, self.n, device=q.device, dtype=torch.float32) if out is None else out
         if out.dtype != torch.float32 or not out.is_contiguous() or tuple(out.shape) != (BH, G, self.n):
             raise ValueError(f"out must be a contiguous float32 [{BH}, {G}, {self.n}] tensor")
+        if G > G_CALL:
+            for g0, g1 in _head_groups(G):
+                part = out[:, g0:g1].contiguous()
+                Chan4Store.scan(self, q[:, g0:g1], act, nact, out=part, blocks=blocks)
+                out[:, g0:g1].copy_(part)
+            return out
         nb = math.ceil(self.n / BLK)
         b0, b1 = (0, nb) if blocks is None else (int(blocks[0]), int(blocks[1]))
         qc = q.contiguous().float()

@@ -177,6 +177,38 @@ def test_scan_matches_oracle(cfg, n, BH, sub):
     _scores_close(scores, ref)
 
 
+@pytest.mark.parametrize("G,n,k", [(12, 9000, 512), (16, 40000, 300)])
+def test_store_methods_more_than_8_query_heads(G, n, k):
+    """G > 8 query heads per KV head (the scan kernels take 8 per launch; the
+    store methods run groups of at most 8): scores within tolerance of the
+    float64 oracle, and scan_topk, plan_scan_topk and plan_scan_topk_attention
+    equal the oracle's top-k of those scores and gather_attention over it."""
+    print(f"[G>8] G={G} n={n} k={k}", flush=True)
+    x = W.config_inputs(2, seed=3, n=n, BH=2)
+    K = x["K"]
+    gen = torch.Generator().manual_seed(G)
+    q = torch.randn(2, G, 128, generator=gen)
+    g = x["g"].to(DEV)
+    st = bp.PlaneStore(K.to(DEV))
+    plan = bp.make_plan(g, 48.0)
+    qd = q.to(DEV)
+    sc = st.scan(qd, plan)
+    code_r, sc_r = O.quantise_u4(K.float().numpy())
+    _scores_close(sc.cpu().numpy(), O.scan_planes(q.numpy(), code_r, sc_r.astype(np.float16).astype(np.float32),
+                                                   plan["t"].cpu().numpy()))
+    ref = O.sink_local_topk(sc.cpu().numpy(), k, 4, 32)
+    np.testing.assert_array_equal(st.scan_topk(qd, plan, k).cpu().numpy(), ref)
+    got, t = st.plan_scan_topk(qd, g, 48.0, k, return_t=True)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+    assert torch.equal(t, plan["t"])
+    Kb = K.to(torch.bfloat16).to(DEV).contiguous()
+    Vb = torch.randn(K.shape, generator=gen).to(torch.bfloat16).to(DEV)
+    idx, out = st.plan_scan_topk_attention(qd, g, 48.0, k, Kb, Vb)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref)
+    ref_out, _ = off.gather_attention(qd, idx, n, Kb, Vb, n)
+    _attn_close(out.cpu().numpy(), ref_out.cpu().numpy())  # launch shapes differ per head group
+
+
 @pytest.mark.parametrize("budget,umax", [(16.0, None), (24.0, None), (40.0, None), (48.0, None), (48.0, 64),
                                          (48.0, 16), (64.0, None), (80.0, None), (90.0, None), (90.0, 200),
                                          (100.0, None), (100.0, 64)])
