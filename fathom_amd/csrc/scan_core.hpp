@@ -236,12 +236,14 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
   }
   // the prologue's global loads are issued together: the class lists (every
   // in-range entry of the bmax x D table) and the queries; or wave 0 plans the
-  // row while the others load the queries
+  // row while the other waves load the queries
   {
     static_assert(kMaxD == 2 * kWave, "two channels per lane");
+    static_assert(kThreads >= 2 * kWave, "a wave besides the planning one");
     const int nthr = (int)blockDim.x;
-    const int w = tid >> 6, l = tid & 63, nw = nthr >> 6;
+    const int w = tid >> 6, l = tid & 63;
     if (own && w == 0) plan_row(sh, a, bh, l);
+    const int qw = own ? w - 1 : w, nw = own ? (nthr >> 6) - 1 : nthr >> 6;  // query waves: all but the planner
     for (int i0 = tid; !own && i0 < 4 * kMaxD; i0 += 2 * nthr) {
       int jr[2];
 #pragma unroll
@@ -256,8 +258,8 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
           sh.schan[(c == 0 ? 0 : SF[c - 1]) + e] = (uint16_t)min(max(jr[u2], 0), a.D - 1);
       }
     }
-    // a wave per head (heads w, w + nw, ...): its largest |q| gives sigma_h
-    for (int h0 = w; h0 < kMaxG; h0 += 2 * nw) {
+    // a wave per head (heads qw, qw + nw, ...): its largest |q| gives sigma_h
+    for (int h0 = qw; qw >= 0 && h0 < kMaxG; h0 += 2 * nw) {
       float qv[2][2];
 #pragma unroll
       for (int u2 = 0; u2 < 2; ++u2) {
@@ -299,34 +301,42 @@ __device__ __forceinline__ int plan_tables(Shared &sh, const ScanArgs &a, int64_
     sh.ureal = ureal;
   }
   __syncthreads();
-  // the A rows: one (unit, head) pair per thread, 64 units of a head at a time
-  // (consecutive threads, consecutive units of one row: no bank conflicts)
-  for (int base = 0; base < ureal; base += 64) {
-    for (int it = tid; it < 64 * kMaxG; it += (int)blockDim.x) {
-      const int v = base + (it & 63), h = it >> 6;
-      if (v >= ureal) continue;
-      const int c = (v >= UE[0]) + (v >= UE[1]) + (v >= UE[2]);  // the unit's class: c + 1 planes
+  // the A rows: a unit per thread (consecutive threads, consecutive units of
+  // every row: no bank conflicts), its channel read once, then the heads;
+  // zero rows past G and zero-weight, zero-scale padding units past ureal
+  // (they read plane word 0 of the superblock)
+  const int G = a.G;
+  for (int v = tid; v < UP; v += (int)blockDim.x) {
+    int c = 0, p = 0, j = 0;
+    if (v < ureal) {
+      c = (v >= UE[0]) + (v >= UE[1]) + (v >= UE[2]);  // the unit's class: c + 1 planes
       const int r = v - (c == 0 ? 0 : UE[c - 1]);
       const int q = c == 0 ? r : c == 1 ? r >> 1 : c == 3 ? r >> 2 : (int)(((uint32_t)r * 0xAAABu) >> 17);  // r / (c + 1)
-      const int p = r - q * (c + 1);
-      const int j = sh.schan[(c == 0 ? 0 : SF[c - 1]) + q];
-      const bool on = h < a.G;
+      p = r - q * (c + 1);
+      j = sh.schan[(c == 0 ? 0 : SF[c - 1]) + q];
+    }
+    const float cf = ldexpf(1.0f, -(c + 1)) - 1.0f;
+#pragma unroll
+    for (int h = 0; h < kMaxG; ++h) {
+      if (h >= G) {  // uniform: a zero row (-0 C weights where a real unit starts a channel, as 0 * (2^-(c+1) - 1))
+        const _Float16 z = (_Float16)0.0f, cz = p == 0 && v < ureal ? (_Float16)-0.0f : z;
+        sh.qa[2 * h][v] = sh.qa[2 * h + 1][v] = z;
+        sh.ca[2 * h][v] = cz;
+        sh.ca[2 * h + 1][v] = z;
+        continue;
+      }
+      const bool on = v < ureal;
       const float qv = on ? sh.qs[h][j] : 0.0f;
       const int sg = on ? sh.sig[h] : 0;
       const float Q = ldexpf(qv, -(p + sg));
       const _Float16 qh = f16_rtz(Q);
       sh.qa[2 * h][v] = qh;
       sh.qa[2 * h + 1][v] = f16_rtz(Q - (float)qh);
-      const float cq = p == 0 ? ldexpf(qv * (ldexpf(1.0f, -(c + 1)) - 1.0f), -sg) : 0.0f;
+      const float cq = p == 0 && on ? ldexpf(qv * cf, -sg) : 0.0f;  // padding: +0
       const _Float16 ch = f16_rtz(cq);
       sh.ca[2 * h][v] = ch;
       sh.ca[2 * h + 1][v] = f16_rtz(cq - (float)ch);
     }
-  }
-  // zero-weight, zero-scale padding units (they read plane word 0 of the superblock)
-  for (int v = ureal + tid; v < UP; v += (int)blockDim.x) {
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) sh.qa[r][v] = sh.ca[r][v] = (_Float16)0.0f;
   }
   __syncthreads();  // the queries are read: the offsets take their place
   const uint32_t sub = (uint32_t)a.sub;
