@@ -143,6 +143,26 @@ def test_make_plan_scalar_budget_and_iters():
                 assert torch.equal(got[key], tens[key])
 
 
+def test_make_plan_boundary_gains_and_long_bisections():
+    """Gains on exact depth boundaries (powers of two: log2 g an integer, so
+    lg - mid hits the rounding ties of the depth at dyadic mids; channels tied
+    in groups) and bisection counts past the kernel's line-count checkpoints
+    (steps 15, 18, 21, ...): the oracle's plan bit for bit."""
+    rng = np.random.default_rng(21)
+    BH, d = 16, 128
+    g = (np.float32(2.0) ** rng.integers(-12, 12, (BH, d))).astype(np.float32)
+    g[2] = np.exp(rng.standard_normal(d) * 4).astype(np.float32)
+    g[3, :64] = np.float32(8.0)
+    gd = torch.from_numpy(g).to(DEV)
+    for bmax in (4, 2, 3):
+        for it in (16, 17, 18, 19, 31, 40, 60):
+            budget = (rng.integers(0, d * bmax, BH) + 0.5 * (it % 2)).astype(np.float32)
+            ref = O.make_plan(g, budget, bmax=bmax, iters=it)
+            got = bp.make_plan(gd, torch.from_numpy(budget).to(DEV), bmax=bmax, iters=it)
+            for key in ("t", "pairs", "npairs", "act", "nact", "cls", "clsn"):
+                np.testing.assert_array_equal(got[key].cpu().numpy(), ref[key], err_msg=f"{key} bmax={bmax} iters={it}")
+
+
 def test_make_plan_worked_example():
     K = np.array([[1.8, 0.4, -0.2, 0.05], [-1.1, 0.9, 0.3, -0.02], [0.3, -1.2, 0.1, 0.04],
                   [1.2, 0.7, 0.4, 0.01], [-0.6, -0.3, -0.5, 0.03], [0.9, 1.1, -0.3, -0.05]], np.float32)
