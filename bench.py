@@ -447,6 +447,28 @@ def run_config4(torch, bp, W, dev):
             "runs": res}
 
 
+def run_wide_topk(torch, bp, store, x, plan, k=4096):
+    """The fused call with k - sink - local above 2048 (the reference's
+    torch.topk has no limit on k): the scores mode, then the wide selection
+    (64-bit radix select over each score row, bitonic sort of the selected),
+    timed as a HIP graph, beside the standalone sink_local_topk of the same
+    scores.  The fused indices must equal sink_local_topk of the scan's scores."""
+    q, sink, local = x["q"], x["sink"], x["local"]
+    scores = store.scan(q, plan)
+    ref = bp.sink_local_topk(scores, k, sink, local)
+    idx = store.scan_topk(q, plan, k, sink, local)
+    torch.cuda.synchronize()
+    if not bool(torch.equal(idx, ref)):
+        raise RuntimeError("wide fused scan+top-k disagrees with sink_local_topk of the scores")
+    ms = _graph_ms(torch, lambda: store.scan_topk(q, plan, k, sink, local), reps=10)
+    ms_sel = _graph_ms(torch, lambda: bp.sink_local_topk(scores, k, sink, local), reps=10)
+    del scores
+    torch.cuda.empty_cache()
+    return {"k": k, "kk": k - sink - local, "rows": int(q.shape[0] * q.shape[1]), "n": int(store.n),
+            "scan_topk_ms": ms, "sink_local_topk_ms": ms_sel, "equal_to_topk_of_scores": True,
+            "timing": "HIP graph of 10 launches, 10 replays after 30 ms of warm-up replays"}
+
+
 def run_stages(torch, bp, store, x, plan, ref_idx):
     """GPU time of each stage of the fused call (sample, select, candidates,
     finalize), each repeated over the state of one full call on one workspace
@@ -796,6 +818,11 @@ def main():
 
     calib_copy(torch, dev, a.calib_copy_mib)
 
+    wide = None
+    if not a.no_decode and not a.stages_only and a.n is None:
+        wide = run_wide_topk(torch, bp, store, x, hbm["plan"])
+        log(f"[bench] wide top-k (C3, k = 4096): {json.dumps(wide)}")
+
     ktab = None
     if not a.no_decode and not a.stages_only and a.n is None:
         ktab = run_kernel_table(torch, bp, W, dev)
@@ -861,6 +888,7 @@ def main():
         "decode_step": decode,
         "kernel_table": ktab,
         "config4": cfg4,
+        "wide_topk": wide,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
