@@ -1,8 +1,8 @@
 """fathom_scan_topk_noalloc (the fused scan + top-k on the library's static
 scratch array) against fathom_scan_topk on a caller workspace: the same index
 sets, bit for bit, on consecutive calls whose shapes shrink (the array keeps
-the previous call's state), on both the candidate-chain and the row-select
-paths; shapes past the array are refused before any launch; the calls after
+the previous call's state), on the candidate-chain, row-select and wide
+(k - sink - local above 2048) paths; shapes past the array are refused before any launch; the calls after
 the first change no device memory."""
 import ctypes
 
@@ -40,8 +40,10 @@ def _noalloc(st, plan, q, k, sink, local, m, idx):
 
 def test_noalloc_equals_workspace_entry_on_shrinking_calls():
     # (BH, G, n, k, sink, local, m): the chain path twice, the second call
-    # smaller, then the row-select path (n <= 32768) on the same array
-    cases = [(2, 4, 200_000, 512, 4, 32, None), (1, 3, 70_001, 256, 4, 64, 70_010), (2, 7, 20_000, 300, 4, 32, None)]
+    # smaller, then the row-select path (n <= 32768), then k - sink - local
+    # above 2048 (the scores and the wide selection) on the same array
+    cases = [(2, 4, 200_000, 512, 4, 32, None), (1, 3, 70_001, 256, 4, 64, 70_010), (2, 7, 20_000, 300, 4, 32, None),
+             (1, 4, 12_000, 3000, 4, 32, None)]
     prepared = []
     for i, (BH, G, n, k, sink, local, m) in enumerate(cases):
         print(f"[noalloc] prepare BH={BH} G={G} n={n} k={k}", flush=True)
