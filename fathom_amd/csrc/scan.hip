@@ -207,7 +207,7 @@ namespace fathom {
 // per (batch, KV head)).  kk above kSelMaxK: the scores and the wide path's
 // selection state.
 size_t scan_topk_ws(int64_t rows, int64_t n, int64_t k, int64_t kk) {
-  if (kk > kSelMaxK) return ws_align((size_t)rows * (size_t)n * 4) + wide_select_bytes(rows, kk);
+  if (kk > kSelMaxK) return ws_align((size_t)rows * (size_t)n * 4) + wide_topk_bytes(rows, n, k);
   if (n <= kRowSelectMax) return ws_align((size_t)rows * (size_t)n * 4) + ws_align((size_t)rows * cdiv(n, kGroupTok) * 4);
   return topk_layout(rows, n, k, true, nullptr, nullptr, nullptr, nullptr, nullptr) +
          ws_align((size_t)rows * sizeof(sc::PlanTab));
@@ -248,7 +248,8 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
   const int64_t um = units_bound(units_max, D, bmax);
   if (kk > kSelMaxK) {
     // kk beyond the LDS-resident selections: the scores in the workspace (the
-    // candidate stage), then the wide path's selection (the finalize stage)
+    // candidate stage), then the score-row chain and the wide selection over
+    // its candidate lists (the finalize stage)
     Emit es{};
     es.out = static_cast<float *>(workspace);
     const size_t sb = ws_align((size_t)rows * (size_t)n * 4);
@@ -257,8 +258,8 @@ int scan_topk_run(const float *q, int64_t BH, int64_t G, int64_t D, const int32_
       if (rc) return rc;
     }
     return (stages & FATHOM_STAGE_FINALIZE)
-               ? wide_select_run(es.out, rows, n, m, k, sink, local, idx, static_cast<char *>(workspace) + sb,
-                                 workspace_bytes - sb, st)
+               ? wide_topk_run(es.out, rows, n, m, k, sink, local, idx, static_cast<char *>(workspace) + sb,
+                               workspace_bytes - sb, st)
                : FATHOM_OK;
   }
   if (n <= kRowSelectMax) {

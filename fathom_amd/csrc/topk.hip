@@ -1485,6 +1485,40 @@ int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t 
   return launch_status("fixed_only_kernel");
 }
 
+size_t wide_topk_bytes(int64_t rows, int64_t n, int64_t k) {
+  return topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr) +
+         wide_select_bytes(rows, k < n ? k : n);
+}
+
+int wide_topk_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+                  int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st) {
+  const int64_t kk = k - sink - local;
+  const size_t chain = topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
+  const size_t need = chain + wide_select_bytes(rows, kk);
+  if (!workspace || workspace_bytes < need)
+    return fail(FATHOM_ERR_WORKSPACE, "top-k (kk=%lld): workspace %zu bytes, need %zu", (long long)kk, workspace_bytes,
+                need);
+  TopkSel s;
+  uint32_t *samp = nullptr;
+  int64_t samp_cap = 0, S = 1;
+  topk_layout(rows, n, k, false, static_cast<char *>(workspace), &samp, &samp_cap, &s, &S);
+  s.kk = (uint32_t)kk;
+  const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
+  const int64_t r_hi = topk_hi_rank(n, S, kk, kTileTok);
+  int rc = launch_sample_scores(scores, rows, n, S, sink, lstart, samp, samp_cap, st);
+  if (rc) return rc;
+  rc = launch_select_keys(samp, rows, samp_cap, kk, r_hi, s, st);
+  if (rc) return rc;
+  rc = launch_filter_scores(scores, rows, n, sink, lstart, s, false, st);
+  if (rc) return rc;
+  if (r_hi < kk) {  // rows whose first pass found fewer than kk take T_lo
+    rc = launch_filter_scores(scores, rows, n, sink, lstart, s, true, st);
+    if (rc) return rc;
+  }
+  return wide_select_list(s, rows, m, k, sink, local, idx, static_cast<char *>(workspace) + chain,
+                          workspace_bytes - chain, st);
+}
+
 int check_topk_args(int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local, const char *who) {
   if (rows < 1 || rows > 65535) return fail(FATHOM_ERR_INVALID, "%s: rows=%lld outside [1, 65535]", who, (long long)rows);
   if (n < 1 || n > 0x7FFFFFFFLL) return fail(FATHOM_ERR_INVALID, "%s: n=%lld unsupported", who, (long long)n);
@@ -1504,13 +1538,11 @@ using namespace fathom;
 
 namespace fathom {
 namespace {
-// k bounds kk = k - sink - local from above: the chain's layout where kk may
-// exceed kSelMaxK covers the wide path's too.
+// k bounds kk = k - sink - local from above: where kk may exceed kSelMaxK the
+// chain's layout is followed by the wide selection's state.
 size_t topk_ws(int64_t rows, int64_t n, int64_t k) {
-  const size_t chain = topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
-  if (k <= kSelMaxK) return chain;
-  const size_t wide = wide_select_bytes(rows, k < n ? k : n);
-  return chain > wide ? chain : wide;
+  return k <= kSelMaxK ? topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr)
+                       : wide_topk_bytes(rows, n, k);
 }
 }  // namespace
 }  // namespace fathom
@@ -1529,7 +1561,7 @@ extern "C" int fathom_sink_local_topk(const float *scores, int64_t rows, int64_t
   hipStream_t st = (hipStream_t)stream;
   const int64_t kk = k - sink - local;
   if (kk == 0) return launch_fixed_only(rows, m, k, sink, local, idx, st);
-  if (kk > kSelMaxK) return wide_select_run(scores, rows, n, m, k, sink, local, idx, workspace, workspace_bytes, st);
+  if (kk > kSelMaxK) return wide_topk_run(scores, rows, n, m, k, sink, local, idx, workspace, workspace_bytes, st);
   const size_t need = topk_layout(rows, n, k, false, nullptr, nullptr, nullptr, nullptr, nullptr);
   if (!workspace || workspace_bytes < need)
     return fail(FATHOM_ERR_WORKSPACE, "sink_local_topk: workspace %zu bytes, need %zu", workspace_bytes, need);

@@ -163,6 +163,15 @@ constexpr int64_t kSelMaxK = 2048;
 size_t wide_select_bytes(int64_t rows, int64_t kk);
 int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
                     int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st);
+// The same over the candidate lists (list layout) of the chain's filter passes.
+int wide_select_list(const TopkSel &s, int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx,
+                     void *workspace, size_t workspace_bytes, hipStream_t st);
+// Top-k of score rows with kk above kSelMaxK: sample -> select -> filter (and
+// the fallback pass), then the wide selection over each row's candidate list;
+// workspace of wide_topk_bytes(rows, n, k) (k bounds kk from above).
+size_t wide_topk_bytes(int64_t rows, int64_t n, int64_t k);
+int wide_topk_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+                  int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st);
 // Shape checks shared by the top-k entry points (FATHOM_OK or an error status).
 int check_topk_args(int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local, const char *who);
 

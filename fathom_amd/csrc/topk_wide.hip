@@ -1,6 +1,8 @@
 // Top-kk of score rows for any kk up to n: the path of k - sink - local above
 // the LDS-resident selections' limit (torch.topk has no limit,
-// kernels/bitplane.py:372-378).
+// kernels/bitplane.py:372-378).  It runs over a row's candidate list from the
+// sample -> select -> filter chain (which holds the row's top kk; about 2.5 kk
+// values for spread scores) or over the whole score row.
 //
 // Every element of a row is the 64-bit value K64 = key << 32 | (2^32 - 1 - i)
 // (distinct within a row; unsigned order = score descending, index ascending).
@@ -53,6 +55,27 @@ __device__ __forceinline__ uint64_t wide_k64(const float *row, int64_t i, int64_
   return k64_of(key, i);
 }
 
+// The values a row's selection runs over: its masked scores, or the K64
+// candidates of the sample -> select -> filter chain (list layout: the first
+// pass's if it found kk, else the fallback pass's), which hold the row's top kk.
+struct WideSrc {
+  const float *scores;  // [rows, n] (null: candidate lists)
+  int64_t n, sink, lstart;
+  const uint64_t *cand;  // [rows, cand_cap]
+  int64_t cand_cap;
+  const uint32_t *cnt1, *cnt2;  // per row, kCntStride apart
+  uint32_t kk;
+  __device__ __forceinline__ int64_t count(int64_t row) const {
+    if (!cand) return n;
+    const uint32_t c1 = cnt1[row * kCntStride];
+    const int64_t c = c1 >= kk ? c1 : cnt2[row * kCntStride];
+    return c < cand_cap ? c : cand_cap;
+  }
+  __device__ __forceinline__ uint64_t at(int64_t row, int64_t i) const {
+    return cand ? cand[row * cand_cap + i] : wide_k64(scores + row * n, i, sink, lstart);
+  }
+};
+
 __global__ __launch_bounds__(kWideThreads) void wide_init_kernel(WideState w, uint32_t kk) {
   const int64_t row = blockIdx.x;
   for (int b = threadIdx.x; b < kWideBins; b += kWideThreads) w.hist[row * kWideBins + b] = 0u;
@@ -65,11 +88,12 @@ __global__ __launch_bounds__(kWideThreads) void wide_init_kernel(WideState w, ui
 }
 
 // Digit counts of the elements of one chunk of a row that match the fixed bits.
-__global__ __launch_bounds__(kWideThreads) void wide_hist_kernel(const float *__restrict__ scores, int64_t n,
-                                                                 int64_t sink, int64_t lstart, WideState w, int shift,
-                                                                 int width) {
+__global__ __launch_bounds__(kWideThreads) void wide_hist_kernel(WideSrc src, WideState w, int shift, int width) {
   const int64_t row = blockIdx.y;
-  if (w.done[row]) return;  // uniform
+  const int64_t n = src.count(row);
+  const int64_t per = cdiv(n, (int64_t)gridDim.x);  // the row's values spread over the grid's workgroups
+  const int64_t start = (int64_t)blockIdx.x * per;
+  if (w.done[row] || start >= n) return;  // uniform
   __shared__ uint32_t h[kWideBins];
   const int tid = threadIdx.x;
   for (int b = tid; b < kWideBins; b += kWideThreads) h[b] = 0u;
@@ -77,12 +101,23 @@ __global__ __launch_bounds__(kWideThreads) void wide_hist_kernel(const float *__
   const int top = shift + width;  // bits [top, 64) are fixed
   const uint64_t fixed = top < 64 ? (w.thr[row] >> top) : 0ull;
   const uint32_t dmask = (1u << width) - 1u;
-  const float *rs = scores + row * n;
-  const int64_t start = (int64_t)blockIdx.x * kWideChunk;
-  const int64_t end = start + kWideChunk < n ? start + kWideChunk : n;
-  for (int64_t i = start + tid; i < end; i += kWideThreads) {
-    const uint64_t v = wide_k64(rs, i, sink, lstart);
-    if (top >= 64 || (v >> top) == fixed) atomicAdd(&h[(uint32_t)(v >> shift) & dmask], 1u);
+  const int64_t end = start + per < n ? start + per : n;
+  const int lane = tid & (kWave - 1), wave = tid >> 6;
+  for (int64_t i0 = start + wave * kWave; i0 < end; i0 += kWideThreads) {  // wave-uniform trip count
+    const int64_t i = i0 + lane;
+    const uint64_t v = i < end ? src.at(row, i) : 0ull;
+    const bool on = i < end && (top >= 64 || (v >> top) == fixed);
+    const uint32_t dg = (uint32_t)(v >> shift) & dmask;
+    // the lanes sharing the first counted lane's digit add with one atomic
+    // (a row's values crowd into few bins), the others one by one
+    const uint64_t mm = __ballot(on);
+    if (mm == 0ull) continue;
+    const int first = __ffsll((long long)mm) - 1;
+    const uint32_t df = (uint32_t)__shfl((int)dg, first);
+    const bool same = on && dg == df;
+    const uint64_t ms = __ballot(same);
+    if (lane == first) atomicAdd(&h[df], (uint32_t)__popcll(ms));
+    if (on && !same) atomicAdd(&h[dg], 1u);
   }
   __syncthreads();
   uint32_t *gh = w.hist + row * kWideBins;
@@ -144,29 +179,44 @@ __global__ __launch_bounds__(kWideThreads) void wide_pick_kernel(WideState w, in
   }
 }
 
-// The kk values >= the threshold, appended at the row's counter.
-__global__ __launch_bounds__(kWideThreads) void wide_compact_kernel(const float *__restrict__ scores, int64_t n,
-                                                                    int64_t sink, int64_t lstart, WideState w,
-                                                                    uint32_t kk) {
+// The kk values >= the threshold, appended at the row's counter: each wave
+// counts its elements of the chunk, the workgroup reserves its range with one
+// atomic, then each wave writes at its own running offset (no atomics).
+__global__ __launch_bounds__(kWideThreads) void wide_compact_kernel(WideSrc src, WideState w, uint32_t kk) {
+  constexpr int kW = kWideThreads / kWave;
+  __shared__ uint32_t s_wc[kW];
+  __shared__ uint32_t s_base;
   const int64_t row = blockIdx.y;
-  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t n = src.count(row);
+  const int64_t per = cdiv(n, (int64_t)gridDim.x);
+  const int64_t start = (int64_t)blockIdx.x * per;
+  if (start >= n) return;  // uniform
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const uint64_t thr = w.thr[row];
-  const float *rs = scores + row * n;
+  const int64_t end = start + per < n ? start + per : n;
+  uint32_t c = 0u;
+  for (int64_t i = start + threadIdx.x; i < end; i += kWideThreads) c += src.at(row, i) >= thr ? 1u : 0u;
+  c = (uint32_t)wave_sum_i((int)c);
+  if (lane == 0) s_wc[wave] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0u;
+#pragma unroll
+    for (int v = 0; v < kW; ++v) t += s_wc[v];
+    s_base = t ? atomicAdd(w.cnt + row * kCntStride, t) : 0u;
+  }
+  __syncthreads();
+  uint32_t off = s_base;
+  for (int v = 0; v < wave; ++v) off += s_wc[v];
   uint64_t *sel = w.sel + row * w.P;
-  uint32_t *cnt = w.cnt + row * kCntStride;
-  const int64_t start = (int64_t)blockIdx.x * kWideChunk;
-  const int64_t end = start + kWideChunk < n ? start + kWideChunk : n;
-  for (int64_t i0 = start; i0 < end; i0 += kWideThreads) {  // uniform trip count
-    const int64_t i = i0 + threadIdx.x;
-    const uint64_t v = i < end ? wide_k64(rs, i, sink, lstart) : 0ull;
+  for (int64_t i0 = start + wave * kWave; i0 < end; i0 += kWideThreads) {  // wave-uniform trip count
+    const int64_t i = i0 + lane;
+    const uint64_t v = i < end ? src.at(row, i) : 0ull;
     const bool take = i < end && v >= thr;
     const uint64_t mask = __ballot(take);
-    if (mask == 0ull) continue;
-    uint32_t base = 0u;
-    if (lane == 0) base = atomicAdd(cnt, (uint32_t)__popcll(mask));
-    base = __shfl(base, 0);
-    const uint32_t pos = base + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
+    const uint32_t pos = off + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
     if (take && pos < kk) sel[pos] = v;
+    off += (uint32_t)__popcll(mask);
   }
 }
 
@@ -256,7 +306,10 @@ size_t wide_select_bytes(int64_t rows, int64_t kk) {
          ws_align((size_t)rows * kWideBins * 4) + ws_align((size_t)rows * (size_t)P * 8);
 }
 
-int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+namespace {
+// The selection over src (span: an upper bound of every row's count, for the
+// grids of the passes over the values).
+int wide_select_src(const WideSrc &src, int64_t span, int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local,
                     int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st) {
   const int64_t kk = k - sink - local;
   const size_t need = wide_select_bytes(rows, kk);
@@ -277,20 +330,21 @@ int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int
   w.hist = reinterpret_cast<uint32_t *>(p);
   p += ws_align((size_t)rows * kWideBins * 4);
   w.sel = reinterpret_cast<uint64_t *>(p);
-  const int64_t lstart = (m - local) > 0 ? (m - local) : 0;
   const uint32_t ukk = (uint32_t)kk;
-  const dim3 pass((unsigned)cdiv(n, kWideChunk), (unsigned)rows);
+  // about kWideChunk values per workgroup of a full row; a row's actual values
+  // (a candidate list's count) are spread evenly over these workgroups
+  const dim3 pass((unsigned)cdiv(span, kWideChunk), (unsigned)rows);
   wide_init_kernel<<<(unsigned)rows, kWideThreads, 0, st>>>(w, ukk);
   int rc = launch_status("wide_init_kernel");
   for (int r = 0; r < kRounds && !rc; ++r) {
-    wide_hist_kernel<<<pass, kWideThreads, 0, st>>>(scores, n, sink, lstart, w, kShift[r], kWidth[r]);
+    wide_hist_kernel<<<pass, kWideThreads, 0, st>>>(src, w, kShift[r], kWidth[r]);
     rc = launch_status("wide_hist_kernel");
     if (rc) break;
     wide_pick_kernel<<<(unsigned)rows, kWideThreads, 0, st>>>(w, kShift[r], r == kRounds - 1);
     rc = launch_status("wide_pick_kernel");
   }
   if (rc) return rc;
-  wide_compact_kernel<<<pass, kWideThreads, 0, st>>>(scores, n, sink, lstart, w, ukk);
+  wide_compact_kernel<<<pass, kWideThreads, 0, st>>>(src, w, ukk);
   rc = launch_status("wide_compact_kernel");
   if (rc) return rc;
   const int64_t L = w.P < kSortLds ? w.P : kSortLds;
@@ -310,6 +364,28 @@ int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int
   if (rc) return rc;
   wide_output_kernel<<<dim3((unsigned)cdiv(k, 256), (unsigned)rows), 256, 0, st>>>(w, m, k, kk, sink, local, idx);
   return launch_status("wide_output_kernel");
+}
+}  // namespace
+
+int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
+                    int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st) {
+  WideSrc src{};
+  src.scores = scores;
+  src.n = n;
+  src.sink = sink;
+  src.lstart = (m - local) > 0 ? (m - local) : 0;
+  return wide_select_src(src, n, rows, m, k, sink, local, idx, workspace, workspace_bytes, st);
+}
+
+int wide_select_list(const TopkSel &s, int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx,
+                     void *workspace, size_t workspace_bytes, hipStream_t st) {
+  WideSrc src{};
+  src.cand = s.cand;
+  src.cand_cap = s.cand_cap;
+  src.cnt1 = s.cand_cnt;
+  src.cnt2 = s.cand2_cnt;
+  src.kk = s.kk;
+  return wide_select_src(src, s.cand_cap, rows, m, k, sink, local, idx, workspace, workspace_bytes, st);
 }
 
 }  // namespace fathom
