@@ -1340,6 +1340,32 @@ __global__ __launch_bounds__(kFinThreads) void rowselect_gmax_kernel(const float
   }
 }
 
+// The wide selection's kk <= 8192 values of a row (sel [rows, P], all
+// distinct) ranked by one counting sort and written as the row's indices, then
+// the sink and local positions.
+template <int E>
+__global__ __launch_bounds__(kFinThreads) void rank_list_kernel(const uint64_t *__restrict__ sel, int64_t P, int64_t kk,
+                                                               int64_t m, int64_t k, int64_t sink, int64_t local,
+                                                               int64_t *__restrict__ idx) {
+  __shared__ uint64_t cl[kCandLds];
+  __shared__ RangeShared sh;
+  static_assert(E * kFinThreads + kBins <= kCandLds, "the sort's scratch");
+  const int64_t row = blockIdx.x;
+  const uint64_t *src = sel + row * P;
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int64_t i = threadIdx.x + e * kFinThreads;
+    v[e] = i < kk ? src[i] : 0ull;
+  }
+  int nlim = kWave;
+  while (nlim < (int)kk) nlim <<= 1;
+  int64_t *out = idx + row * k;
+  bin_rank_desc<E>(v, (int)kk, cl, sh, nlim,
+                   [&](int rank, uint64_t x) { out[rank] = (int64_t)(0xFFFFFFFFu - (uint32_t)x); });
+  write_fixed(out, (int)kk, kk, m, sink, local);
+}
+
 __global__ __launch_bounds__(256) void fixed_only_kernel(int64_t rows, int64_t m, int64_t k, int64_t sink,
                                                          int64_t local, int64_t *__restrict__ idx) {
   const int64_t total = rows * k;
@@ -1477,6 +1503,16 @@ int launch_rowselect_gmax_attn(const float *scores, const uint32_t *gmax, int64_
              out};
   rowselect_gmax_kernel<true><<<(unsigned)rows, kFinThreads, 0, st>>>(scores, gmax, n, m, k, sink, local, idx, ra);
   return launch_status("rowselect_gmax_kernel");
+}
+
+int launch_rank_list(const uint64_t *sel, int64_t P, int64_t rows, int64_t kk, int64_t m, int64_t k, int64_t sink,
+                     int64_t local, int64_t *idx, hipStream_t st) {
+  if (kk > kRankListMax) return fail(FATHOM_ERR_INVALID, "rank_list: kk=%lld exceeds %lld", (long long)kk, (long long)kRankListMax);
+  if (kk <= 4 * kFinThreads)
+    rank_list_kernel<4><<<(unsigned)rows, kFinThreads, 0, st>>>(sel, P, kk, m, k, sink, local, idx);
+  else
+    rank_list_kernel<8><<<(unsigned)rows, kFinThreads, 0, st>>>(sel, P, kk, m, k, sink, local, idx);
+  return launch_status("rank_list_kernel");
 }
 
 int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx, hipStream_t st) {

@@ -163,6 +163,11 @@ constexpr int64_t kSelMaxK = 2048;
 size_t wide_select_bytes(int64_t rows, int64_t kk);
 int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
                     int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st);
+// Ranks of the kk <= kRankListMax distinct values of each row of sel [rows, P]
+// by one counting sort, written as idx [rows, k] (then the fixed positions).
+constexpr int64_t kRankListMax = 8192;
+int launch_rank_list(const uint64_t *sel, int64_t P, int64_t rows, int64_t kk, int64_t m, int64_t k, int64_t sink,
+                     int64_t local, int64_t *idx, hipStream_t st);
 // The same over the candidate lists (list layout) of the chain's filter passes.
 int wide_select_list(const TopkSel &s, int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx,
                      void *workspace, size_t workspace_bytes, hipStream_t st);

@@ -16,10 +16,12 @@
 //                 scores the key's three rounds usually suffice;
 //   compaction    the kk elements with K64 >= the threshold, appended at a row
 //                 counter (one atomic per wave);
-//   sort          bitonic, descending, over the kk values padded with zeros to
-//                 a power of two P: chunks of up to 16384 values sorted in LDS,
-//                 then for each merge size above that the steps of strides of
-//                 at least a chunk in global memory and the rest in LDS;
+//   sort          up to 8192 values: one counting sort per row (the LDS-resident
+//                 selections' ranking); more: bitonic, descending, over the kk
+//                 values padded with zeros to a power of two P: chunks of up to
+//                 16384 values sorted in LDS, then for each merge size above
+//                 that the steps of strides of at least a chunk in global
+//                 memory and the rest in LDS;
 //   output        indices of the sorted values, then the sink and local
 //                 positions.
 // Every launch is data-independent in shape, so the whole path can be captured
@@ -347,6 +349,8 @@ int wide_select_src(const WideSrc &src, int64_t span, int64_t rows, int64_t m, i
   wide_compact_kernel<<<pass, kWideThreads, 0, st>>>(src, w, ukk);
   rc = launch_status("wide_compact_kernel");
   if (rc) return rc;
+  // up to 8192 values: one counting sort per row ranks them and writes the indices
+  if (kk <= kRankListMax) return launch_rank_list(w.sel, w.P, rows, kk, m, k, sink, local, idx, st);
   const int64_t L = w.P < kSortLds ? w.P : kSortLds;
   const dim3 chunks((unsigned)(w.P / L), (unsigned)rows);
   wide_sort_local_kernel<<<chunks, kSortThreads, 0, st>>>(w, L, 0, ukk, 1);
