@@ -9,7 +9,8 @@ scripts/B_e2e_offload_v2.py:184-202):
   quantiser works per 64-token block, so quantising the gathered blocks gives
   the full store's codes and scales);
 * the fused scan + top-k == sink_local_topk(scan) == the oracle's top-k of the
-  same scores;
+  same scores, at k = 512 and at k above the LDS-resident selections (4096,
+  20036);
 * the zero-copy (host-mapped index) and copy-index (staged runs) paths select
   the HBM path's indices;
 * the union-gathered K/V rows == oracle.gather_union.
@@ -83,6 +84,21 @@ def test_c3_fused_topk_equals_unfused_and_oracle(c3):
     torch.testing.assert_close(c3["idx"], unfused, rtol=0, atol=0)
     ref = O.sink_local_topk(c3["scores"].cpu().numpy().reshape(-1, x["n"]), x["k"], x["sink"], x["local"])
     np.testing.assert_array_equal(c3["idx"].cpu().numpy().reshape(-1, x["k"]), ref)
+
+
+@pytest.mark.parametrize("k", [4096, 20036])
+def test_c3_wide_topk_equals_oracle(c3, k):
+    """k - sink - local above 2048 at full size (kk = 4060: the counting-sort
+    ranking; kk = 20000: the bitonic sort with its global merge steps): the
+    fused call == sink_local_topk(scan) == the oracle's top-k of the same
+    scores (torch.topk has no limit on k, kernels/bitplane.py:376)."""
+    print(f"[c3-full] wide top-k k={k}", flush=True)
+    x = c3["x"]
+    got = c3["st"].scan_topk(c3["q"], c3["plan"], k, x["sink"], x["local"])
+    unfused = bp.sink_local_topk(c3["scores"], k, x["sink"], x["local"])
+    assert torch.equal(got, unfused)
+    ref = O.sink_local_topk(c3["scores"].cpu().numpy().reshape(-1, x["n"]), k, x["sink"], x["local"])
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(-1, k), ref)
 
 
 def test_c3_zero_copy_and_copy_index_equal_hbm(c3):
