@@ -273,8 +273,9 @@ int fathom_scan_topk_noalloc(const float *q, int64_t BH, int64_t G, int64_t D, c
  * select the top kk = k - sink - local by (score descending, index ascending;
  * NaN above +inf, -0.0 == +0.0), then append 0..sink-1 and m-local..m-1.
  *   idx [rows, k] int64.  Requires 0 <= kk <= n, sink <= n, local <= m, n <= m
- * (any kk, as torch.topk: kk above 2048 takes an exact 64-bit radix select and
- * a bitonic sort over the score rows).
+ * (any kk, as torch.topk: kk above 2048 takes an exact 64-bit radix select over
+ * the rows' candidate lists, then a counting sort of up to 8192 values or a
+ * bitonic sort).
  * workspace: fathom_topk_workspace_bytes(rows, n, k) bytes of device memory,
  * contents arbitrary on entry.
  */
