@@ -157,18 +157,16 @@ int launch_fixed_only(int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t 
 // Largest kk of the LDS-resident selections (sample -> select -> filter ->
 // finalize, row-select, the fused scan's chains); larger kk take the wide path.
 constexpr int64_t kSelMaxK = 2048;
-// Workspace and run of the wide path: exact top kk of score rows [rows, n] for
-// any kk <= n by a 64-bit radix select and a bitonic sort (any number of
-// launches, all of data-independent shape).
+// State of the wide selection (exact top kk of candidate lists for any kk by a
+// 64-bit radix select, then a counting or bitonic sort; launches of
+// data-independent shape).
 size_t wide_select_bytes(int64_t rows, int64_t kk);
-int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
-                    int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st);
 // Ranks of the kk <= kRankListMax distinct values of each row of sel [rows, P]
 // by one counting sort, written as idx [rows, k] (then the fixed positions).
 constexpr int64_t kRankListMax = 8192;
 int launch_rank_list(const uint64_t *sel, int64_t P, int64_t rows, int64_t kk, int64_t m, int64_t k, int64_t sink,
                      int64_t local, int64_t *idx, hipStream_t st);
-// The same over the candidate lists (list layout) of the chain's filter passes.
+// The wide selection over the candidate lists (list layout) of the chain's filter passes.
 int wide_select_list(const TopkSel &s, int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx,
                      void *workspace, size_t workspace_bytes, hipStream_t st);
 // Top-k of score rows with kk above kSelMaxK: sample -> select -> filter (and

@@ -2,7 +2,7 @@
 // the LDS-resident selections' limit (torch.topk has no limit,
 // kernels/bitplane.py:372-378).  It runs over a row's candidate list from the
 // sample -> select -> filter chain (which holds the row's top kk; about 2.5 kk
-// values for spread scores) or over the whole score row.
+// values for spread scores).
 //
 // Every element of a row is the 64-bit value K64 = key << 32 | (2^32 - 1 - i)
 // (distinct within a row; unsigned order = score descending, index ascending).
@@ -52,30 +52,20 @@ struct WideState {
   int64_t P;
 };
 
-__device__ __forceinline__ uint64_t wide_k64(const float *row, int64_t i, int64_t sink, int64_t lstart) {
-  const uint32_t key = (i < sink || i >= lstart) ? kKeyNegInf : score_key(row[i]);
-  return k64_of(key, i);
-}
-
-// The values a row's selection runs over: its masked scores, or the K64
-// candidates of the sample -> select -> filter chain (list layout: the first
-// pass's if it found kk, else the fallback pass's), which hold the row's top kk.
+// The values a row's selection runs over: the K64 candidates of the sample ->
+// select -> filter chain (list layout: the first pass's if it found kk, else
+// the fallback pass's), which hold the row's top kk.
 struct WideSrc {
-  const float *scores;  // [rows, n] (null: candidate lists)
-  int64_t n, sink, lstart;
   const uint64_t *cand;  // [rows, cand_cap]
   int64_t cand_cap;
   const uint32_t *cnt1, *cnt2;  // per row, kCntStride apart
   uint32_t kk;
   __device__ __forceinline__ int64_t count(int64_t row) const {
-    if (!cand) return n;
     const uint32_t c1 = cnt1[row * kCntStride];
     const int64_t c = c1 >= kk ? c1 : cnt2[row * kCntStride];
     return c < cand_cap ? c : cand_cap;
   }
-  __device__ __forceinline__ uint64_t at(int64_t row, int64_t i) const {
-    return cand ? cand[row * cand_cap + i] : wide_k64(scores + row * n, i, sink, lstart);
-  }
+  __device__ __forceinline__ uint64_t at(int64_t row, int64_t i) const { return cand[row * cand_cap + i]; }
 };
 
 __global__ __launch_bounds__(kWideThreads) void wide_init_kernel(WideState w, uint32_t kk) {
@@ -370,16 +360,6 @@ int wide_select_src(const WideSrc &src, int64_t span, int64_t rows, int64_t m, i
   return launch_status("wide_output_kernel");
 }
 }  // namespace
-
-int wide_select_run(const float *scores, int64_t rows, int64_t n, int64_t m, int64_t k, int64_t sink, int64_t local,
-                    int64_t *idx, void *workspace, size_t workspace_bytes, hipStream_t st) {
-  WideSrc src{};
-  src.scores = scores;
-  src.n = n;
-  src.sink = sink;
-  src.lstart = (m - local) > 0 ? (m - local) : 0;
-  return wide_select_src(src, n, rows, m, k, sink, local, idx, workspace, workspace_bytes, st);
-}
 
 int wide_select_list(const TopkSel &s, int64_t rows, int64_t m, int64_t k, int64_t sink, int64_t local, int64_t *idx,
                      void *workspace, size_t workspace_bytes, hipStream_t st) {
