@@ -1234,11 +1234,12 @@ def _full_depth_plan(act, nact, D=128):
     return {"cls": cls, "clsn": clsn}
 
 
-@pytest.mark.parametrize("G,n,r", [(4, 5000, 32), (7, 3000, 16), (1, 700, 128), (3, 2100, 0)])
+@pytest.mark.parametrize("G,n,r", [(4, 5000, 32), (7, 3000, 16), (1, 700, 128), (3, 2100, 0), (12, 3000, 32)])
 def test_scan_chan4_matches_oracle_and_plane_scan(G, n, r):
     """Chan4 scores against the float64 oracle, and the plane scan of a plan with
     t = 4 on the same channels against the same oracle scores (the two stores hold
-    the same codes; their kernels sum in different orders)."""
+    the same codes; their kernels sum in different orders).  G = 12: both store
+    methods run their heads in groups of at most 8, the block sub-range too."""
     print(f"[scan-chan4] G={G} n={n} r={r}", flush=True)
     BH = 3
     K = _keys(BH, n, dtype=torch.bfloat16, edge=False)
