@@ -13,17 +13,19 @@ namespace fathom {
 namespace {
 
 constexpr int kKltThreads = 256;
-constexpr int kKltMaxG = 8;
+constexpr int kKltMaxG = 32;                     // query heads per (batch, KV head) row
 constexpr int kKltMaxD = 256;
 constexpr int kKltCols = 16;                     // output coordinates per workgroup
 constexpr int kKltParts = kKltThreads / kKltCols;  // d ranges per coordinate
 
+// MAXG: the heads the workgroup holds (8 for GQA groups of up to 8, else 32).
+template <int MAXG>
 __global__ __launch_bounds__(kKltThreads) void klt_query_kernel(const float *__restrict__ q,
                                                                  const float *__restrict__ Vt,
                                                                  const float *__restrict__ lam, int G, int D,
                                                                  float *__restrict__ qr, float *__restrict__ gain) {
-  __shared__ float qs[kKltMaxG][kKltMaxD];
-  __shared__ float part[kKltParts][kKltMaxG][kKltCols];
+  __shared__ float qs[MAXG][kKltMaxD];
+  __shared__ float part[kKltParts][MAXG][kKltCols];
   const int tid = threadIdx.x;
   const int64_t bh = blockIdx.y;
   const int e0 = blockIdx.x * kKltCols;
@@ -32,22 +34,22 @@ __global__ __launch_bounds__(kKltThreads) void klt_query_kernel(const float *__r
   const float *V = Vt + bh * (int64_t)D * D;
   const int c = tid % kKltCols, pt = tid / kKltCols, e = e0 + c;
   const int per = (D + kKltParts - 1) / kKltParts;
-  float acc[kKltMaxG];
+  float acc[MAXG];
 #pragma unroll
-  for (int g = 0; g < kKltMaxG; ++g) acc[g] = 0.0f;
+  for (int g = 0; g < MAXG; ++g) acc[g] = 0.0f;
   if (e < D) {
     for (int i = 0; i < per; ++i) {
       const int d = pt * per + i;
       if (d < D) {
         const float v = V[(int64_t)d * D + e];
 #pragma unroll
-        for (int g = 0; g < kKltMaxG; ++g)
+        for (int g = 0; g < MAXG; ++g)
           if (g < G) acc[g] = fmaf(qs[g][d], v, acc[g]);
       }
     }
   }
 #pragma unroll
-  for (int g = 0; g < kKltMaxG; ++g) part[pt][g][c] = acc[g];
+  for (int g = 0; g < MAXG; ++g) part[pt][g][c] = acc[g];
   __syncthreads();
   if (tid < kKltCols && e0 + tid < D) {
     const int eo = e0 + tid;
@@ -76,6 +78,9 @@ extern "C" int fathom_klt_query(const float *q, const float *Vt, const float *la
   if (D < 1 || D > kKltMaxD) return fail(FATHOM_ERR_INVALID, "klt_query: D=%lld outside [1, %d]", (long long)D, kKltMaxD);
   const dim3 grid((unsigned)cdiv(D, kKltCols), (unsigned)BH);
   if (BH > 65535) return fail(FATHOM_ERR_INVALID, "klt_query: BH=%lld above 65535", (long long)BH);
-  klt_query_kernel<<<grid, kKltThreads, 0, (hipStream_t)stream>>>(q, Vt, lam, (int)G, (int)D, qr, gain);
+  if (G <= 8)
+    klt_query_kernel<8><<<grid, kKltThreads, 0, (hipStream_t)stream>>>(q, Vt, lam, (int)G, (int)D, qr, gain);
+  else
+    klt_query_kernel<kKltMaxG><<<grid, kKltThreads, 0, (hipStream_t)stream>>>(q, Vt, lam, (int)G, (int)D, qr, gain);
   return launch_status("klt_query_kernel");
 }

@@ -159,7 +159,7 @@ int fathom_scan_chan4(const float *q, int64_t BH, int64_t G, int64_t D, const in
  * qr[bh, g] = q[bh, g] @ Vt[bh] and gain[bh, e] = sum_g qr[bh, g, e]^2 * lam[bh, e]
  * (the make_plan gains of the rotated coordinates).  q [BH, G, D], Vt [BH, D, D]
  * row-major (column e = basis vector e), lam [BH, D], qr [BH, G, D], gain [BH, D],
- * all float32; G <= 8, D <= 256.
+ * all float32; G <= 32, D <= 256.
  */
 int fathom_klt_query(const float *q, const float *Vt, const float *lam, int64_t BH, int64_t G, int64_t D, float *qr,
                      float *gain, void *stream);

@@ -1332,6 +1332,27 @@ def test_klt_params_and_query_match_oracle():
     np.testing.assert_allclose(gain.cpu().numpy(), rg, rtol=1e-5, atol=1e-6 * np.abs(rg).max())
 
 
+def test_klt_query_and_scan_more_than_8_heads():
+    """G = 12 query heads: the query kernel's wider instance (up to 32 heads,
+    the gains still summed in head order) and the rotated store's scan in head
+    groups, against the oracle."""
+    from fathom_amd import klt
+    x, Qcal = _klt_case()
+    Kd = x["K"].to(DEV)
+    p = klt.klt_params(Kd, Qcal.to(DEV))
+    st = klt.KLTPlaneStore(Kd, p)
+    q = torch.randn(Kd.shape[0], 12, 128, generator=torch.Generator().manual_seed(12))
+    qr, gain = st.query(q.to(DEV))
+    rq, rg = O.klt_query(q.numpy(), p["Vt"].cpu().numpy(), p["lam"].cpu().numpy())
+    np.testing.assert_allclose(qr.cpu().numpy(), rq, rtol=1e-5, atol=1e-5 * np.abs(rq).max())
+    np.testing.assert_allclose(gain.cpu().numpy(), rg, rtol=1e-5, atol=1e-6 * np.abs(rg).max())
+    plan = st.plan(q.to(DEV), 48.0)
+    Kr = torch.matmul(Kd.float() - p["mu"][:, None, :], p["Vt"]).cpu()
+    code_r, sc_r = O.quantise_u4(Kr.numpy())
+    s = st.scan(q.to(DEV), plan)
+    _scores_close(s.cpu().numpy(), O.scan_planes(qr.cpu().numpy(), code_r, sc_r, plan["t"].cpu().numpy()))
+
+
 @pytest.mark.parametrize("budget", [40.0, 48.0, 80.0])
 def test_klt_store_scan_and_topk(budget):
     """The rotated store: codes of the rotated keys bit-exact, scores within tolerance of
